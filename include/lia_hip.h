@@ -1,0 +1,239 @@
+/*
+ * lia_hip.h - C ABI of the MI355X (gfx950) paged continuous-batching attention path.
+ *
+ * Every entry point takes plain pointers and sizes.  Device pointers are HIP device
+ * addresses; `stream` is a hipStream_t (NULL = the legacy default stream).  All device
+ * entry points are asynchronous on `stream`, perform no allocation and no host
+ * synchronisation (so they may be captured in a hipGraph), validate their arguments
+ * before launching anything, and return LIA_OK (0) or a negative lia_status.
+ *
+ * KV pool layout (identical to the reference engine, src/inference/initialize.rs:22-57):
+ *   two planes per layer, K and V, each [pool_pages * page_size][num_kv_heads][head_dim]
+ *   elements of the KV dtype; physical slot of logical position p of table row s is
+ *   pages[s * stride + p / page_size] * page_size + p % page_size
+ *   (src/gpu/kernels/llama.rs:174-177).  FP8 pools carry one fp32 scale per
+ *   (page, kv head) and plane: k_scales[page * num_kv_heads + head].
+ *
+ * Query / output layout: [rows][num_q_heads][head_dim] (src/gpu/llama_attention.rs:37-41).
+ */
+#ifndef LIA_HIP_H
+#define LIA_HIP_H
+
+#include <stddef.h>
+#include <stdint.h>
+
+#ifdef __cplusplus
+extern "C" {
+#endif
+
+typedef void *lia_stream_t; /* hipStream_t */
+
+/* Status codes.  The packing codes mirror the ensure! checks of Engine::run_paged
+ * (src/inference/paging.rs:120-172) in the order the reference evaluates them. */
+enum lia_status {
+    LIA_OK = 0,
+    LIA_E_ROWS = -1,            /* "invalid packed row count"          paging.rs:120-123 */
+    LIA_E_OUTPUT_COUNT = -2,    /* "invalid output row count"          paging.rs:124-127 */
+    LIA_E_OUTPUT_ROW = -3,      /* "output row outside packed input"   paging.rs:128-131 */
+    LIA_E_TABLES = -4,          /* "too many sequence tables"          paging.rs:132-135 */
+    LIA_E_TABLE_LEN = -5,       /* "sequence table exceeds context"    paging.rs:138 */
+    LIA_E_PAGE_RANGE = -6,      /* "physical page outside KV pool"     paging.rs:139-144 */
+    LIA_E_TOKEN = -7,           /* "invalid packed token"              paging.rs:155 */
+    LIA_E_POSITION = -8,        /* "packed position exceeds context"   paging.rs:156 */
+    LIA_E_MISSING_TABLE = -9,   /* "missing sequence table"            paging.rs:157-159 */
+    LIA_E_MISSING_PAGE = -10,   /* "missing physical KV page"          paging.rs:160-162 */
+    LIA_E_DUPLICATE_SLOT = -11, /* "duplicate physical KV write"       paging.rs:163-166 */
+    LIA_E_NONCONSECUTIVE = -12, /* "packed positions must be consecutive" paging.rs:167-172 */
+    LIA_E_CONFIG = -19,         /* configure_paging limits             paging.rs:39-50 */
+    LIA_E_ARG = -20,            /* invalid extent / geometry   gpu/llama_attention.rs:36-61 */
+    LIA_E_ALIGN = -21,          /* unaligned buffers           gpu/llama_attention.rs:62-68 */
+    LIA_E_WORKSPACE = -22,      /* workspace exhausted         gpu/llama_attention.rs:53-61 */
+    LIA_E_UNSUPPORTED = -23,    /* geometry this build has no kernel for */
+    LIA_E_HIP = -30             /* a HIP runtime call failed */
+};
+
+enum lia_dtype { LIA_F32 = 0, LIA_F16 = 1, LIA_BF16 = 2, LIA_FP8_E4M3 = 3 };
+
+/* PagedRow (src/inference/paging.rs:7-11). */
+typedef struct lia_paged_row {
+    uint32_t token;
+    uint32_t position;
+    uint32_t sequence;
+} lia_paged_row;
+
+/* Query group = one cu_seqlens segment (src/inference/llama_plan.rs:2-6). */
+typedef struct lia_group {
+    uint32_t start;
+    uint32_t count;
+    uint32_t maximum; /* last position + 1 */
+} lia_group;
+
+/* Limits configured once per engine (Engine::configure_paging, paging.rs:30-93). */
+typedef struct lia_paging_limits {
+    uint32_t max_sequences; /* 1..=64 in the reference */
+    uint32_t context;       /* per-request context, 1..=131072 */
+    uint32_t page_size;     /* PAGE_TOKENS (32 in the reference) */
+    uint32_t pool_pages;    /* physical pool capacity / page_size */
+    uint32_t vocabulary;    /* token ids must be below this */
+    uint32_t prefill_batch; /* maximum packed rows */
+} lia_paging_limits;
+
+/* Packing result besides the arrays (paging.rs:173-201). */
+typedef struct lia_pack_info {
+    uint32_t stride;   /* ceil(context / page_size), row stride of the flat table */
+    uint32_t maximum;  /* max(position) + 1 over the batch */
+    uint32_t decoding; /* rows <= 8 and outputs == 0..rows */
+    uint32_t span;     /* split-K span the reference would choose */
+    uint32_t parts;    /* split-K parts the reference would choose */
+    uint32_t n_groups;
+} lia_pack_info;
+
+/*
+ * Host packing and validation of one continuous-batching step.
+ * Replaces Engine::run_paged's host section (src/inference/paging.rs:118-201).
+ * tables: n_tables tables concatenated in table_data, table_lens[i] pages each.
+ * Outputs (caller-allocated host arrays):
+ *   positions[n_rows], sequences[n_rows], flat_pages[max_sequences * stride] (unused = 0xFFFFFFFF),
+ *   groups[n_rows] (first info->n_groups valid), cu_seqlens[n_rows + 1] (n_groups + 1 valid),
+ *   slot_mapping[n_rows] = page * page_size + position % page_size.
+ * Returns the first failing check's status; outputs are unspecified on error.
+ */
+int lia_pack_rows(const lia_paging_limits *limits, const lia_paged_row *rows, uint32_t n_rows,
+                  const uint32_t *table_data, const uint32_t *table_lens, uint32_t n_tables,
+                  const uint32_t *outputs, uint32_t n_outputs, uint32_t *positions,
+                  uint32_t *sequences, uint32_t *flat_pages, lia_group *groups,
+                  uint32_t *cu_seqlens, uint32_t *slot_mapping, lia_pack_info *info);
+
+/* decode_span / decode_parts (src/inference/llama.rs:15-35) without the env override. */
+uint32_t lia_decode_span(uint32_t tokens);
+uint32_t lia_decode_parts(uint32_t tokens, uint32_t span);
+
+/*
+ * Device packing: builds the per-row metadata of a step on the GPU from per-sequence
+ * descriptors, so a step needs no host round trip (the reference stages five arrays and
+ * synchronises, paging.rs:224-237).  For batch sequence b (0 <= b < n_seqs):
+ *   table row seq_slots[b], q_lens[b] new tokens at positions cached[b] .. cached[b]+q_lens[b]-1.
+ * Writes cu_seqlens[n_seqs+1], positions[rows], sequences[rows], slot_mapping[rows].
+ * Rows beyond the batch total up to max_rows are left untouched.  status (device, one u32)
+ * receives 0 or the first failing lia_status as a positive number (-status): a missing page
+ * (table entry 0xFFFFFFFF or >= pool_pages), a position >= context, or too many rows.
+ */
+int lia_pack_device(uint32_t n_seqs, const uint32_t *seq_slots, const uint32_t *q_lens,
+                    const uint32_t *cached, const uint32_t *pages, uint32_t stride,
+                    uint32_t page_size, uint32_t pool_pages, uint32_t context, uint32_t max_rows,
+                    uint32_t *cu_seqlens, uint32_t *positions, uint32_t *sequences,
+                    uint32_t *slot_mapping, uint32_t *status, lia_stream_t stream);
+
+/* KV pool geometry. */
+typedef struct lia_kv_layout {
+    uint32_t num_kv_heads;
+    uint32_t head_dim;   /* 64 or 128 */
+    uint32_t page_size;  /* power of two >= 16 */
+    uint32_t pool_pages;
+    int32_t dtype;       /* LIA_F16, LIA_BF16 or LIA_FP8_E4M3 */
+} lia_kv_layout;
+
+/*
+ * KV append scatter through the block table.  Replaces llama_cache_paged
+ * (src/gpu/kernels/llama.rs:162-183): for row r and element i of its
+ * num_kv_heads*head_dim K and V values, writes kc/vc at
+ *   (slot(r) * num_kv_heads * head_dim + i)
+ * with slot(r) = slot_mapping[r] when slot_mapping != NULL, else computed from
+ * positions/sequences/pages/stride exactly as the reference does.  Values are converted
+ * from src_dtype (LIA_F32, LIA_F16 or LIA_BF16) to the pool dtype with round-to-nearest-even
+ * (FP8: divided by the page's scale first, saturated to +-448).
+ */
+int lia_kv_append(const lia_kv_layout *layout, uint32_t rows, const uint32_t *positions,
+                  const uint32_t *sequences, const uint32_t *pages, uint32_t stride,
+                  const uint32_t *slot_mapping, int32_t src_dtype, const void *k, const void *v,
+                  void *kc, void *vc, const float *k_scales, const float *v_scales,
+                  lia_stream_t stream);
+
+/*
+ * FP8 page quantisation: converts n_pages whole pages (page ids in page_ids) of K and V
+ * given as [n_pages][page_size][num_kv_heads][head_dim] in src_dtype into the e4m3 pool,
+ * computing each (page, head) scale as amax / 448 (1 when the page is all zero).
+ * No counterpart in the reference (its KV cache is f16 only).
+ */
+int lia_kv_quantize_pages(const lia_kv_layout *layout, uint32_t n_pages, const uint32_t *page_ids,
+                          int32_t src_dtype, const void *k, const void *v, void *kc, void *vc,
+                          float *k_scales, float *v_scales, lia_stream_t stream);
+
+/* Geometry and capacity of one paged-attention engine. */
+typedef struct lia_attention_config {
+    uint32_t num_q_heads;
+    uint32_t num_kv_heads;
+    uint32_t head_dim;    /* 64 or 128 */
+    uint32_t page_size;   /* power of two >= 16 */
+    uint32_t pool_pages;
+    uint32_t stride;      /* table row stride (pages per sequence) */
+    int32_t q_dtype;      /* LIA_F32 or LIA_BF16 */
+    int32_t kv_dtype;     /* LIA_F16, LIA_BF16 or LIA_FP8_E4M3 */
+    int32_t out_dtype;    /* LIA_F32 or LIA_BF16 */
+    float scale;          /* softmax scale, 1/sqrt(head_dim) in the reference */
+    uint32_t max_seqs;    /* capacity of cu_seqlens - 1 */
+    uint32_t max_rows;    /* capacity of the packed rows */
+    uint32_t max_context; /* largest key count of one sequence */
+} lia_attention_config;
+
+/* Bytes of device workspace lia_paged_attention needs.  Replaces llama::workspace
+ * (src/inference/llama.rs:37-43). */
+size_t lia_attention_workspace_bytes(const lia_attention_config *config);
+
+/*
+ * Paged causal GQA attention over one ragged packed batch: decode rows, MTP-verify rows
+ * (several consecutive rows of one sequence) and chunked / prefix-cached prefill chunks
+ * in any mix.  Replaces the tile loop of llama_attention_selected together with
+ * gpu::llama_attention::{partial, merge} (src/inference/llama.rs:253-288,
+ * src/gpu/llama_attention.rs:24-207).
+ * Batch sequence b owns rows cu_seqlens[b] .. cu_seqlens[b+1]-1, all of table row
+ * sequences[cu_seqlens[b]], with consecutive positions; row r attends keys
+ * 0 ..= positions[r] of its sequence (the reference's per-row causal limit,
+ * src/gpu/kernels/llama_flash_kernel.rs:145-154).  The new rows' K/V must already be
+ * appended.  Output: out[r][h][d] = softmax(q.K^T * scale) V in out_dtype.
+ */
+int lia_paged_attention(const lia_attention_config *config, uint32_t n_seqs, uint32_t n_rows,
+                        const uint32_t *cu_seqlens, const uint32_t *positions,
+                        const uint32_t *sequences, const uint32_t *pages, const void *q,
+                        const void *kc, const void *vc, const float *k_scales,
+                        const float *v_scales, void *workspace, size_t workspace_bytes,
+                        void *out, lia_stream_t stream);
+
+/*
+ * The three stages of lia_paged_attention, for callers that share one plan across layers
+ * (the metadata of a step is the same for every layer) and for timing the stages apart.
+ *   lia_attention_plan:    builds the step's work list in the workspace from cu_seqlens
+ *                          and positions (replaces the host planning of llama_plan::tiles,
+ *                          src/inference/llama_plan.rs:16-101).
+ *   lia_attention_partial: the split attention kernel; units covered by one wavefront are
+ *                          written normalised to out, the others leave partial records
+ *                          (replaces gpu::llama_attention::partial, llama_attention.rs:24-159).
+ *   lia_attention_merge:   combines the partial records into out (replaces
+ *                          gpu::llama_attention::merge, llama_attention.rs:163-207).
+ * n_seqs / n_rows must be the same in all three calls of one plan.
+ */
+int lia_attention_plan(const lia_attention_config *config, uint32_t n_seqs, uint32_t n_rows,
+                       const uint32_t *cu_seqlens, const uint32_t *positions, void *workspace,
+                       size_t workspace_bytes, lia_stream_t stream);
+int lia_attention_partial(const lia_attention_config *config, uint32_t n_seqs, uint32_t n_rows,
+                          const uint32_t *cu_seqlens, const uint32_t *positions,
+                          const uint32_t *sequences, const uint32_t *pages, const void *q,
+                          const void *kc, const void *vc, const float *k_scales,
+                          const float *v_scales, void *workspace, size_t workspace_bytes,
+                          void *out, lia_stream_t stream);
+int lia_attention_merge(const lia_attention_config *config, uint32_t n_seqs, uint32_t n_rows,
+                        const uint32_t *cu_seqlens, const uint32_t *positions, void *workspace,
+                        size_t workspace_bytes, void *out, lia_stream_t stream);
+
+/* Number of compute units the library schedules decode work for (device 0 unless
+ * lia_init selected another).  0 on failure. */
+uint32_t lia_device_cus(void);
+
+/* Optional: select the device and cache its properties.  Returns LIA_OK. */
+int lia_init(int device);
+
+#ifdef __cplusplus
+}
+#endif
+
+#endif /* LIA_HIP_H */

@@ -1,0 +1,373 @@
+"""Host side of the MI355X paged continuous-batching attention path.
+
+A thin ctypes layer over liblia_hip.so (the C ABI declared in include/lia_hip.h) plus a
+small engine object that mirrors the reference engine's paged entry points
+(src/inference/paging.rs: Engine::configure_paging, the packing half of
+Engine::run_paged; src/inference/llama.rs: the attention half of
+llama_attention_selected).  PyTorch is used only for device memory and streams.
+
+Importing this module requires the built library: there is no fallback path.
+"""
+import ctypes as C
+import os
+
+import numpy as np
+
+HERE = os.path.dirname(os.path.abspath(__file__))
+LIB_PATH = os.path.join(HERE, "liblia_hip.so")
+
+F32, F16, BF16, FP8 = 0, 1, 2, 3
+NONE = 0xFFFFFFFF
+
+ERRORS = {
+    -1: "invalid packed row count", -2: "invalid output row count",
+    -3: "output row outside packed input", -4: "too many sequence tables",
+    -5: "sequence table exceeds context", -6: "physical page outside KV pool",
+    -7: "invalid packed token", -8: "packed position exceeds context",
+    -9: "missing sequence table", -10: "missing physical KV page",
+    -11: "duplicate physical KV write",
+    -12: "packed positions must be consecutive within each request",
+    -19: "invalid paging configuration", -20: "invalid argument", -21: "unaligned buffer",
+    -22: "workspace exhausted", -23: "unsupported geometry", -30: "HIP runtime error",
+}
+
+
+class LiaError(RuntimeError):
+    def __init__(self, status, where=""):
+        self.status = status
+        super().__init__(f"{where}: {ERRORS.get(status, 'status %d' % status)} ({status})")
+
+
+class PagedRow(C.Structure):
+    """PagedRow (src/inference/paging.rs:7-11)."""
+    _fields_ = [("token", C.c_uint32), ("position", C.c_uint32), ("sequence", C.c_uint32)]
+
+
+class Group(C.Structure):
+    """Query group (src/inference/llama_plan.rs:2-6)."""
+    _fields_ = [("start", C.c_uint32), ("count", C.c_uint32), ("maximum", C.c_uint32)]
+
+
+class PagingLimits(C.Structure):
+    _fields_ = [("max_sequences", C.c_uint32), ("context", C.c_uint32),
+                ("page_size", C.c_uint32), ("pool_pages", C.c_uint32),
+                ("vocabulary", C.c_uint32), ("prefill_batch", C.c_uint32)]
+
+
+class PackInfo(C.Structure):
+    _fields_ = [("stride", C.c_uint32), ("maximum", C.c_uint32), ("decoding", C.c_uint32),
+                ("span", C.c_uint32), ("parts", C.c_uint32), ("n_groups", C.c_uint32)]
+
+
+class KVLayout(C.Structure):
+    _fields_ = [("num_kv_heads", C.c_uint32), ("head_dim", C.c_uint32),
+                ("page_size", C.c_uint32), ("pool_pages", C.c_uint32), ("dtype", C.c_int32)]
+
+
+class AttentionConfig(C.Structure):
+    _fields_ = [("num_q_heads", C.c_uint32), ("num_kv_heads", C.c_uint32),
+                ("head_dim", C.c_uint32), ("page_size", C.c_uint32),
+                ("pool_pages", C.c_uint32), ("stride", C.c_uint32), ("q_dtype", C.c_int32),
+                ("kv_dtype", C.c_int32), ("out_dtype", C.c_int32), ("scale", C.c_float),
+                ("max_seqs", C.c_uint32), ("max_rows", C.c_uint32),
+                ("max_context", C.c_uint32)]
+
+
+EXPORTS = {
+    # name: (restype, argtypes)
+    "lia_pack_rows": (C.c_int, [C.POINTER(PagingLimits), C.POINTER(PagedRow), C.c_uint32,
+                                C.c_void_p, C.c_void_p, C.c_uint32, C.c_void_p, C.c_uint32,
+                                C.c_void_p, C.c_void_p, C.c_void_p, C.c_void_p, C.c_void_p,
+                                C.c_void_p, C.POINTER(PackInfo)]),
+    "lia_decode_span": (C.c_uint32, [C.c_uint32]),
+    "lia_decode_parts": (C.c_uint32, [C.c_uint32, C.c_uint32]),
+    "lia_pack_device": (C.c_int, [C.c_uint32, C.c_void_p, C.c_void_p, C.c_void_p, C.c_void_p,
+                                  C.c_uint32, C.c_uint32, C.c_uint32, C.c_uint32, C.c_uint32,
+                                  C.c_void_p, C.c_void_p, C.c_void_p, C.c_void_p, C.c_void_p,
+                                  C.c_void_p]),
+    "lia_kv_append": (C.c_int, [C.POINTER(KVLayout), C.c_uint32, C.c_void_p, C.c_void_p,
+                                C.c_void_p, C.c_uint32, C.c_void_p, C.c_int32, C.c_void_p,
+                                C.c_void_p, C.c_void_p, C.c_void_p, C.c_void_p, C.c_void_p,
+                                C.c_void_p]),
+    "lia_kv_quantize_pages": (C.c_int, [C.POINTER(KVLayout), C.c_uint32, C.c_void_p, C.c_int32,
+                                        C.c_void_p, C.c_void_p, C.c_void_p, C.c_void_p,
+                                        C.c_void_p, C.c_void_p, C.c_void_p]),
+    "lia_attention_workspace_bytes": (C.c_size_t, [C.POINTER(AttentionConfig)]),
+    "lia_paged_attention": (C.c_int, [C.POINTER(AttentionConfig), C.c_uint32, C.c_uint32,
+                                      C.c_void_p, C.c_void_p, C.c_void_p, C.c_void_p,
+                                      C.c_void_p, C.c_void_p, C.c_void_p, C.c_void_p,
+                                      C.c_void_p, C.c_void_p, C.c_size_t, C.c_void_p,
+                                      C.c_void_p]),
+    "lia_attention_plan": (C.c_int, [C.POINTER(AttentionConfig), C.c_uint32, C.c_uint32,
+                                     C.c_void_p, C.c_void_p, C.c_void_p, C.c_size_t,
+                                     C.c_void_p]),
+    "lia_attention_partial": (C.c_int, [C.POINTER(AttentionConfig), C.c_uint32, C.c_uint32,
+                                        C.c_void_p, C.c_void_p, C.c_void_p, C.c_void_p,
+                                        C.c_void_p, C.c_void_p, C.c_void_p, C.c_void_p,
+                                        C.c_void_p, C.c_void_p, C.c_size_t, C.c_void_p,
+                                        C.c_void_p]),
+    "lia_attention_merge": (C.c_int, [C.POINTER(AttentionConfig), C.c_uint32, C.c_uint32,
+                                      C.c_void_p, C.c_void_p, C.c_void_p, C.c_size_t,
+                                      C.c_void_p, C.c_void_p]),
+    "lia_device_cus": (C.c_uint32, []),
+    "lia_init": (C.c_int, [C.c_int]),
+}
+
+_lib = None
+
+
+def lib():
+    """Load liblia_hip.so.  Raises if it has not been built: there is no fallback."""
+    global _lib
+    if _lib is None:
+        if not os.path.exists(LIB_PATH):
+            raise RuntimeError(f"{LIB_PATH} is missing: build it with "
+                               "`python lia.rs_amd/build.py` (no CPU fallback exists)")
+        _lib = C.CDLL(LIB_PATH)
+        for name, (res, args) in EXPORTS.items():
+            fn = getattr(_lib, name)
+            fn.restype = res
+            fn.argtypes = args
+    return _lib
+
+
+def _check(status, where):
+    if status != 0:
+        raise LiaError(status, where)
+
+
+def _dptr(t):
+    """Device (or host) address of a torch tensor, None for None."""
+    if t is None:
+        return None
+    return C.c_void_p(t.data_ptr())
+
+
+def _stream(stream=None):
+    import torch
+    s = stream if stream is not None else torch.cuda.current_stream()
+    return C.c_void_p(s.cuda_stream)
+
+
+def torch_dtype_code(dt):
+    import torch
+    return {torch.float32: F32, torch.float16: F16, torch.bfloat16: BF16,
+            torch.uint8: FP8}[dt]
+
+
+# ------------------------------------------------------------------ host packing
+
+def pack_rows(limits, rows, tables, outputs=()):
+    """Engine::run_paged host packing (src/inference/paging.rs:118-201).
+
+    rows: iterable of (token, position, sequence); tables: list of page lists.
+    Returns a dict of numpy arrays, raising LiaError with the reference's message on the
+    first failing check."""
+    rows = list(rows)
+    n = len(rows)
+    row_arr = (PagedRow * max(n, 1))(*[PagedRow(*r) for r in rows])
+    lens = np.ascontiguousarray([len(t) for t in tables] or [0], dtype=np.uint32)
+    data = np.ascontiguousarray(
+        np.concatenate([np.asarray(t, dtype=np.uint32) for t in tables])
+        if tables and sum(map(len, tables)) else np.zeros(1, np.uint32), dtype=np.uint32)
+    outs = np.ascontiguousarray(list(outputs) or [0], dtype=np.uint32)
+    stride = (limits.context + limits.page_size - 1) // limits.page_size
+    cap = max(n, 1)
+    positions = np.zeros(cap, np.uint32)
+    sequences = np.zeros(cap, np.uint32)
+    flat = np.zeros(max(limits.max_sequences * stride, 1), np.uint32)
+    groups = (Group * cap)()
+    cu = np.zeros(cap + 1, np.uint32)
+    slots = np.zeros(cap, np.uint32)
+    info = PackInfo()
+    st = lib().lia_pack_rows(C.byref(limits), row_arr, n, data.ctypes.data, lens.ctypes.data,
+                             len(tables), outs.ctypes.data, len(outputs), positions.ctypes.data,
+                             sequences.ctypes.data, flat.ctypes.data, C.addressof(groups),
+                             cu.ctypes.data, slots.ctypes.data, C.byref(info))
+    _check(st, "pack_rows")
+    g = info.n_groups
+    return dict(positions=positions[:n], sequences=sequences[:n], flat=flat,
+                groups=np.array([[groups[i].start, groups[i].count, groups[i].maximum]
+                                 for i in range(g)], dtype=np.uint32).reshape(g, 3),
+                cu_seqlens=cu[:g + 1].copy(), slot_mapping=slots[:n], stride=info.stride,
+                maximum=info.maximum, decoding=bool(info.decoding), span=info.span,
+                parts=info.parts)
+
+
+def decode_span(tokens):
+    return lib().lia_decode_span(tokens)
+
+
+def decode_parts(tokens, span):
+    return lib().lia_decode_parts(tokens, span)
+
+
+# ------------------------------------------------------------------ device entry points
+
+def pack_device(seq_slots, q_lens, cached, pages, stride, page_size, pool_pages, context,
+                max_rows, cu_seqlens, positions, sequences, slot_mapping, status, stream=None):
+    """Device packing (lia_pack_device); all arrays are int32/uint32 cuda tensors."""
+    st = lib().lia_pack_device(seq_slots.numel(), _dptr(seq_slots), _dptr(q_lens), _dptr(cached),
+                               _dptr(pages), stride, page_size, pool_pages, context, max_rows,
+                               _dptr(cu_seqlens), _dptr(positions), _dptr(sequences),
+                               _dptr(slot_mapping), _dptr(status), _stream(stream))
+    _check(st, "pack_device")
+
+
+def kv_append(layout, k, v, kc, vc, positions=None, sequences=None, pages=None, stride=0,
+              slot_mapping=None, k_scales=None, v_scales=None, stream=None):
+    """KV append scatter (lia_kv_append, semantics of llama_cache_paged)."""
+    rows = k.shape[0]
+    st = lib().lia_kv_append(C.byref(layout), rows, _dptr(positions), _dptr(sequences),
+                             _dptr(pages), stride, _dptr(slot_mapping), torch_dtype_code(k.dtype),
+                             _dptr(k), _dptr(v), _dptr(kc), _dptr(vc), _dptr(k_scales),
+                             _dptr(v_scales), _stream(stream))
+    _check(st, "kv_append")
+
+
+def kv_quantize_pages(layout, page_ids, k, v, kc, vc, k_scales, v_scales, stream=None):
+    st = lib().lia_kv_quantize_pages(C.byref(layout), page_ids.numel(), _dptr(page_ids),
+                                     torch_dtype_code(k.dtype), _dptr(k), _dptr(v), _dptr(kc),
+                                     _dptr(vc), _dptr(k_scales), _dptr(v_scales), _stream(stream))
+    _check(st, "kv_quantize_pages")
+
+
+def workspace_bytes(config):
+    return lib().lia_attention_workspace_bytes(C.byref(config))
+
+
+def paged_attention(config, n_seqs, cu_seqlens, positions, sequences, pages, q, kc, vc, out,
+                    workspace, k_scales=None, v_scales=None, stream=None):
+    """Ragged paged attention (lia_paged_attention)."""
+    st = lib().lia_paged_attention(C.byref(config), n_seqs, q.shape[0], _dptr(cu_seqlens),
+                                   _dptr(positions), _dptr(sequences), _dptr(pages), _dptr(q),
+                                   _dptr(kc), _dptr(vc), _dptr(k_scales), _dptr(v_scales),
+                                   _dptr(workspace), workspace.numel() * workspace.element_size(),
+                                   _dptr(out), _stream(stream))
+    _check(st, "paged_attention")
+
+
+def attention_plan(config, n_seqs, n_rows, cu_seqlens, positions, workspace, stream=None):
+    st = lib().lia_attention_plan(C.byref(config), n_seqs, n_rows, _dptr(cu_seqlens),
+                                  _dptr(positions), _dptr(workspace),
+                                  workspace.numel() * workspace.element_size(), _stream(stream))
+    _check(st, "attention_plan")
+
+
+def attention_partial(config, n_seqs, cu_seqlens, positions, sequences, pages, q, kc, vc, out,
+                      workspace, k_scales=None, v_scales=None, stream=None):
+    st = lib().lia_attention_partial(C.byref(config), n_seqs, q.shape[0], _dptr(cu_seqlens),
+                                     _dptr(positions), _dptr(sequences), _dptr(pages), _dptr(q),
+                                     _dptr(kc), _dptr(vc), _dptr(k_scales), _dptr(v_scales),
+                                     _dptr(workspace),
+                                     workspace.numel() * workspace.element_size(), _dptr(out),
+                                     _stream(stream))
+    _check(st, "attention_partial")
+
+
+def attention_merge(config, n_seqs, n_rows, cu_seqlens, positions, out, workspace, stream=None):
+    st = lib().lia_attention_merge(C.byref(config), n_seqs, n_rows, _dptr(cu_seqlens),
+                                   _dptr(positions), _dptr(workspace),
+                                   workspace.numel() * workspace.element_size(), _dptr(out),
+                                   _stream(stream))
+    _check(st, "attention_merge")
+
+
+# ------------------------------------------------------------------ engine mirror
+
+class Engine:
+    """Paged KV pool + metadata of one engine, mirroring the reference Engine's paged
+    surface (src/inference/paging.rs:30-261, src/inference/llama.rs:79-299) for the
+    attention path only: the model's projections are outside this path, so
+    `attention()` takes the per-layer q/k/v rows directly."""
+
+    def __init__(self, num_q_heads=16, num_kv_heads=2, head_dim=128, pool_tokens=65536,
+                 layers=1, page_size=32, kv_dtype=F16, q_dtype=F32, out_dtype=F32,
+                 vocabulary=130560, prefill_batch=512, scale=None, device="cuda"):
+        import torch
+        if pool_tokens % page_size:
+            raise LiaError(-19, "Engine: physical KV pool must contain complete pages")
+        self.hq, self.hkv, self.d = num_q_heads, num_kv_heads, head_dim
+        self.page_size, self.pool_pages = page_size, pool_tokens // page_size
+        self.layers, self.kv_dtype = layers, kv_dtype
+        self.q_dtype, self.out_dtype = q_dtype, out_dtype
+        self.vocabulary, self.prefill_batch = vocabulary, prefill_batch
+        self.scale = float(scale if scale is not None else 1.0 / np.sqrt(head_dim))
+        self.device = device
+        storage = torch.uint8 if kv_dtype == FP8 else torch.uint16
+        shape = (pool_tokens, num_kv_heads, head_dim)
+        self.k = [torch.zeros(shape, dtype=storage, device=device) for _ in range(layers)]
+        self.v = [torch.zeros(shape, dtype=storage, device=device) for _ in range(layers)]
+        if kv_dtype == FP8:
+            self.k_scales = [torch.ones(self.pool_pages * num_kv_heads, dtype=torch.float32,
+                                        device=device) for _ in range(layers)]
+            self.v_scales = [torch.ones_like(self.k_scales[0]) for _ in range(layers)]
+        else:
+            self.k_scales = self.v_scales = [None] * layers
+        self.paging = None
+
+    def configure_paging(self, maximum_sequences, context):
+        """Engine::configure_paging (src/inference/paging.rs:30-93)."""
+        import torch
+        if self.paging is not None:
+            raise LiaError(-19, "paging must be configured before execution")
+        if not 1 <= maximum_sequences <= 64:
+            raise LiaError(-19, "invalid sequence count")
+        if not 1 <= context <= 131072:
+            raise LiaError(-19, "invalid per-request context")
+        stride = -(-context // self.page_size)
+        rows = self.prefill_batch
+        dev = self.device
+        self.limits = PagingLimits(maximum_sequences, context, self.page_size, self.pool_pages,
+                                   self.vocabulary, rows)
+        self.config = AttentionConfig(self.hq, self.hkv, self.d, self.page_size, self.pool_pages,
+                                      stride, self.q_dtype, self.kv_dtype, self.out_dtype,
+                                      self.scale, maximum_sequences, rows, context)
+        self.paging = dict(
+            stride=stride,
+            positions=torch.zeros(rows, dtype=torch.int32, device=dev),
+            sequences=torch.zeros(rows, dtype=torch.int32, device=dev),
+            slot_mapping=torch.zeros(rows, dtype=torch.int32, device=dev),
+            pages=torch.zeros(maximum_sequences * stride, dtype=torch.int32, device=dev),
+            cu_seqlens=torch.zeros(rows + 1, dtype=torch.int32, device=dev),
+            workspace=torch.zeros(workspace_bytes(self.config), dtype=torch.uint8, device=dev),
+            n_seqs=0, n_rows=0)
+        torch.cuda.synchronize()
+
+    def stage(self, rows, tables, outputs=()):
+        """Host packing + metadata upload of Engine::run_paged (paging.rs:118-237)."""
+        import torch
+        if self.paging is None:
+            raise LiaError(-19, "paging is not configured")
+        packed = pack_rows(self.limits, rows, tables, outputs)
+        w = self.paging
+        n = len(packed["positions"])
+        ng = len(packed["cu_seqlens"]) - 1
+        as_i32 = lambda a: torch.from_numpy(a.view(np.int32))
+        w["positions"][:n].copy_(as_i32(packed["positions"]))
+        w["sequences"][:n].copy_(as_i32(packed["sequences"]))
+        w["slot_mapping"][:n].copy_(as_i32(packed["slot_mapping"]))
+        w["pages"].copy_(as_i32(packed["flat"]))
+        w["cu_seqlens"][:ng + 1].copy_(as_i32(packed["cu_seqlens"]))
+        w["n_seqs"], w["n_rows"] = ng, n
+        torch.cuda.current_stream().synchronize()
+        return packed
+
+    def attention(self, layer, q, k, v, out=None):
+        """Append this step's K/V rows to layer's pool and attend (llama.rs:203-288)."""
+        import torch
+        w = self.paging
+        n = w["n_rows"]
+        if q.shape[0] != n or k.shape[0] != n:
+            raise LiaError(-20, "attention: row count differs from the staged batch")
+        layout = KVLayout(self.hkv, self.d, self.page_size, self.pool_pages, self.kv_dtype)
+        kv_append(layout, k.reshape(n, -1), v.reshape(n, -1), self.k[layer], self.v[layer],
+                  slot_mapping=w["slot_mapping"], k_scales=self.k_scales[layer],
+                  v_scales=self.v_scales[layer])
+        if out is None:
+            odt = torch.float32 if self.out_dtype == F32 else torch.bfloat16
+            out = torch.empty((n, self.hq, self.d), dtype=odt, device=q.device)
+        paged_attention(self.config, w["n_seqs"], w["cu_seqlens"], w["positions"],
+                        w["sequences"], w["pages"], q, self.k[layer], self.v[layer], out,
+                        w["workspace"], self.k_scales[layer], self.v_scales[layer])
+        return out

@@ -1,0 +1,134 @@
+// Shared device helpers for the gfx950 (CDNA4) paged attention kernels.
+#pragma once
+
+#include <hip/hip_runtime.h>
+#include <stdint.h>
+
+#include "../../include/lia_hip.h"
+
+namespace lia {
+
+typedef __attribute__((ext_vector_type(8))) __bf16 bf16x8;
+typedef __attribute__((ext_vector_type(8))) _Float16 f16x8;
+typedef __attribute__((ext_vector_type(4))) float f32x4;
+typedef __attribute__((ext_vector_type(4))) uint32_t u32x4;
+typedef __attribute__((ext_vector_type(2))) uint32_t u32x2;
+typedef __attribute__((__vector_size__(4 * sizeof(short)))) short s16x4;
+
+constexpr uint32_t kWave = 64;
+constexpr uint32_t kNone = 0xffffffffu;
+
+// ------------------------------------------------------------------ conversions
+// Round-to-nearest-even conversions written from the IEEE / OCP format definitions.
+// They are bit-identical to the CPU oracle's (tests assert it) and to the hardware
+// conversion instructions for every finite input.
+
+__device__ __forceinline__ uint32_t f2u(float f) { return __builtin_bit_cast(uint32_t, f); }
+__device__ __forceinline__ float u2f(uint32_t u) { return __builtin_bit_cast(float, u); }
+
+__device__ __forceinline__ uint16_t f32_to_bf16(float f) {
+    uint32_t x = f2u(f);
+    if ((x & 0x7fffffffu) > 0x7f800000u) return (uint16_t)(((x >> 16) & 0x8000u) | 0x7fc0u);
+    x += 0x7fffu + ((x >> 16) & 1u);
+    return (uint16_t)(x >> 16);
+}
+
+__device__ __forceinline__ float bf16_to_f32(uint32_t b) { return u2f(b << 16); }
+
+__device__ __forceinline__ uint16_t f32_to_f16(float f) {
+    uint32_t x = f2u(f);
+    uint32_t sign = (x >> 16) & 0x8000u;
+    uint32_t ax = x & 0x7fffffffu;
+    if (ax > 0x7f800000u) return (uint16_t)(sign | 0x7e00u);
+    if (ax >= 0x477ff000u) return (uint16_t)(sign | 0x7c00u);
+    if (ax < 0x38800000u) {
+        uint32_t e = ax >> 23;
+        if (e < 102) return (uint16_t)sign;
+        uint32_t m = (ax & 0x7fffffu) | 0x800000u;
+        uint32_t shift = 126 - e;
+        uint32_t q = m >> shift;
+        uint32_t rem = m & ((1u << shift) - 1);
+        uint32_t half = 1u << (shift - 1);
+        if (rem > half || (rem == half && (q & 1))) q++;
+        return (uint16_t)(sign | q);
+    }
+    uint32_t r = ax - (112u << 23);
+    r += 0xfffu + ((r >> 13) & 1u);
+    return (uint16_t)(sign | (r >> 13));
+}
+
+__device__ __forceinline__ float f16_to_f32(uint32_t h) {
+    return (float)__builtin_bit_cast(_Float16, (uint16_t)h);
+}
+
+// OCP E4M3FN, saturating to +-448, NaN -> 0x7f.
+__device__ __forceinline__ uint8_t f32_to_e4m3(float f) {
+    uint32_t x = f2u(f);
+    uint32_t sign = (x >> 24) & 0x80u;
+    uint32_t ax = x & 0x7fffffffu;
+    if (ax > 0x7f800000u) return 0x7f;
+    if (ax >= 0x43e00000u) return (uint8_t)(sign | 0x7e);
+    if (ax < 0x3c800000u) {
+        float q = __builtin_rintf(u2f(ax) * 512.0f);
+        return (uint8_t)(sign | (uint32_t)q);
+    }
+    uint32_t r = ax + 0x7ffffu + ((ax >> 20) & 1u);
+    uint32_t code = (r >> 20) - (120u << 3);
+    if (code > 0x7e) code = 0x7e;
+    return (uint8_t)(sign | code);
+}
+
+// Two e4m3 bytes (bits 0-7 and 16-23 of t) -> two f16 lanes holding value * 2^-8.
+// E4M3 is a sub-format of binary16 once the exponent bias is moved from 7 to 15:
+// shifting the 7 exponent+mantissa bits left by 7 yields exactly value * 2^-8 for
+// normals and subnormals alike (the caller folds 2^8 into its scale).
+__device__ __forceinline__ uint32_t e4m3x2_to_f16x2_scaled(uint32_t t) {
+    return ((t & 0x00800080u) << 8) | ((t & 0x007f007fu) << 7);
+}
+
+// 4 packed e4m3 bytes -> 4 f16 (as 2 dwords), value * 2^-8.
+__device__ __forceinline__ u32x2 e4m3x4_to_f16x4_scaled(uint32_t w) {
+    uint32_t lo = __builtin_amdgcn_perm(0u, w, 0x0c010c00u); // bytes b0, b1 -> bits 0-7, 16-23
+    uint32_t hi = __builtin_amdgcn_perm(0u, w, 0x0c030c02u); // bytes b2, b3
+    u32x2 r;
+    r.x = e4m3x2_to_f16x2_scaled(lo);
+    r.y = e4m3x2_to_f16x2_scaled(hi);
+    return r;
+}
+
+// ------------------------------------------------------------------ wave helpers
+
+__device__ __forceinline__ float shfl_xor(float v, int mask) { return __shfl_xor(v, mask, 64); }
+
+__device__ __forceinline__ uint32_t lane_id() { return __lane_id(); }
+
+template <typename T>
+__device__ __forceinline__ T uniform(T v) {
+    return __builtin_bit_cast(T, __builtin_amdgcn_readfirstlane(__builtin_bit_cast(int, v)));
+}
+
+// MFMA 16x16x32 with f32 accumulation; operands are raw 16-byte register quads.
+// A[m][k]: lane l holds row m = l%16, k = 8*(l/16) .. +7.  B[k][n]: lane l holds column
+// n = l%16, the same k.  D[m][n]: lane l holds rows 4*(l/16) .. +3 of column l%16.
+template <bool BF16>
+__device__ __forceinline__ f32x4 mfma16x16x32(u32x4 a, u32x4 b, f32x4 c) {
+    if constexpr (BF16)
+        return __builtin_amdgcn_mfma_f32_16x16x32_bf16(__builtin_bit_cast(bf16x8, a),
+                                                       __builtin_bit_cast(bf16x8, b), c, 0, 0, 0);
+    else
+        return __builtin_amdgcn_mfma_f32_16x16x32_f16(__builtin_bit_cast(f16x8, a),
+                                                      __builtin_bit_cast(f16x8, b), c, 0, 0, 0);
+}
+
+template <bool BF16>
+__device__ __forceinline__ uint32_t pack2(float a, float b) {
+    if constexpr (BF16)
+        return (uint32_t)f32_to_bf16(a) | ((uint32_t)f32_to_bf16(b) << 16);
+    else
+        return (uint32_t)__builtin_bit_cast(uint16_t, (_Float16)a) |
+               ((uint32_t)__builtin_bit_cast(uint16_t, (_Float16)b) << 16);
+}
+
+__device__ __forceinline__ float fast_exp2(float x) { return __builtin_amdgcn_exp2f(x); }
+
+} // namespace lia

@@ -1,0 +1,264 @@
+// Packing, slot mapping and KV-append scatter for the paged KV pool (gfx950).
+#include "common.hpp"
+
+namespace lia {
+
+// Per-step packing on the device.  One workgroup scans the per-sequence new-token counts
+// into cu_seqlens and then every thread fills rows: position = cached + i, sequence =
+// table row, slot = pages[seq * stride + pos / P] * P + pos % P (the slot rule of
+// src/inference/paging.rs:163-166 and src/gpu/kernels/llama.rs:174-177).
+__global__ __launch_bounds__(1024) void pack_kernel(uint32_t n_seqs, const uint32_t *seq_slots,
+                                                    const uint32_t *q_lens, const uint32_t *cached,
+                                                    const uint32_t *pages, uint32_t stride,
+                                                    uint32_t page_shift, uint32_t pool_pages,
+                                                    uint32_t context, uint32_t max_rows,
+                                                    uint32_t *cu, uint32_t *positions,
+                                                    uint32_t *sequences, uint32_t *slot_mapping,
+                                                    uint32_t *status) {
+    __shared__ uint32_t scan[1024];
+    __shared__ uint32_t carry, error;
+    const uint32_t t = threadIdx.x;
+    if (t == 0) { carry = 0; error = 0; }
+    __syncthreads();
+    const uint32_t P = 1u << page_shift;
+    for (uint32_t base = 0; base < n_seqs; base += 1024) {
+        uint32_t b = base + t;
+        uint32_t n = b < n_seqs ? q_lens[b] : 0;
+        scan[t] = n;
+        __syncthreads();
+        for (uint32_t off = 1; off < 1024; off <<= 1) {
+            uint32_t a = t >= off ? scan[t - off] : 0;
+            __syncthreads();
+            scan[t] += a;
+            __syncthreads();
+        }
+        uint32_t start = carry + scan[t] - n;
+        if (b < n_seqs) {
+            cu[b] = start;
+            if (b == n_seqs - 1) cu[n_seqs] = start + n;
+        }
+        __syncthreads();
+        if (t == 1023) carry += scan[1023];
+        __syncthreads();
+    }
+    const uint32_t total = carry;
+    if (total > max_rows) {
+        if (t == 0) *status = (uint32_t)(-LIA_E_ROWS);
+        return;
+    }
+    // Rows: walk sequences, threads stride over each sequence's rows.
+    for (uint32_t b = 0; b < n_seqs; b++) {
+        uint32_t start = cu[b], n = q_lens[b], slot = seq_slots[b], c0 = cached[b];
+        for (uint32_t i = t; i < n; i += 1024) {
+            uint32_t pos = c0 + i;
+            uint32_t r = start + i;
+            uint32_t s = kNone;
+            if (pos >= context) {
+                atomicCAS(&error, 0u, (uint32_t)(-LIA_E_POSITION));
+            } else {
+                uint32_t page = pages[(size_t)slot * stride + (pos >> page_shift)];
+                if (page >= pool_pages) atomicCAS(&error, 0u, (uint32_t)(-LIA_E_MISSING_PAGE));
+                else s = page * P + (pos & (P - 1));
+            }
+            positions[r] = pos;
+            sequences[r] = slot;
+            slot_mapping[r] = s;
+        }
+    }
+    __syncthreads();
+    if (t == 0) *status = error;
+}
+
+template <typename SRC>
+__device__ __forceinline__ float load_src(const SRC *p, size_t i);
+template <>
+__device__ __forceinline__ float load_src<float>(const float *p, size_t i) { return p[i]; }
+template <>
+__device__ __forceinline__ float load_src<uint16_t>(const uint16_t *p, size_t i) {
+    return bf16_to_f32(p[i]);
+}
+
+// KV append: one thread per (row, 4 consecutive elements).  Mirrors llama_cache_paged
+// (src/gpu/kernels/llama.rs:162-183) for any head count / head_dim / page size and the
+// three pool element types.  src_kind: 0 = f32, 1 = f16, 2 = bf16.
+template <int KVT>
+__global__ __launch_bounds__(256) void append_kernel(uint32_t rows, uint32_t width, uint32_t hd,
+                                                     uint32_t hkv, const uint32_t *positions,
+                                                     const uint32_t *sequences,
+                                                     const uint32_t *pages, uint32_t stride,
+                                                     uint32_t page_shift,
+                                                     const uint32_t *slot_mapping, int src_kind,
+                                                     const void *k, const void *v, void *kc,
+                                                     void *vc, const float *k_scales,
+                                                     const float *v_scales) {
+    const size_t i = ((size_t)blockIdx.x * 256 + threadIdx.x);
+    const uint32_t quads = width / 4;
+    if (i >= (size_t)rows * quads) return;
+    const uint32_t r = (uint32_t)(i / quads), e0 = (uint32_t)(i % quads) * 4;
+    uint32_t slot;
+    if (slot_mapping) {
+        slot = slot_mapping[r];
+    } else {
+        uint32_t pos = positions[r];
+        slot = pages[(size_t)sequences[r] * stride + (pos >> page_shift)] * (1u << page_shift) +
+               (pos & ((1u << page_shift) - 1));
+    }
+    if (slot == kNone) return;
+    float kx[4], vx[4];
+    size_t src = (size_t)r * width + e0;
+#pragma unroll
+    for (int j = 0; j < 4; j++) {
+        if (src_kind == 0) {
+            kx[j] = ((const float *)k)[src + j];
+            vx[j] = ((const float *)v)[src + j];
+        } else if (src_kind == 1) {
+            kx[j] = f16_to_f32(((const uint16_t *)k)[src + j]);
+            vx[j] = f16_to_f32(((const uint16_t *)v)[src + j]);
+        } else {
+            kx[j] = bf16_to_f32(((const uint16_t *)k)[src + j]);
+            vx[j] = bf16_to_f32(((const uint16_t *)v)[src + j]);
+        }
+    }
+    size_t dst = (size_t)slot * width + e0;
+    if constexpr (KVT == LIA_FP8_E4M3) {
+        uint32_t page = slot >> page_shift, h = e0 / hd;
+        float ks = k_scales[(size_t)page * hkv + h], vs = v_scales[(size_t)page * hkv + h];
+        uint32_t kw = 0, vw = 0;
+#pragma unroll
+        for (int j = 0; j < 4; j++) {
+            kw |= (uint32_t)f32_to_e4m3(kx[j] / ks) << (8 * j);
+            vw |= (uint32_t)f32_to_e4m3(vx[j] / vs) << (8 * j);
+        }
+        *(uint32_t *)((uint8_t *)kc + dst) = kw;
+        *(uint32_t *)((uint8_t *)vc + dst) = vw;
+    } else {
+        uint16_t kh[4], vh[4];
+#pragma unroll
+        for (int j = 0; j < 4; j++) {
+            kh[j] = KVT == LIA_BF16 ? f32_to_bf16(kx[j]) : f32_to_f16(kx[j]);
+            vh[j] = KVT == LIA_BF16 ? f32_to_bf16(vx[j]) : f32_to_f16(vx[j]);
+        }
+        u32x2 kq = u32x2{(uint32_t)kh[0] | ((uint32_t)kh[1] << 16), (uint32_t)kh[2] | ((uint32_t)kh[3] << 16)};
+        u32x2 vq = u32x2{(uint32_t)vh[0] | ((uint32_t)vh[1] << 16), (uint32_t)vh[2] | ((uint32_t)vh[3] << 16)};
+        *(u32x2 *)((uint16_t *)kc + dst) = kq;
+        *(u32x2 *)((uint16_t *)vc + dst) = vq;
+    }
+}
+
+// FP8 page quantisation: one workgroup per (page, kv head, plane).  The scale is the
+// page's absolute maximum over that head / 448, 1 for an all-zero page.
+__global__ __launch_bounds__(256) void quantize_kernel(uint32_t P, uint32_t hkv, uint32_t hd,
+                                                       const uint32_t *page_ids, int src_kind,
+                                                       const void *k, const void *v, void *kc,
+                                                       void *vc, float *k_scales,
+                                                       float *v_scales) {
+    __shared__ float red[256];
+    const uint32_t n = blockIdx.x, h = blockIdx.y, plane = blockIdx.z, t = threadIdx.x;
+    const void *src = plane ? v : k;
+    uint8_t *dst = (uint8_t *)(plane ? vc : kc);
+    float *scales = plane ? v_scales : k_scales;
+    const uint32_t page = page_ids[n];
+    const uint32_t count = P * hd;
+    auto at = [&](uint32_t e) -> size_t {
+        uint32_t tok = e / hd, d = e % hd;
+        return (((size_t)n * P + tok) * hkv + h) * hd + d;
+    };
+    auto val = [&](size_t i) -> float {
+        if (src_kind == 0) return ((const float *)src)[i];
+        if (src_kind == 1) return f16_to_f32(((const uint16_t *)src)[i]);
+        return bf16_to_f32(((const uint16_t *)src)[i]);
+    };
+    float amax = 0.0f;
+    for (uint32_t e = t; e < count; e += 256) amax = fmaxf(amax, fabsf(val(at(e))));
+    red[t] = amax;
+    __syncthreads();
+    for (uint32_t off = 128; off > 0; off >>= 1) {
+        if (t < off) red[t] = fmaxf(red[t], red[t + off]);
+        __syncthreads();
+    }
+    float s = red[0] > 0.0f ? red[0] / 448.0f : 1.0f;
+    if (t == 0) scales[(size_t)page * hkv + h] = s;
+    for (uint32_t e = t; e < count; e += 256) {
+        uint32_t tok = e / hd, d = e % hd;
+        dst[(((size_t)page * P + tok) * hkv + h) * hd + d] = f32_to_e4m3(val(at(e)) / s);
+    }
+}
+
+} // namespace lia
+
+using namespace lia;
+
+static int src_kind_of(int32_t dtype) {
+    return dtype == LIA_F32 ? 0 : dtype == LIA_F16 ? 1 : dtype == LIA_BF16 ? 2 : -1;
+}
+
+extern "C" int lia_pack_device(uint32_t n_seqs, const uint32_t *seq_slots, const uint32_t *q_lens,
+                               const uint32_t *cached, const uint32_t *pages, uint32_t stride,
+                               uint32_t page_size, uint32_t pool_pages, uint32_t context,
+                               uint32_t max_rows, uint32_t *cu_seqlens, uint32_t *positions,
+                               uint32_t *sequences, uint32_t *slot_mapping, uint32_t *status,
+                               lia_stream_t stream) {
+    if (n_seqs == 0 || !seq_slots || !q_lens || !cached || !pages || !cu_seqlens || !positions ||
+        !sequences || !slot_mapping || !status || stride == 0)
+        return LIA_E_ARG;
+    if (page_size == 0 || (page_size & (page_size - 1))) return LIA_E_ARG;
+    hipLaunchKernelGGL(pack_kernel, dim3(1), dim3(1024), 0, (hipStream_t)stream, n_seqs, seq_slots,
+                       q_lens, cached, pages, stride, (uint32_t)__builtin_ctz(page_size), pool_pages,
+                       context, max_rows, cu_seqlens, positions, sequences, slot_mapping, status);
+    return hipGetLastError() == hipSuccess ? LIA_OK : LIA_E_HIP;
+}
+
+extern "C" int lia_kv_append(const lia_kv_layout *L, uint32_t rows, const uint32_t *positions,
+                             const uint32_t *sequences, const uint32_t *pages, uint32_t stride,
+                             const uint32_t *slot_mapping, int32_t src_dtype, const void *k,
+                             const void *v, void *kc, void *vc, const float *k_scales,
+                             const float *v_scales, lia_stream_t stream) {
+    if (!L || !k || !v || !kc || !vc) return LIA_E_ARG;
+    if (rows == 0) return LIA_OK;
+    if (!slot_mapping && (!positions || !sequences || !pages || stride == 0)) return LIA_E_ARG;
+    if (L->page_size == 0 || (L->page_size & (L->page_size - 1))) return LIA_E_ARG;
+    if (L->num_kv_heads == 0 || L->head_dim == 0 || L->head_dim % 4) return LIA_E_ARG;
+    int kind = src_kind_of(src_dtype);
+    if (kind < 0) return LIA_E_UNSUPPORTED;
+    if (L->dtype == LIA_FP8_E4M3 && (!k_scales || !v_scales)) return LIA_E_ARG;
+    uint32_t width = L->num_kv_heads * L->head_dim;
+    size_t threads = (size_t)rows * (width / 4);
+    dim3 grid((uint32_t)((threads + 255) / 256));
+    uint32_t shift = (uint32_t)__builtin_ctz(L->page_size);
+    hipStream_t s = (hipStream_t)stream;
+    switch (L->dtype) {
+    case LIA_F16:
+        hipLaunchKernelGGL(append_kernel<LIA_F16>, grid, dim3(256), 0, s, rows, width, L->head_dim,
+                           L->num_kv_heads, positions, sequences, pages, stride, shift, slot_mapping,
+                           kind, k, v, kc, vc, k_scales, v_scales);
+        break;
+    case LIA_BF16:
+        hipLaunchKernelGGL(append_kernel<LIA_BF16>, grid, dim3(256), 0, s, rows, width, L->head_dim,
+                           L->num_kv_heads, positions, sequences, pages, stride, shift, slot_mapping,
+                           kind, k, v, kc, vc, k_scales, v_scales);
+        break;
+    case LIA_FP8_E4M3:
+        hipLaunchKernelGGL(append_kernel<LIA_FP8_E4M3>, grid, dim3(256), 0, s, rows, width,
+                           L->head_dim, L->num_kv_heads, positions, sequences, pages, stride, shift,
+                           slot_mapping, kind, k, v, kc, vc, k_scales, v_scales);
+        break;
+    default:
+        return LIA_E_UNSUPPORTED;
+    }
+    return hipGetLastError() == hipSuccess ? LIA_OK : LIA_E_HIP;
+}
+
+extern "C" int lia_kv_quantize_pages(const lia_kv_layout *L, uint32_t n_pages,
+                                     const uint32_t *page_ids, int32_t src_dtype, const void *k,
+                                     const void *v, void *kc, void *vc, float *k_scales,
+                                     float *v_scales, lia_stream_t stream) {
+    if (!L || !page_ids || !k || !v || !kc || !vc || !k_scales || !v_scales) return LIA_E_ARG;
+    if (L->dtype != LIA_FP8_E4M3) return LIA_E_UNSUPPORTED;
+    if (n_pages == 0) return LIA_OK;
+    int kind = src_kind_of(src_dtype);
+    if (kind < 0) return LIA_E_UNSUPPORTED;
+    hipLaunchKernelGGL(quantize_kernel, dim3(n_pages, L->num_kv_heads, 2), dim3(256), 0,
+                       (hipStream_t)stream, L->page_size, L->num_kv_heads, L->head_dim, page_ids,
+                       kind, k, v, kc, vc, k_scales, v_scales);
+    return hipGetLastError() == hipSuccess ? LIA_OK : LIA_E_HIP;
+}
