@@ -1,0 +1,221 @@
+"""Benchmark of the paged decode-attention hot path on one MI355X.
+
+Workload: ragged bf16 decode, batch 8, contexts U[1024, 32768]
+(seeded), 16 query / 2 KV heads, head_dim 128, 16-token pages scattered by a seeded
+permutation, N(0,1) data, 40 layers as independent KV slices.
+
+One step = device packing of the batch (cu_seqlens, positions, slot mapping), the work
+plan, then per layer: KV append of the 8 new tokens, the split attention kernel and the
+split combine.  The step is captured once as a HIP graph and replayed (the reference
+replays CUDA graphs of the paged forward, src/inference/paging.rs:238-259).
+
+value = decode tokens/s of the whole step (8 tokens per step).  The roofline object
+covers the dominant kernel (the split attention kernel), timed alone with HIP events on
+its stream; its algorithmic bytes are K/V of every attended key + Q + O + block table.
+"""
+import argparse
+import json
+import os
+import sys
+import time
+
+import numpy as np
+
+ROOT = os.path.dirname(os.path.abspath(__file__))
+sys.path.insert(0, ROOT)
+
+PEAK_HBM_GBPS = 8000.0
+METRIC = "decode-attn tokens/s + achieved HBM GB/s (% peak), ragged batch 8, 1 GPU"
+
+
+def log(msg):
+    print(f"[bench] {msg}", file=sys.stderr, flush=True)
+
+
+def parse():
+    ap = argparse.ArgumentParser()
+    ap.add_argument("--gpus", type=int, default=1)
+    ap.add_argument("--steps", type=int, default=200)
+    ap.add_argument("--warmup", type=int, default=20)
+    ap.add_argument("--layers", type=int, default=40)
+    ap.add_argument("--seed", type=int, default=0)
+    ap.add_argument("--cpu-seconds", type=float, default=10.0)
+    ap.add_argument("--no-cpu", action="store_true")
+    ap.add_argument("--kernel-reps", type=int, default=20)
+    return ap.parse_args()
+
+
+def main():
+    args = parse()
+    if args.gpus != 1 or int(os.environ.get("WORLD_SIZE", "1")) > 1:
+        print("bench.py: this build measures one GPU only (the path shards by sequence / KV "
+              "head with no cross-GPU exchange; see DESIGN.md); run with --gpus 1",
+              file=sys.stderr)
+        sys.exit(2)
+    import torch
+    from __graft_entry__ import package
+    lia = package()
+    import lia_rs_amd.workloads as wl
+
+    torch.cuda.set_device(0)
+    dev = "cuda"
+    b = wl.config2(seed=args.seed, layers=args.layers)
+    g = b.geom
+    L = args.layers
+    P = g.page_size
+    tokens = b.pool_pages * P
+    log(f"config2: ctx={b.ctx.tolist()} sum={int(b.ctx.sum())} pool_pages={b.pool_pages} "
+        f"layers={L}; {b.notes}")
+
+    # ---- resident inputs: per-layer KV pools, queries and this step's new K/V rows
+    gen = torch.Generator(device=dev)
+    gen.manual_seed(args.seed)
+    kpool, vpool, qs, newk, newv = [], [], [], [], []
+    for layer in range(L):
+        kpool.append(torch.randn((tokens, g.hkv, g.d), generator=gen, device=dev).to(torch.bfloat16))
+        vpool.append(torch.randn((tokens, g.hkv, g.d), generator=gen, device=dev).to(torch.bfloat16))
+        qs.append(torch.randn((b.n_rows, g.hq, g.d), generator=gen, device=dev).to(torch.bfloat16))
+        newk.append(torch.randn((b.n_rows, g.hkv * g.d), generator=gen, device=dev).to(torch.bfloat16))
+        newv.append(torch.randn((b.n_rows, g.hkv * g.d), generator=gen, device=dev).to(torch.bfloat16))
+    outs = [torch.empty((b.n_rows, g.hq, g.d), dtype=torch.bfloat16, device=dev) for _ in range(L)]
+    i32 = lambda a: torch.from_numpy(np.asarray(a, np.uint32).view(np.int32)).to(dev)
+    seq_slots, q_lens, cached = i32(np.arange(b.n_seqs)), i32(b.q_len), i32(b.cached)
+    flat = i32(b.flat_table())
+    rows = b.n_rows
+    cu = torch.zeros(b.n_seqs + 1, dtype=torch.int32, device=dev)
+    positions = torch.zeros(rows, dtype=torch.int32, device=dev)
+    sequences = torch.zeros(rows, dtype=torch.int32, device=dev)
+    slots = torch.zeros(rows, dtype=torch.int32, device=dev)
+    status = torch.zeros(1, dtype=torch.int32, device=dev)
+    cfg = lia.AttentionConfig(g.hq, g.hkv, g.d, P, b.pool_pages, b.stride, g.q_dtype, g.kv_dtype,
+                              g.out_dtype, g.scale, b.n_seqs, rows, int(b.ctx.max()))
+    ws = torch.zeros(lia.workspace_bytes(cfg), dtype=torch.uint8, device=dev)
+    layout = lia.KVLayout(g.hkv, g.d, P, b.pool_pages, g.kv_dtype)
+    context = b.stride * P
+    torch.cuda.synchronize()
+
+    def step():
+        lia.pack_device(seq_slots, q_lens, cached, flat, b.stride, P, b.pool_pages, context, rows,
+                        cu, positions, sequences, slots, status)
+        lia.attention_plan(cfg, b.n_seqs, rows, cu, positions, sequences, ws)
+        for layer in range(L):
+            lia.kv_append(layout, newk[layer], newv[layer], kpool[layer], vpool[layer],
+                          slot_mapping=slots)
+            lia.attention_partial(cfg, b.n_seqs, flat, qs[layer], kpool[layer], vpool[layer],
+                                  outs[layer], ws)
+            lia.attention_merge(cfg, b.n_seqs, rows, outs[layer], ws)
+
+    # eager step once (validates arguments, checks the packing status)
+    step()
+    torch.cuda.synchronize()
+    if status.item() != 0:
+        raise RuntimeError(f"device packing failed: status {status.item()}")
+    graph = torch.cuda.CUDAGraph()
+    with torch.cuda.graph(graph):
+        step()
+    torch.cuda.synchronize()
+
+    # ---- timed region: K graph replays of the whole step
+    for _ in range(args.warmup):
+        graph.replay()
+    torch.cuda.synchronize()
+    start, stop = torch.cuda.Event(enable_timing=True), torch.cuda.Event(enable_timing=True)
+    t0 = time.perf_counter()
+    start.record()
+    for _ in range(args.steps):
+        graph.replay()
+    stop.record()
+    torch.cuda.synchronize()
+    wall = time.perf_counter() - t0
+    ms_step = start.elapsed_time(stop) / args.steps
+    log(f"step: {ms_step:.4f} ms (wall {wall * 1e3 / args.steps:.4f} ms)")
+
+    # ---- dominant kernel alone: one graph of L split-attention launches
+    kgraph = torch.cuda.CUDAGraph()
+    stream = torch.cuda.Stream()
+    with torch.cuda.stream(stream):
+        with torch.cuda.graph(kgraph, stream=stream):
+            for layer in range(L):
+                lia.attention_partial(cfg, b.n_seqs, flat, qs[layer], kpool[layer],
+                                      vpool[layer], outs[layer], ws)
+    torch.cuda.synchronize()
+    for _ in range(3):
+        kgraph.replay()
+    torch.cuda.synchronize()
+    ks, ke = torch.cuda.Event(enable_timing=True), torch.cuda.Event(enable_timing=True)
+    cur = torch.cuda.current_stream()
+    ks.record(cur)
+    for _ in range(args.kernel_reps):
+        kgraph.replay()
+    ke.record(cur)
+    torch.cuda.synchronize()
+    kernel_us = ks.elapsed_time(ke) * 1e3 / (args.kernel_reps * L)
+    layer_bytes = b.algorithmic_bytes()
+    achieved = layer_bytes / (kernel_us * 1e-6) / 1e9
+    step_bytes = layer_bytes * L + rows * g.hkv * g.d * 2 * 2 * L  # + appended K/V rows
+    step_gbps = step_bytes / (ms_step * 1e-3) / 1e9
+    log(f"attention kernel: {kernel_us:.2f} us/launch, {achieved:.1f} GB/s "
+        f"({achieved / PEAK_HBM_GBPS:.1%} of peak), layer bytes {layer_bytes}")
+
+    # ---- the reference algorithm on the host cores (bounded sample, one layer repeated)
+    cpu = None
+    if not args.no_cpu:
+        from oracle import oracle as O
+        kc = kpool[0].view(torch.int16).cpu().numpy().view(np.uint16).reshape(-1)
+        vc = vpool[0].view(torch.int16).cpu().numpy().view(np.uint16).reshape(-1)
+        q32 = qs[0].float().cpu().numpy()
+        geom = O.geom(g.hq, g.hkv, g.d, P, b.stride, g.kv_dtype, g.scale)
+        pos_h, seq_h, flat_h = b.positions(), b.sequences(), b.flat_table()
+        reps, t0 = 0, time.perf_counter()
+        while True:
+            O.paged_attention_f32(geom, pos_h, seq_h, flat_h, q32, kc, vc, span=256)
+            reps += 1
+            el = time.perf_counter() - t0
+            if el >= args.cpu_seconds or reps >= 4 * L:
+                break
+        per_layer = el / reps
+        threads = int(os.environ.get("OMP_NUM_THREADS", os.cpu_count() or 1))
+        cpu = {"value": round(b.n_rows / (per_layer * L), 4), "unit": "tokens/s",
+               "cores": threads, "kind": "port",
+               "sample": f"{reps} x one layer of the config-2 batch (8 rows, sum ctx "
+                         f"{int(b.ctx.sum())}) in f32 split-K (span 256) + merge, "
+                         f"scaled to {L} layers; {per_layer * 1e3:.1f} ms/layer, "
+                         f"{layer_bytes / per_layer / 1e9:.2f} GB/s"}
+        log(f"cpu baseline: {cpu}")
+
+    out = {
+        "metric": METRIC,
+        "value": round(b.n_rows / (ms_step * 1e-3), 2),
+        "unit": "tokens/s",
+        "n_gpus": 1,
+        "steps": args.steps,
+        "warmup": args.warmup,
+        "ms_per_step": round(ms_step, 5),
+        "higher_is_better": True,
+        "scaling": "weak",
+        "vs_baseline": None,
+        "dtype": "bf16",
+        "data": "synthetic (seeded N(0,1) K/V/Q, random-permutation block tables)",
+        "config": {
+            "workload": "BASELINE config 2: ragged bf16 paged decode, batch 8, ctx U[1024,32768] "
+                        "seed %d, 16q/2kv heads, head_dim 128, page 16, %d layers as independent "
+                        "KV slices; step = device pack + plan + per layer (KV append + split "
+                        "attention + combine), HIP-graph replay" % (args.seed, L),
+            "batch": b.n_seqs, "layers": L, "ctx": b.ctx.tolist(), "sum_ctx": int(b.ctx.sum()),
+            "page_size": P, "pool_pages": b.pool_pages,
+            "step_hbm_GBps": round(step_gbps, 1),
+            "step_hbm_frac": round(step_gbps / PEAK_HBM_GBPS, 4),
+        },
+        "roofline": {
+            "bound": "hbm", "achieved": round(achieved, 1), "peak": PEAK_HBM_GBPS, "unit": "GB/s",
+            "frac": round(achieved / PEAK_HBM_GBPS, 4), "traffic": None,
+            "kernel": "attention_kernel<128,1,bf16>", "kernel_us": round(kernel_us, 3),
+            "bytes_per_launch": layer_bytes,
+        },
+        "cpu_baseline": cpu,
+    }
+    print(json.dumps(out), flush=True)
+
+
+if __name__ == "__main__":
+    main()

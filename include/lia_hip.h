@@ -202,9 +202,10 @@ int lia_paged_attention(const lia_attention_config *config, uint32_t n_seqs, uin
 /*
  * The three stages of lia_paged_attention, for callers that share one plan across layers
  * (the metadata of a step is the same for every layer) and for timing the stages apart.
- *   lia_attention_plan:    builds the step's work list in the workspace from cu_seqlens
- *                          and positions (replaces the host planning of llama_plan::tiles,
- *                          src/inference/llama_plan.rs:16-101).
+ *   lia_attention_plan:    builds the step's work list in the workspace from cu_seqlens,
+ *                          positions and sequences (replaces the host planning of
+ *                          llama_plan::tiles, src/inference/llama_plan.rs:16-101); the
+ *                          other two stages read the per-row metadata from it.
  *   lia_attention_partial: the split attention kernel; units covered by one wavefront are
  *                          written normalised to out, the others leave partial records
  *                          (replaces gpu::llama_attention::partial, llama_attention.rs:24-159).
@@ -213,17 +214,15 @@ int lia_paged_attention(const lia_attention_config *config, uint32_t n_seqs, uin
  * n_seqs / n_rows must be the same in all three calls of one plan.
  */
 int lia_attention_plan(const lia_attention_config *config, uint32_t n_seqs, uint32_t n_rows,
-                       const uint32_t *cu_seqlens, const uint32_t *positions, void *workspace,
-                       size_t workspace_bytes, lia_stream_t stream);
+                       const uint32_t *cu_seqlens, const uint32_t *positions,
+                       const uint32_t *sequences, void *workspace, size_t workspace_bytes,
+                       lia_stream_t stream);
 int lia_attention_partial(const lia_attention_config *config, uint32_t n_seqs, uint32_t n_rows,
-                          const uint32_t *cu_seqlens, const uint32_t *positions,
-                          const uint32_t *sequences, const uint32_t *pages, const void *q,
-                          const void *kc, const void *vc, const float *k_scales,
-                          const float *v_scales, void *workspace, size_t workspace_bytes,
-                          void *out, lia_stream_t stream);
+                          const uint32_t *pages, const void *q, const void *kc, const void *vc,
+                          const float *k_scales, const float *v_scales, void *workspace,
+                          size_t workspace_bytes, void *out, lia_stream_t stream);
 int lia_attention_merge(const lia_attention_config *config, uint32_t n_seqs, uint32_t n_rows,
-                        const uint32_t *cu_seqlens, const uint32_t *positions, void *workspace,
-                        size_t workspace_bytes, void *out, lia_stream_t stream);
+                        void *workspace, size_t workspace_bytes, void *out, lia_stream_t stream);
 
 /* Number of compute units the library schedules decode work for (device 0 unless
  * lia_init selected another).  0 on failure. */

@@ -99,16 +99,14 @@ EXPORTS = {
                                       C.c_void_p, C.c_void_p, C.c_size_t, C.c_void_p,
                                       C.c_void_p]),
     "lia_attention_plan": (C.c_int, [C.POINTER(AttentionConfig), C.c_uint32, C.c_uint32,
-                                     C.c_void_p, C.c_void_p, C.c_void_p, C.c_size_t,
+                                     C.c_void_p, C.c_void_p, C.c_void_p, C.c_void_p, C.c_size_t,
                                      C.c_void_p]),
     "lia_attention_partial": (C.c_int, [C.POINTER(AttentionConfig), C.c_uint32, C.c_uint32,
                                         C.c_void_p, C.c_void_p, C.c_void_p, C.c_void_p,
-                                        C.c_void_p, C.c_void_p, C.c_void_p, C.c_void_p,
-                                        C.c_void_p, C.c_void_p, C.c_size_t, C.c_void_p,
-                                        C.c_void_p]),
+                                        C.c_void_p, C.c_void_p, C.c_void_p, C.c_size_t,
+                                        C.c_void_p, C.c_void_p]),
     "lia_attention_merge": (C.c_int, [C.POINTER(AttentionConfig), C.c_uint32, C.c_uint32,
-                                      C.c_void_p, C.c_void_p, C.c_void_p, C.c_size_t,
-                                      C.c_void_p, C.c_void_p]),
+                                      C.c_void_p, C.c_size_t, C.c_void_p, C.c_void_p]),
     "lia_device_cus": (C.c_uint32, []),
     "lia_init": (C.c_int, [C.c_int]),
 }
@@ -247,17 +245,19 @@ def paged_attention(config, n_seqs, cu_seqlens, positions, sequences, pages, q, 
     _check(st, "paged_attention")
 
 
-def attention_plan(config, n_seqs, n_rows, cu_seqlens, positions, workspace, stream=None):
+def attention_plan(config, n_seqs, n_rows, cu_seqlens, positions, sequences, workspace,
+                   stream=None):
+    """Stage 1: the step's work list (shared by every layer of the step)."""
     st = lib().lia_attention_plan(C.byref(config), n_seqs, n_rows, _dptr(cu_seqlens),
-                                  _dptr(positions), _dptr(workspace),
+                                  _dptr(positions), _dptr(sequences), _dptr(workspace),
                                   workspace.numel() * workspace.element_size(), _stream(stream))
     _check(st, "attention_plan")
 
 
-def attention_partial(config, n_seqs, cu_seqlens, positions, sequences, pages, q, kc, vc, out,
-                      workspace, k_scales=None, v_scales=None, stream=None):
-    st = lib().lia_attention_partial(C.byref(config), n_seqs, q.shape[0], _dptr(cu_seqlens),
-                                     _dptr(positions), _dptr(sequences), _dptr(pages), _dptr(q),
+def attention_partial(config, n_seqs, pages, q, kc, vc, out, workspace, k_scales=None,
+                      v_scales=None, stream=None):
+    """Stage 2: the split attention kernel over the planned work list."""
+    st = lib().lia_attention_partial(C.byref(config), n_seqs, q.shape[0], _dptr(pages), _dptr(q),
                                      _dptr(kc), _dptr(vc), _dptr(k_scales), _dptr(v_scales),
                                      _dptr(workspace),
                                      workspace.numel() * workspace.element_size(), _dptr(out),
@@ -265,9 +265,9 @@ def attention_partial(config, n_seqs, cu_seqlens, positions, sequences, pages, q
     _check(st, "attention_partial")
 
 
-def attention_merge(config, n_seqs, n_rows, cu_seqlens, positions, out, workspace, stream=None):
-    st = lib().lia_attention_merge(C.byref(config), n_seqs, n_rows, _dptr(cu_seqlens),
-                                   _dptr(positions), _dptr(workspace),
+def attention_merge(config, n_seqs, n_rows, out, workspace, stream=None):
+    """Stage 3: combine the split records into out."""
+    st = lib().lia_attention_merge(C.byref(config), n_seqs, n_rows, _dptr(workspace),
                                    workspace.numel() * workspace.element_size(), _dptr(out),
                                    _stream(stream))
     _check(st, "attention_merge")

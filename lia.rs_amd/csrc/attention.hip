@@ -5,23 +5,40 @@
 // columns are the rpc*group (row, query head) pairs that share that KV head.  A unit
 // attends keys 0 .. positions[last row of the block], tiled in 32-token blocks.
 //
-// Scheduling is balanced over wavefronts rather than over units: the key blocks of all
-// units are laid end to end and wave w of N takes blocks [w*B/N, (w+1)*B/N).  A unit
-// covered by one wave is written normalised straight to `out`; a unit split across
-// waves leaves one partial record (unnormalised O, running max, running sum) per wave
-// and the combine kernel merges them, which is the reference's split-K partial + merge
+// Scheduling is balanced over workgroups rather than over units: the key blocks of all
+// units are laid end to end and workgroup w of N takes blocks [w*B/N, (w+1)*B/N).  The
+// four wavefronts of a workgroup interleave the 32-token chunks of its range and merge
+// their online-softmax states in LDS at the end of every unit segment.  A unit covered by
+// one workgroup is written normalised straight to `out`; a unit split across workgroups
+// leaves one partial record per workgroup (unnormalised O, reference max, mass) and the
+// combine kernel merges them - the reference's split-K partial + merge
 // (src/gpu/kernels/llama_flash_kernel.rs:321-376, src/gpu/kernels/llama_merge.rs:10-76)
 // with splits chosen for load balance instead of a batch-uniform span.
 //
-// Per 32-token block a wave computes S^T = K * Q^T with K straight from HBM as the MFMA
-// A operand (16 tokens x 32 dims per instruction) and Q^T resident in registers, runs
-// the online softmax in the log2 domain per column, stages V through LDS in its natural
-// token-major layout and reads it back transposed (ds_read_b64_tr_b16) as the A operand
-// of O^T += V^T * P^T.  Causal masking is per column: row r sees keys <= positions[r]
-// (src/gpu/kernels/llama_flash_kernel.rs:145-175).
+// Per 32-token chunk a wave computes S^T = K * Q^T with K straight from HBM (bounded
+// buffer loads) as the MFMA A operand (16 tokens x 32 dims per instruction) and Q^T
+// resident in registers, runs the online softmax in the log2 domain per column, stages V
+// through LDS in its natural token-major layout and reads it back transposed
+// (ds_read_b64_tr_b16) as the A operand of O^T += V^T * P^T.  Causal masking is per
+// column: row r sees keys <= positions[r] (src/gpu/kernels/llama_flash_kernel.rs:145-175).
 #include "common.hpp"
 
 namespace lia {
+
+constexpr int kWaves = 4;                         // wavefronts per attention workgroup
+constexpr uint32_t kThreads = kWaves * 64;
+
+// Unit descriptor written by the plan kernel (32 bytes).
+struct UnitDesc {
+    uint32_t block_start; // first block in the flattened block order
+    uint32_t nblocks;     // 32-token blocks of keys the unit attends
+    uint32_t rowbeg;      // first packed row of the column block
+    uint32_t nrows;       // rows in the column block
+    uint32_t kend;        // keys attended by the last row (positions[last] + 1)
+    uint32_t table_row;   // block-table row of the sequence
+    uint32_t hk;          // KV head
+    uint32_t pos0;        // positions[rowbeg]; rows of a sequence have consecutive positions
+};
 
 struct AttnParams {
     const void *q;
@@ -34,23 +51,27 @@ struct AttnParams {
     const uint32_t *sequences;
     const uint32_t *pages;
     void *out;
-    const uint4 *units;      // [U + 1]: {b, cb, hk, first block}; units[U].w = B
-    const uint32_t *header;  // {U, B}
+    const UnitDesc *units;   // [U + 1]; units[U].block_start = B
+    const uint4 *wg_desc;    // per workgroup: {first unit, first block, end block, 0}
+    const uint32_t *header;  // {U, B, N (workgroups with work), overflow}
     float *part_o;           // [records][cols][D]
     float *part_ml;          // [records][cols][2]
-    uint32_t hq, hkv, group, stride, page_shift, n_waves, rpc;
+    uint32_t hq, hkv, group, stride, page_shift, n_wg, rpc;
     float scale_log2;        // softmax scale * log2(e)
     int q_f32, out_f32;
 };
 
 // ------------------------------------------------------------------ plan
 
-// One workgroup builds the unit list of a step.  Positions within a sequence are
-// consecutive (validated by packing, src/inference/paging.rs:167-172), so the key count
-// of a column block is positions[first row] + (last row index + 1).
+// One workgroup builds the unit list of a step and the block range of every attention
+// workgroup.  Positions within a sequence are consecutive (validated by packing,
+// src/inference/paging.rs:167-172), so the key count of a column block follows from the
+// position of its first row.
 __global__ __launch_bounds__(256) void plan_kernel(uint32_t n_seqs, const uint32_t *cu,
-                                                   const uint32_t *positions, uint32_t rpc,
-                                                   uint32_t hkv, uint32_t max_units, uint4 *units,
+                                                   const uint32_t *positions,
+                                                   const uint32_t *sequences, uint32_t rpc,
+                                                   uint32_t hkv, uint32_t max_units,
+                                                   uint32_t n_wg, UnitDesc *units, uint4 *wg_desc,
                                                    uint32_t *header) {
     __shared__ uint32_t s_units[256], s_blocks[256];
     __shared__ uint32_t carry_units, carry_blocks, overflow;
@@ -59,18 +80,16 @@ __global__ __launch_bounds__(256) void plan_kernel(uint32_t n_seqs, const uint32
     __syncthreads();
     for (uint32_t base = 0; base < n_seqs; base += 256) {
         uint32_t b = base + t;
-        uint32_t nu = 0, nb = 0, r0 = 0, nr = 0, p0 = 0;
+        uint32_t nu = 0, nb = 0, r0 = 0, nr = 0, p0 = 0, trow = 0;
         if (b < n_seqs) {
             r0 = cu[b];
             nr = cu[b + 1] - r0;
             if (nr > 0) {
                 p0 = positions[r0];
+                trow = sequences[r0];
                 uint32_t ncb = (nr + rpc - 1) / rpc;
                 nu = ncb * hkv;
-                for (uint32_t cb = 0; cb < ncb; cb++) {
-                    uint32_t last = min((cb + 1) * rpc, nr);
-                    nb += (p0 + last + 31) / 32;
-                }
+                for (uint32_t cb = 0; cb < ncb; cb++) nb += (p0 + min((cb + 1) * rpc, nr) + 31) / 32;
                 nb *= hkv;
             }
         }
@@ -90,10 +109,12 @@ __global__ __launch_bounds__(256) void plan_kernel(uint32_t n_seqs, const uint32
         if (nu && u + nu <= max_units) {
             uint32_t ncb = nu / hkv;
             for (uint32_t cb = 0; cb < ncb; cb++) {
-                uint32_t last = min((cb + 1) * rpc, nr);
-                uint32_t blocks = (p0 + last + 31) / 32;
+                uint32_t rows = min(rpc, nr - cb * rpc);
+                uint32_t kend = p0 + cb * rpc + rows;
+                uint32_t blocks = (kend + 31) / 32;
                 for (uint32_t h = 0; h < hkv; h++) {
-                    units[u++] = make_uint4(b, cb, h, blk);
+                    units[u++] = UnitDesc{blk, blocks, r0 + cb * rpc, rows, kend, trow, h,
+                                          p0 + cb * rpc};
                     blk += blocks;
                 }
             }
@@ -102,12 +123,26 @@ __global__ __launch_bounds__(256) void plan_kernel(uint32_t n_seqs, const uint32
         if (t == 255) { carry_units += s_units[255]; carry_blocks += s_blocks[255]; }
         __syncthreads();
     }
+    const uint32_t U = overflow ? 0 : carry_units, B = overflow ? 0 : carry_blocks;
+    const uint32_t N = min(n_wg, B);
     if (t == 0) {
-        uint32_t U = overflow ? 0 : carry_units, B = overflow ? 0 : carry_blocks;
-        units[U] = make_uint4(0, 0, 0, B);
+        units[U] = UnitDesc{B, 0, 0, 0, 0, 0, 0, 0};
         header[0] = U;
         header[1] = B;
-        header[2] = overflow;
+        header[2] = N;
+        header[3] = overflow;
+    }
+    __threadfence();
+    __syncthreads();
+    for (uint32_t w = t; w < N; w += 256) {
+        uint32_t lo = (uint32_t)((uint64_t)w * B / N), hi = (uint32_t)((uint64_t)(w + 1) * B / N);
+        uint32_t a = 0, e = U; // last unit whose first block <= lo
+        while (a + 1 < e) {
+            uint32_t mid = (a + e) >> 1;
+            if (units[mid].block_start <= lo) a = mid; else e = mid;
+        }
+        while (a + 1 < U && units[a].block_start + units[a].nblocks <= lo) a++;
+        wg_desc[w] = make_uint4(a, lo, hi, 0);
     }
 }
 
@@ -133,63 +168,107 @@ struct Chunk {
     float ks[2], vs[2];
 };
 
+// Page ids of a segment live in the lanes of the wave: lane i holds the physical page
+// of logical page base + i, so the chunk loop gets page ids with v_readlane (no memory
+// round trip between consecutive K/V loads; a dependent vector load there would also
+// drain every load issued before it, vmcnt being in order).
+struct PageWindow {
+    uint32_t base;  // first logical page covered (wave-uniform)
+    uint32_t page;  // per lane: physical page of logical page base + lane (0 past the end)
+    float ks, vs;   // per lane: FP8 scales of that page
+};
+
+template <bool FP8>
+__device__ __forceinline__ void window_load(const AttnParams &p, PageWindow &w,
+                                            const uint32_t *table, uint32_t first, uint32_t limit,
+                                            uint32_t hk) {
+    const uint32_t idx = first + lane_id();
+    w.base = first;
+    w.page = idx < limit ? table[idx] : 0u;
+    if constexpr (FP8) {
+        w.ks = idx < limit ? p.k_scales[(size_t)w.page * p.hkv + hk] : 0.0f;
+        w.vs = idx < limit ? p.v_scales[(size_t)w.page * p.hkv + hk] : 0.0f;
+    }
+}
+
+// Loads one 32-token chunk starting at token t (t is a multiple of 32, pages hold >= 16
+// tokens, so each 16-token tile lies in one page) with buffer loads bounded to the live
+// tokens [.., tlim) of the tile's page: rows past tlim read as zeros without touching
+// memory, so the loop issues every load unconditionally (no waitcnt joins) and the V rows
+// of masked tokens are zero.
 template <int D, int KVT>
 __device__ __forceinline__ void load_chunk(const AttnParams &p, Chunk<D, KVT> &c, uint32_t t,
-                                           uint32_t kend, const uint32_t *table, uint32_t hk) {
+                                           const PageWindow &w, uint32_t hk, uint32_t tlim) {
     using C = Cfg<D, KVT>;
     const uint32_t lane = lane_id(), g = lane >> 4, li = lane & 15;
     const uint32_t P = 1u << p.page_shift;
-    const uint8_t *kc = (const uint8_t *)p.kc;
-    const uint8_t *vc = (const uint8_t *)p.vc;
+    const uint32_t row_bytes = p.hkv * D * C::EB; // bytes per slot (all KV heads)
+    const uint32_t head_off = hk * D * C::EB;
+    __amdgpu_buffer_rsrc_t kr[2], vr[2];
 #pragma unroll
     for (int j = 0; j < 2; j++) {
-        uint32_t t0 = t + 16 * j;
-        bool live = t0 < kend;
-        uint32_t page = live ? table[t0 >> p.page_shift] : 0;
+        const uint32_t t0 = t + 16 * j;
+        const uint32_t rel = (t0 >> p.page_shift) - w.base;
+        const uint32_t page = (uint32_t)__builtin_amdgcn_readlane((int)w.page, (int)(rel & 63));
+        const uint32_t pstart = t0 & ~(P - 1);           // first token of the page
+        const uint32_t live = (rel < 64 && tlim > pstart) ? min(tlim - pstart, P) : 0u;
+        const size_t base = (size_t)page * P * row_bytes;
+        kr[j] = make_rsrc((const uint8_t *)p.kc + base, live * row_bytes);
+        vr[j] = make_rsrc((const uint8_t *)p.vc + base, live * row_bytes);
         if constexpr (C::FP8) {
-            c.ks[j] = live ? p.k_scales[(size_t)page * p.hkv + hk] : 0.0f;
-            c.vs[j] = live ? p.v_scales[(size_t)page * p.hkv + hk] : 0.0f;
+            c.ks[j] = __builtin_bit_cast(float, __builtin_amdgcn_readlane(__builtin_bit_cast(int, w.ks), (int)(rel & 63)));
+            c.vs[j] = __builtin_bit_cast(float, __builtin_amdgcn_readlane(__builtin_bit_cast(int, w.vs), (int)(rel & 63)));
         }
-        uint32_t tok = t0 + li;
-        size_t slot = (size_t)page * P + (tok & (P - 1));
-        const u32x4 *src = (const u32x4 *)(kc + ((slot * p.hkv + hk) * D + g * (D / 4)) * C::EB);
+    }
 #pragma unroll
-        for (int s = 0; s < C::KQ; s++) c.k[j][s] = (live && tok < kend) ? src[s] : u32x4{0, 0, 0, 0};
+    for (int j = 0; j < 2; j++) {
+        // instruction s, lane group g reads the 16-byte piece 4s+g of the token's head row:
+        // the four groups of a token cover 64 contiguous bytes per instruction
+        uint32_t off = (((t + 16 * j) & (P - 1)) + li) * row_bytes + head_off + 16 * g;
+#pragma unroll
+        for (int s = 0; s < C::KQ; s++) c.k[j][s] = buffer_load16(kr[j], off + 64 * s);
     }
 #pragma unroll
     for (int s = 0; s < C::NVL; s++) {
         uint32_t item = s * 64 + lane;
         uint32_t tl = item / C::CPT, chunk = item % C::CPT;
-        uint32_t tok = t + tl;
-        bool live = tok < kend;
-        uint32_t page = (t + (tl & 16)) < kend ? table[(t + (tl & 16)) >> p.page_shift] : 0;
-        size_t slot = (size_t)page * P + (tok & (P - 1));
-        const u32x4 *src = (const u32x4 *)(vc + ((slot * p.hkv + hk) * D) * C::EB + chunk * 16);
-        c.v[s] = live ? *src : u32x4{0, 0, 0, 0};
+        constexpr int dummy = 0;
+        (void)dummy;
+        const int tile = (s * 64) / C::CPT / 16; // wave-uniform: one tile per instruction
+        uint32_t off = (((t + 16 * tile) & (P - 1)) + (tl & 15)) * row_bytes + head_off + chunk * 16;
+        c.v[s] = buffer_load16(vr[tile], off);
     }
 }
 
-// Query operand for one 16-column tile: lane (g, col) holds q[col][(D/4)*g .. +D/4) as KS
-// MFMA B-operand quads (the same head_dim permutation the K loads use).
+// Query operand for one 16-column tile: lane (g, col) holds, for MFMA k-step ks, the eight
+// head_dim elements the K loads put in the same k slots: d = 8*(4*ks + g) + j for 16-bit
+// K, d = 16*(4*(ks/2) + g) + 8*(ks%2) + j for FP8 K (a 16-byte FP8 piece spans two k-steps).
+template <int D, int KVT>
+__device__ __forceinline__ uint32_t q_dim(uint32_t ks, uint32_t g) {
+    if constexpr (Cfg<D, KVT>::FP8) return 16 * (4 * (ks / 2) + g) + 8 * (ks % 2);
+    else return 8 * (4 * ks + g);
+}
+
 template <int D, int KVT>
 __device__ __forceinline__ void load_q(const AttnParams &p, u32x4 *qr, uint32_t row, uint32_t head,
                                        bool valid) {
     using C = Cfg<D, KVT>;
     const uint32_t g = lane_id() >> 4;
-    size_t base = ((size_t)row * p.hq + head) * D + g * (D / 4);
+    const size_t base = ((size_t)row * p.hq + head) * D;
 #pragma unroll
     for (int s = 0; s < C::KS; s++) {
+        const size_t at = base + q_dim<D, KVT>(s, g);
         float x[8];
         if (!valid) {
 #pragma unroll
             for (int e = 0; e < 8; e++) x[e] = 0.0f;
         } else if (p.q_f32) {
-            const float4 *src = (const float4 *)((const float *)p.q + base + s * 8);
+            const float4 *src = (const float4 *)((const float *)p.q + at);
             float4 a = src[0], b = src[1];
             x[0] = a.x; x[1] = a.y; x[2] = a.z; x[3] = a.w;
             x[4] = b.x; x[5] = b.y; x[6] = b.z; x[7] = b.w;
         } else {
-            u32x4 w = *(const u32x4 *)((const uint16_t *)p.q + base + s * 8);
+            u32x4 w = *(const u32x4 *)((const uint16_t *)p.q + at);
             if constexpr (C::MBF16) { qr[s] = w; continue; }
 #pragma unroll
             for (int e = 0; e < 4; e++) {
@@ -247,7 +326,7 @@ __device__ __forceinline__ void compute_chunk(const AttnParams &p, const Chunk<D
             for (int ks = 0; ks < C::KS; ks++) {
                 u32x4 a;
                 if constexpr (C::FP8) {
-                    // k-step ks uses bytes 8*ks .. 8*ks+7 of the lane's D/4-byte run
+                    // k-step ks uses half ks%2 of 16-byte load ks/2 (see q_dim)
                     const u32x4 &raw = c.k[j][ks / 2];
                     uint32_t w0 = (ks & 1) ? raw.z : raw.x, w1 = (ks & 1) ? raw.w : raw.y;
                     u32x2 x0 = e4m3x4_to_f16x4_scaled(w0), x1 = e4m3x4_to_f16x4_scaled(w1);
@@ -258,7 +337,10 @@ __device__ __forceinline__ void compute_chunk(const AttnParams &p, const Chunk<D
                 s[j] = mfma16x16x32<C::MBF16>(a, qr[nt][ks], s[j]);
             }
         }
-        // Online softmax for column nt*16 + li over tokens t + 16j + 4g + i.
+        // Online softmax for column nt*16 + li over tokens t + 16j + 4g + i, with a lazily
+        // updated reference maximum: exponentials are taken against m, which is raised
+        // (and O, l rescaled) only when a score exceeds it by more than 2^8.  Numerator and
+        // denominator share the reference, so the normalised result is unchanged.
         float x[2][4];
         float mx = -INFINITY;
 #pragma unroll
@@ -272,10 +354,16 @@ __device__ __forceinline__ void compute_chunk(const AttnParams &p, const Chunk<D
             }
         mx = fmaxf(mx, shfl_xor(mx, 16));
         mx = fmaxf(mx, shfl_xor(mx, 32));
-        float mnew = fmaxf(m[nt], mx);
-        float muse = mnew == -INFINITY ? 0.0f : mnew;
-        float factor = fast_exp2(m[nt] - muse);
-        m[nt] = mnew;
+        const bool first = m[nt] == -INFINITY;
+        const bool raise = !first && mx > m[nt] + 8.0f;
+        if (__builtin_amdgcn_ballot_w64(raise)) { // wave-uniform: rare after the first chunk
+            float factor = raise ? fast_exp2(m[nt] - mx) : 1.0f;
+            l[nt] *= factor;
+#pragma unroll
+            for (int n = 0; n < C::DT; n++) o[nt][n] *= factor;
+        }
+        if (first || raise) m[nt] = mx;
+        const float muse = m[nt] == -INFINITY ? 0.0f : m[nt];
         float pr[2][4];
         float sum = 0.0f;
 #pragma unroll
@@ -286,12 +374,11 @@ __device__ __forceinline__ void compute_chunk(const AttnParams &p, const Chunk<D
                 sum += e;
                 pr[j][i] = e * vscale[j];
             }
-        l[nt] = l[nt] * factor + sum;
+        l[nt] += sum;
         u32x4 pb = u32x4{pack2<C::MBF16>(pr[0][0], pr[0][1]), pack2<C::MBF16>(pr[0][2], pr[0][3]),
                          pack2<C::MBF16>(pr[1][0], pr[1][1]), pack2<C::MBF16>(pr[1][2], pr[1][3])};
 #pragma unroll
         for (int n = 0; n < C::DT; n++) {
-            o[nt][n] *= factor;
             // V^T operand: rows 16n .. 16n+15 of d, k slots = tokens {4g..4g+3, 16+4g..16+4g+3}.
             const uint16_t *r0 = vlds + (4 * g + li / 4) * C::PITCH + 16 * n + 4 * (li & 3);
             const uint16_t *r1 = r0 + 16 * C::PITCH;
@@ -311,33 +398,39 @@ __device__ __forceinline__ uint32_t owner_of(uint32_t blk, uint32_t N, uint32_t 
 }
 
 template <int D, int NT, int KVT>
-__global__ __launch_bounds__(64) void attention_kernel(AttnParams p) {
+struct Smem {
+    static constexpr uint32_t COLS = 16 * NT;
+    static constexpr uint32_t STAGE = kWaves * 32 * Cfg<D, KVT>::PITCH * 2; // V staging bytes
+    static constexpr uint32_t MERGE = kWaves * COLS * (D + 2) * 4;            // merge bytes
+    static constexpr uint32_t BYTES = STAGE > MERGE ? STAGE : MERGE;
+};
+
+template <int D, int NT, int KVT>
+__global__ __launch_bounds__(kThreads) void attention_kernel(AttnParams p) {
     using C = Cfg<D, KVT>;
-    __shared__ __attribute__((aligned(16))) uint16_t vlds[32 * C::PITCH];
-    const uint32_t lane = lane_id(), g = lane >> 4, li = lane & 15;
-    const uint32_t w = blockIdx.x;
-    const uint32_t U = p.header[0], B = p.header[1];
-    const uint32_t N = min(p.n_waves, B);
-    if (w >= N) return;
-    uint32_t lo = (uint32_t)((uint64_t)w * B / N), hi = (uint32_t)((uint64_t)(w + 1) * B / N);
-    // last unit whose first block <= lo
-    uint32_t a = 0, e = U;
-    while (a + 1 < e) {
-        uint32_t mid = (a + e) >> 1;
-        if (p.units[mid].w <= lo) a = mid; else e = mid;
-    }
-    uint32_t u = a;
+    using S = Smem<D, NT, KVT>;
+    constexpr uint32_t COLS = S::COLS;
+    __shared__ __attribute__((aligned(16))) uint8_t smem[S::BYTES];
+    const uint32_t wg = blockIdx.x;
+    const uint32_t N = p.header[2];
+    if (wg >= N) return;
+    const uint32_t tid = threadIdx.x, lane = tid & 63;
+    const uint32_t wave = (uint32_t)__builtin_amdgcn_readfirstlane((int)(tid >> 6)); // uniform: SGPR
+    const uint32_t g = lane >> 4, li = lane & 15;
+    uint16_t *vlds = (uint16_t *)smem + wave * 32 * C::PITCH;
+    const uint4 wd = p.wg_desc[wg];
+    uint32_t u = wd.x, lo = wd.y;
+    const uint32_t hi = wd.z, U = p.header[0];
+
     while (lo < hi && u < U) {
-        uint4 un = p.units[u];
-        uint32_t ustart = un.w, uend = p.units[u + 1].w;
+        const UnitDesc ud = p.units[u];
+        const uint32_t uend = ud.block_start + ud.nblocks;
         if (uend <= lo) { u++; continue; }
-        const uint32_t b = un.x, cb = un.y, hk = un.z;
         const uint32_t seg_end = min(hi, uend);
-        const uint32_t r0 = p.cu[b], nr = p.cu[b + 1] - r0;
-        const uint32_t rowbeg = r0 + cb * p.rpc, nrows = min(p.rpc, nr - cb * p.rpc);
-        const uint32_t *table = p.pages + (size_t)p.sequences[r0] * p.stride;
-        const uint32_t kend = p.positions[rowbeg + nrows - 1] + 1;
-        const uint32_t ncols = nrows * p.group;
+        const uint32_t hk = ud.hk;
+        const uint32_t *table = p.pages + (size_t)ud.table_row * p.stride;
+        const uint32_t kend = ud.kend;
+        const uint32_t ncols = ud.nrows * p.group;
 
         u32x4 qr[NT][C::KS];
         uint32_t lim[NT];
@@ -345,141 +438,207 @@ __global__ __launch_bounds__(64) void attention_kernel(AttnParams p) {
         f32x4 o[NT][C::DT];
 #pragma unroll
         for (int nt = 0; nt < NT; nt++) {
-            uint32_t col = nt * 16 + li;
-            bool valid = col < ncols;
-            uint32_t row = rowbeg + (valid ? col / p.group : 0);
-            uint32_t head = hk * p.group + col % p.group;
-            lim[nt] = valid ? p.positions[row] + 1 : 0;
-            load_q<D, KVT>(p, qr[nt], row, head, valid);
+            const uint32_t col = nt * 16 + li;
+            const bool valid = col < ncols;
+            const uint32_t ri = valid ? col / p.group : 0;
+            lim[nt] = valid ? ud.pos0 + ri + 1 : 0;
+            load_q<D, KVT>(p, qr[nt], ud.rowbeg + ri, hk * p.group + col % p.group, valid);
             m[nt] = -INFINITY;
             l[nt] = 0.0f;
 #pragma unroll
             for (int n = 0; n < C::DT; n++) o[nt][n] = f32x4{0.0f, 0.0f, 0.0f, 0.0f};
         }
 
-        const uint32_t tbeg = (lo - ustart) * 32;
-        const uint32_t tend = min((seg_end - ustart) * 32, kend);
-        Chunk<D, KVT> c0, c1;
-        if (tbeg < tend) load_chunk<D, KVT>(p, c0, tbeg, kend, table, hk);
-        for (uint32_t t = tbeg; t < tend; t += 64) {
-            if (t + 32 < tend) load_chunk<D, KVT>(p, c1, t + 32, kend, table, hk);
-            compute_chunk<D, NT, KVT>(p, c0, t, qr, lim, m, l, o, vlds);
-            if (t + 32 >= tend) break;
-            if (t + 64 < tend) load_chunk<D, KVT>(p, c0, t + 64, kend, table, hk);
-            compute_chunk<D, NT, KVT>(p, c1, t + 32, qr, lim, m, l, o, vlds);
+        const uint32_t tbeg = (lo - ud.block_start) * 32;
+        const uint32_t tend = min((seg_end - ud.block_start) * 32, kend);
+        const uint32_t page_limit = (kend + (1u << p.page_shift) - 1) >> p.page_shift;
+        // Windows of at most 64 pages: each lane holds one page id, so the chunk loop issues
+        // no metadata loads.  Wave k takes chunks k, k + kWaves, ... of each window.
+        for (uint32_t wbeg = tbeg; wbeg < tend;) {
+            const uint32_t wend = min(tend, ((wbeg >> p.page_shift) + 64) << p.page_shift);
+            const uint32_t t0 = wbeg + 32 * wave;
+            if (t0 < wend) {
+                PageWindow win;
+                window_load<C::FP8>(p, win, table, wbeg >> p.page_shift, page_limit, hk);
+                constexpr uint32_t step = 32 * kWaves;
+                Chunk<D, KVT> c0, c1;
+                load_chunk<D, KVT>(p, c0, t0, win, hk, wend);
+                for (uint32_t t = t0;; t += 2 * step) {
+                    load_chunk<D, KVT>(p, c1, t + step, win, hk, wend); // past wend: no traffic
+                    compute_chunk<D, NT, KVT>(p, c0, t, qr, lim, m, l, o, vlds);
+                    if (t + step >= wend) break;
+                    load_chunk<D, KVT>(p, c0, t + 2 * step, win, hk, wend);
+                    compute_chunk<D, NT, KVT>(p, c1, t + step, qr, lim, m, l, o, vlds);
+                    if (t + 2 * step >= wend) break;
+                }
+            }
+            wbeg = wend;
         }
 
-        const bool whole = lo == ustart && seg_end == uend;
-        const uint32_t rec = w + u;
+        // Merge the waves' states through LDS: O^T, reference max and mass per column.
+        float *mo = (float *)smem;                       // [wave][COLS][D]
+        float *mml = mo + kWaves * COLS * D;             // [wave][COLS][2]
+        __syncthreads(); // every wave is done with its V staging
 #pragma unroll
         for (int nt = 0; nt < NT; nt++) {
             float lt = l[nt];
             lt += shfl_xor(lt, 16);
             lt += shfl_xor(lt, 32);
-            uint32_t col = nt * 16 + li;
+            const uint32_t col = nt * 16 + li;
+            float *dst = mo + ((size_t)wave * COLS + col) * D + 4 * g;
+#pragma unroll
+            for (int n = 0; n < C::DT; n++) *(f32x4 *)(dst + 16 * n) = o[nt][n];
+            if (g == 0) {
+                mml[(wave * COLS + col) * 2] = m[nt];
+                mml[(wave * COLS + col) * 2 + 1] = lt;
+            }
+        }
+        __syncthreads();
+        const bool whole = lo == ud.block_start && seg_end == uend;
+        const uint32_t rec = wg + u;
+        for (uint32_t e = tid; e < COLS * D; e += kThreads) {
+            const uint32_t col = e / D, d = e % D;
             if (col >= ncols) continue;
-            uint32_t row = rowbeg + col / p.group;
-            uint32_t head = hk * p.group + col % p.group;
-            if (whole) {
-                float inv = lt > 0.0f ? 1.0f / lt : 0.0f;
-                size_t base = ((size_t)row * p.hq + head) * D + 4 * g;
+            float M = -INFINITY;
 #pragma unroll
-                for (int n = 0; n < C::DT; n++) {
-                    f32x4 v = o[nt][n] * inv;
-                    if (p.out_f32) {
-                        *(f32x4 *)((float *)p.out + base + 16 * n) = v;
-                    } else {
-                        u32x2 h = u32x2{(uint32_t)f32_to_bf16(v.x) | ((uint32_t)f32_to_bf16(v.y) << 16),
-                                        (uint32_t)f32_to_bf16(v.z) | ((uint32_t)f32_to_bf16(v.w) << 16)};
-                        *(u32x2 *)((uint16_t *)p.out + base + 16 * n) = h;
-                    }
+            for (int k = 0; k < kWaves; k++)
+                if (mml[(k * COLS + col) * 2 + 1] > 0.0f) M = fmaxf(M, mml[(k * COLS + col) * 2]);
+            float num = 0.0f, den = 0.0f;
+#pragma unroll
+            for (int k = 0; k < kWaves; k++) {
+                const float mass = mml[(k * COLS + col) * 2 + 1];
+                if (mass > 0.0f) {
+                    const float w = fast_exp2(mml[(k * COLS + col) * 2] - M);
+                    den = fmaf(w, mass, den);
+                    num = fmaf(w, mo[((size_t)k * COLS + col) * D + d], num);
                 }
+            }
+            if (whole) {
+                const uint32_t row = ud.rowbeg + col / p.group;
+                const uint32_t head = hk * p.group + col % p.group;
+                const size_t at = ((size_t)row * p.hq + head) * D + d;
+                const float v = den > 0.0f ? num / den : 0.0f;
+                if (p.out_f32) ((float *)p.out)[at] = v;
+                else ((uint16_t *)p.out)[at] = f32_to_bf16(v);
             } else {
-                size_t rbase = (size_t)rec * (16 * NT) + col;
-                float *po = p.part_o + rbase * D + 4 * g;
-#pragma unroll
-                for (int n = 0; n < C::DT; n++) *(f32x4 *)(po + 16 * n) = o[nt][n];
-                if (g == 0) {
-                    p.part_ml[rbase * 2] = m[nt];
-                    p.part_ml[rbase * 2 + 1] = lt;
+                const size_t rb = (size_t)rec * COLS + col;
+                p.part_o[rb * D + d] = num;
+                if (d == 0) {
+                    p.part_ml[rb * 2] = M;
+                    p.part_ml[rb * 2 + 1] = den;
                 }
             }
         }
+        __syncthreads(); // LDS is reused by the next segment
         lo = seg_end;
         u++;
     }
 }
 
-// Merge the partial records of every unit that was split across waves.  Weights follow
-// the reference merge: a record with zero mass contributes nothing, the others are
-// scaled by 2^(m_r - M) (m in the log2 domain here), out = sum w o / sum w l.
+// Merge the partial records of every unit that was split across workgroups.  Weights
+// follow the reference merge: a record with zero mass contributes nothing, the others
+// are scaled by 2^(m_r - M) (m in the log2 domain here), out = sum w o / sum w l
+// (src/gpu/kernels/llama.rs:201-290).  One workgroup per (unit, column): the record
+// weights are reduced in parallel, then kCombineThreads / D groups of threads each
+// accumulate a strided subset of the records for every head_dim element.
+constexpr uint32_t kCombineThreads = 512;
+constexpr uint32_t kCombineMaxRecords = 4096;
+
 template <int D, int NT>
-__global__ __launch_bounds__(256) void combine_kernel(AttnParams p) {
-    const uint32_t u = blockIdx.x;
-    const uint32_t U = p.header[0], B = p.header[1];
+__global__ __launch_bounds__(kCombineThreads) void combine_kernel(AttnParams p) {
+    __shared__ float wts[kCombineMaxRecords];
+    __shared__ float red[kCombineThreads];
+    const uint32_t u = blockIdx.x, col = blockIdx.y, t = threadIdx.x;
+    const uint32_t U = p.header[0], B = p.header[1], N = p.header[2];
     if (u >= U) return;
-    const uint32_t N = min(p.n_waves, B);
-    uint4 un = p.units[u];
-    uint32_t ustart = un.w, uend = p.units[u + 1].w;
-    if (uend <= ustart) return;
-    uint32_t wf = owner_of(ustart, N, B), wl = owner_of(uend - 1, N, B);
-    if (wf == wl) return; // written directly by its only wave
-    const uint32_t b = un.x, cb = un.y, hk = un.z;
-    const uint32_t r0 = p.cu[b], nr = p.cu[b + 1] - r0;
-    const uint32_t rowbeg = r0 + cb * p.rpc, nrows = min(p.rpc, nr - cb * p.rpc);
-    const uint32_t ncols = nrows * p.group;
+    const UnitDesc ud = p.units[u];
+    if (ud.nblocks == 0) return;
+    const uint32_t wf = owner_of(ud.block_start, N, B);
+    const uint32_t wl = owner_of(ud.block_start + ud.nblocks - 1, N, B);
+    if (wf == wl) return; // written directly by its only workgroup
+    if (col >= ud.nrows * p.group) return;
     constexpr uint32_t COLS = 16 * NT;
-    constexpr uint32_t PER = COLS * D / 256; // outputs per thread
-    for (uint32_t k = 0; k < PER; k++) {
-        uint32_t idx = k * 256 + threadIdx.x;
-        uint32_t col = idx / D, d = idx % D;
-        if (col >= ncols) continue;
-        float M = -INFINITY;
-        for (uint32_t w = wf; w <= wl; w++) {
-            size_t rb = (size_t)(w + u) * COLS + col;
-            if (p.part_ml[rb * 2 + 1] > 0.0f) M = fmaxf(M, p.part_ml[rb * 2]);
-        }
-        float num = 0.0f, den = 0.0f;
-        for (uint32_t w = wf; w <= wl; w++) {
-            size_t rb = (size_t)(w + u) * COLS + col;
-            float mass = p.part_ml[rb * 2 + 1];
-            if (mass > 0.0f) {
-                float wt = fast_exp2(p.part_ml[rb * 2] - M);
-                den = fmaf(wt, mass, den);
-                num = fmaf(wt, p.part_o[rb * D + d], num);
-            }
-        }
-        float v = den > 0.0f ? num / den : 0.0f;
-        uint32_t row = rowbeg + col / p.group, head = hk * p.group + col % p.group;
-        size_t at = ((size_t)row * p.hq + head) * D + d;
-        if (p.out_f32) ((float *)p.out)[at] = v;
-        else ((uint16_t *)p.out)[at] = f32_to_bf16(v);
+    const uint32_t n = wl - wf + 1;
+    const uint32_t rec0 = wf + u;
+    float M = -INFINITY;
+    for (uint32_t r = t; r < n; r += kCombineThreads) {
+        const size_t rb = (size_t)(rec0 + r) * COLS + col;
+        if (p.part_ml[rb * 2 + 1] > 0.0f) M = fmaxf(M, p.part_ml[rb * 2]);
     }
+    red[t] = M;
+    __syncthreads();
+    for (uint32_t off = kCombineThreads / 2; off > 0; off >>= 1) {
+        if (t < off) red[t] = fmaxf(red[t], red[t + off]);
+        __syncthreads();
+    }
+    M = red[0];
+    __syncthreads();
+    float den = 0.0f;
+    for (uint32_t r = t; r < n; r += kCombineThreads) {
+        const size_t rb = (size_t)(rec0 + r) * COLS + col;
+        const float mass = p.part_ml[rb * 2 + 1];
+        const float w = mass > 0.0f ? fast_exp2(p.part_ml[rb * 2] - M) : 0.0f;
+        wts[r] = w;
+        den = fmaf(w, mass, den);
+    }
+    red[t] = den;
+    __syncthreads();
+    for (uint32_t off = kCombineThreads / 2; off > 0; off >>= 1) {
+        if (t < off) red[t] += red[t + off];
+        __syncthreads();
+    }
+    den = red[0];
+    __syncthreads();
+    constexpr uint32_t GROUPS = kCombineThreads / D;
+    const uint32_t d = t % D, grp = t / D;
+    float num = 0.0f;
+    const float *po = p.part_o + ((size_t)rec0 * COLS + col) * D + d;
+    const size_t step = (size_t)COLS * D;
+    uint32_t r = grp;
+    for (; r + 3 * GROUPS < n; r += 4 * GROUPS) {
+        const float a0 = po[(r + 0 * GROUPS) * step], a1 = po[(r + 1 * GROUPS) * step];
+        const float a2 = po[(r + 2 * GROUPS) * step], a3 = po[(r + 3 * GROUPS) * step];
+        num = fmaf(wts[r + 0 * GROUPS], a0, num);
+        num = fmaf(wts[r + 1 * GROUPS], a1, num);
+        num = fmaf(wts[r + 2 * GROUPS], a2, num);
+        num = fmaf(wts[r + 3 * GROUPS], a3, num);
+    }
+    for (; r < n; r += GROUPS) num = fmaf(wts[r], po[r * step], num);
+    red[t] = num;
+    __syncthreads();
+    if (grp != 0) return;
+    for (uint32_t k = 1; k < GROUPS; k++) num += red[k * D + d];
+    const float v = den > 0.0f ? num / den : 0.0f;
+    const uint32_t row = ud.rowbeg + col / p.group, head = ud.hk * p.group + col % p.group;
+    const size_t at = ((size_t)row * p.hq + head) * D + d;
+    if (p.out_f32) ((float *)p.out)[at] = v;
+    else ((uint16_t *)p.out)[at] = f32_to_bf16(v);
 }
 
 // ------------------------------------------------------------------ host side
 
 struct Layout {
-    size_t header, units, part_ml, part_o, total;
+    size_t header, units, wg_desc, part_ml, part_o, total;
     uint32_t max_units, max_records;
 };
 
 static inline uint32_t nt_for(uint32_t n_rows, uint32_t n_seqs, uint32_t group) {
     // Decode-only batches (one row per sequence) use one 16-column tile; batches with
     // multi-row sequences (MTP verify, prefill chunks) use two.
-    return (n_rows > n_seqs && group <= 16) ? 2 : 1;
+    return (n_rows > n_seqs || group > 16) ? 2 : 1;
 }
 
-static Layout layout_for(const lia_attention_config *c, uint32_t n_waves) {
+static Layout layout_for(const lia_attention_config *c, uint32_t n_wg) {
     Layout L;
     uint32_t group = c->num_q_heads / c->num_kv_heads;
-    uint32_t rpc1 = 16 / group ? 16 / group : 1; // smallest rows-per-block over NT choices
-    if (rpc1 == 0) rpc1 = 1;
+    uint32_t rpc1 = group <= 16 ? 16 / group : 1; // smallest rows-per-block over NT choices
     L.max_units = (c->max_rows / rpc1 + c->max_seqs + 1) * c->num_kv_heads;
-    L.max_records = n_waves + L.max_units;
+    L.max_records = n_wg + L.max_units;
     size_t off = 0;
     L.header = off; off += 256;
-    L.units = off; off += ((size_t)L.max_units + 1) * sizeof(uint4);
+    L.units = off; off += ((size_t)L.max_units + 1) * sizeof(UnitDesc);
+    off = (off + 255) & ~(size_t)255;
+    L.wg_desc = off; off += (size_t)n_wg * sizeof(uint4);
     off = (off + 255) & ~(size_t)255;
     L.part_ml = off; off += (size_t)L.max_records * 32 * 2 * sizeof(float);
     off = (off + 255) & ~(size_t)255;
@@ -514,15 +673,18 @@ extern "C" uint32_t lia_device_cus(void) {
     return g_cus;
 }
 
-static uint32_t waves_for_device() {
+// Attention workgroups per launch: one per compute unit (a unit never spans more
+// records than the combine holds).
+static uint32_t workgroups_for_device() {
     uint32_t cus = lia_device_cus();
     if (!cus) cus = 256;
-    return cus * 4;
+    uint32_t n = cus * 1;
+    return n < kCombineMaxRecords ? n : kCombineMaxRecords;
 }
 
 extern "C" size_t lia_attention_workspace_bytes(const lia_attention_config *c) {
     if (!c || !c->num_kv_heads) return 0;
-    return layout_for(c, waves_for_device()).total;
+    return layout_for(c, workgroups_for_device()).total;
 }
 
 static int validate(const lia_attention_config *c) {
@@ -542,15 +704,15 @@ static int validate(const lia_attention_config *c) {
 }
 
 template <int D, int NT, int KVT>
-static void launch_partial(const AttnParams &p, uint32_t n_waves, hipStream_t s) {
-    hipLaunchKernelGGL((attention_kernel<D, NT, KVT>), dim3(n_waves), dim3(64), 0, s, p);
+static void launch_partial(const AttnParams &p, uint32_t n_wg, hipStream_t s) {
+    hipLaunchKernelGGL((attention_kernel<D, NT, KVT>), dim3(n_wg), dim3(kThreads), 0, s, p);
 }
 
 template <int D, int NT>
-static void launch_partial_kv(int kv, const AttnParams &p, uint32_t n_waves, hipStream_t s) {
-    if (kv == LIA_BF16) launch_partial<D, NT, LIA_BF16>(p, n_waves, s);
-    else if (kv == LIA_F16) launch_partial<D, NT, LIA_F16>(p, n_waves, s);
-    else launch_partial<D, NT, LIA_FP8_E4M3>(p, n_waves, s);
+static void launch_partial_kv(int kv, const AttnParams &p, uint32_t n_wg, hipStream_t s) {
+    if (kv == LIA_BF16) launch_partial<D, NT, LIA_BF16>(p, n_wg, s);
+    else if (kv == LIA_F16) launch_partial<D, NT, LIA_F16>(p, n_wg, s);
+    else launch_partial<D, NT, LIA_FP8_E4M3>(p, n_wg, s);
 }
 
 enum Stage { kPlan = 1, kPartial = 2, kMerge = 4 };
@@ -565,60 +727,63 @@ static int run_stages(int stages, const lia_attention_config *c, uint32_t n_seqs
     if (st) return st;
     if (n_seqs == 0 || n_seqs > c->max_seqs || n_rows == 0 || n_rows > c->max_rows) return LIA_E_ARG;
     if (!cu_seqlens || !positions || !workspace) return LIA_E_ARG;
+    if ((stages & kPlan) && !sequences) return LIA_E_ARG;
     if (stages & (kPartial | kMerge)) {
         if (!out) return LIA_E_ARG;
         if ((uintptr_t)out & 15) return LIA_E_ALIGN;
     }
     if (stages & kPartial) {
-        if (!sequences || !pages || !q || !kc || !vc) return LIA_E_ARG;
+        if (!pages || !q || !kc || !vc) return LIA_E_ARG;
         if (c->kv_dtype == LIA_FP8_E4M3 && (!k_scales || !v_scales)) return LIA_E_ARG;
         if (((uintptr_t)q | (uintptr_t)kc | (uintptr_t)vc) & 15) return LIA_E_ALIGN;
     }
-    uint32_t n_waves = waves_for_device();
-    Layout L = layout_for(c, n_waves);
+    const uint32_t n_wg = workgroups_for_device();
+    Layout L = layout_for(c, n_wg);
     if (workspace_bytes < L.total) return LIA_E_WORKSPACE;
     if ((uintptr_t)workspace & 255) return LIA_E_ALIGN;
-    uint32_t group = c->num_q_heads / c->num_kv_heads;
-    uint32_t NT = nt_for(n_rows, n_seqs, group);
-    if (group > 16 * NT) NT = 2;
-    uint32_t rpc = (16 * NT) / group;
+    const uint32_t group = c->num_q_heads / c->num_kv_heads;
+    const uint32_t NT = nt_for(n_rows, n_seqs, group);
+    const uint32_t rpc = (16 * NT) / group;
     uint8_t *ws = (uint8_t *)workspace;
     AttnParams p;
     p.q = q; p.kc = kc; p.vc = vc; p.k_scales = k_scales; p.v_scales = v_scales;
     p.cu = cu_seqlens; p.positions = positions; p.sequences = sequences; p.pages = pages;
     p.out = out;
-    p.units = (const uint4 *)(ws + L.units);
+    p.units = (const UnitDesc *)(ws + L.units);
+    p.wg_desc = (const uint4 *)(ws + L.wg_desc);
     p.header = (const uint32_t *)(ws + L.header);
     p.part_o = (float *)(ws + L.part_o);
     p.part_ml = (float *)(ws + L.part_ml);
     p.hq = c->num_q_heads; p.hkv = c->num_kv_heads; p.group = group; p.stride = c->stride;
     p.page_shift = (uint32_t)__builtin_ctz(c->page_size);
-    p.n_waves = n_waves;
+    p.n_wg = n_wg;
     p.rpc = rpc;
     p.scale_log2 = c->scale * 1.4426950408889634f;
     p.q_f32 = c->q_dtype == LIA_F32;
     p.out_f32 = c->out_dtype == LIA_F32;
     hipStream_t s = (hipStream_t)stream;
     if (stages & kPlan)
-        hipLaunchKernelGGL(plan_kernel, dim3(1), dim3(256), 0, s, n_seqs, cu_seqlens, positions, rpc,
-                           c->num_kv_heads, L.max_units, (uint4 *)(ws + L.units),
+        hipLaunchKernelGGL(plan_kernel, dim3(1), dim3(256), 0, s, n_seqs, cu_seqlens, positions,
+                           sequences, rpc, c->num_kv_heads, L.max_units, n_wg,
+                           (UnitDesc *)(ws + L.units), (uint4 *)(ws + L.wg_desc),
                            (uint32_t *)(ws + L.header));
     if (stages & kPartial) {
         if (c->head_dim == 128) {
-            if (NT == 1) launch_partial_kv<128, 1>(c->kv_dtype, p, n_waves, s);
-            else launch_partial_kv<128, 2>(c->kv_dtype, p, n_waves, s);
+            if (NT == 1) launch_partial_kv<128, 1>(c->kv_dtype, p, n_wg, s);
+            else launch_partial_kv<128, 2>(c->kv_dtype, p, n_wg, s);
         } else {
-            if (NT == 1) launch_partial_kv<64, 1>(c->kv_dtype, p, n_waves, s);
-            else launch_partial_kv<64, 2>(c->kv_dtype, p, n_waves, s);
+            if (NT == 1) launch_partial_kv<64, 1>(c->kv_dtype, p, n_wg, s);
+            else launch_partial_kv<64, 2>(c->kv_dtype, p, n_wg, s);
         }
     }
     if (stages & kMerge) {
+        dim3 grid(L.max_units, 16 * NT);
         if (c->head_dim == 128) {
-            if (NT == 1) hipLaunchKernelGGL((combine_kernel<128, 1>), dim3(L.max_units), dim3(256), 0, s, p);
-            else hipLaunchKernelGGL((combine_kernel<128, 2>), dim3(L.max_units), dim3(256), 0, s, p);
+            if (NT == 1) hipLaunchKernelGGL((combine_kernel<128, 1>), grid, dim3(kCombineThreads), 0, s, p);
+            else hipLaunchKernelGGL((combine_kernel<128, 2>), grid, dim3(kCombineThreads), 0, s, p);
         } else {
-            if (NT == 1) hipLaunchKernelGGL((combine_kernel<64, 1>), dim3(L.max_units), dim3(256), 0, s, p);
-            else hipLaunchKernelGGL((combine_kernel<64, 2>), dim3(L.max_units), dim3(256), 0, s, p);
+            if (NT == 1) hipLaunchKernelGGL((combine_kernel<64, 1>), grid, dim3(kCombineThreads), 0, s, p);
+            else hipLaunchKernelGGL((combine_kernel<64, 2>), grid, dim3(kCombineThreads), 0, s, p);
         }
     }
     return hipGetLastError() == hipSuccess ? LIA_OK : LIA_E_HIP;
@@ -637,27 +802,28 @@ extern "C" int lia_paged_attention(const lia_attention_config *c, uint32_t n_seq
 
 extern "C" int lia_attention_plan(const lia_attention_config *c, uint32_t n_seqs, uint32_t n_rows,
                                   const uint32_t *cu_seqlens, const uint32_t *positions,
-                                  void *workspace, size_t workspace_bytes, lia_stream_t stream) {
-    return run_stages(kPlan, c, n_seqs, n_rows, cu_seqlens, positions, nullptr, nullptr, nullptr,
-                      nullptr, nullptr, nullptr, nullptr, workspace, workspace_bytes, nullptr,
-                      stream);
+                                  const uint32_t *sequences, void *workspace,
+                                  size_t workspace_bytes, lia_stream_t stream) {
+    return run_stages(kPlan, c, n_seqs, n_rows, cu_seqlens, positions, sequences, nullptr,
+                      nullptr, nullptr, nullptr, nullptr, nullptr, workspace, workspace_bytes,
+                      nullptr, stream);
 }
 
 extern "C" int lia_attention_partial(const lia_attention_config *c, uint32_t n_seqs,
-                                     uint32_t n_rows, const uint32_t *cu_seqlens,
-                                     const uint32_t *positions, const uint32_t *sequences,
-                                     const uint32_t *pages, const void *q, const void *kc,
-                                     const void *vc, const float *k_scales, const float *v_scales,
-                                     void *workspace, size_t workspace_bytes, void *out,
-                                     lia_stream_t stream) {
-    return run_stages(kPartial, c, n_seqs, n_rows, cu_seqlens, positions, sequences, pages, q, kc,
-                      vc, k_scales, v_scales, workspace, workspace_bytes, out, stream);
+                                     uint32_t n_rows, const uint32_t *pages, const void *q,
+                                     const void *kc, const void *vc, const float *k_scales,
+                                     const float *v_scales, void *workspace,
+                                     size_t workspace_bytes, void *out, lia_stream_t stream) {
+    // the plan carries the per-row metadata; cu_seqlens / positions are not re-read
+    static const uint32_t dummy = 0;
+    return run_stages(kPartial, c, n_seqs, n_rows, &dummy, &dummy, nullptr, pages, q, kc, vc,
+                      k_scales, v_scales, workspace, workspace_bytes, out, stream);
 }
 
 extern "C" int lia_attention_merge(const lia_attention_config *c, uint32_t n_seqs, uint32_t n_rows,
-                                   const uint32_t *cu_seqlens, const uint32_t *positions,
                                    void *workspace, size_t workspace_bytes, void *out,
                                    lia_stream_t stream) {
-    return run_stages(kMerge, c, n_seqs, n_rows, cu_seqlens, positions, nullptr, nullptr, nullptr,
+    static const uint32_t dummy = 0;
+    return run_stages(kMerge, c, n_seqs, n_rows, &dummy, &dummy, nullptr, nullptr, nullptr,
                       nullptr, nullptr, nullptr, nullptr, workspace, workspace_bytes, out, stream);
 }

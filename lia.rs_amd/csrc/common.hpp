@@ -120,15 +120,33 @@ __device__ __forceinline__ f32x4 mfma16x16x32(u32x4 a, u32x4 b, f32x4 c) {
                                                       __builtin_bit_cast(f16x8, b), c, 0, 0, 0);
 }
 
+// Hot-path packing of two floats into an MFMA operand word with the hardware
+// round-to-nearest-even converts (v_cvt_pk_bf16_f32 / v_cvt_f16_f32).
+typedef __attribute__((ext_vector_type(2))) __bf16 bf16x2;
+typedef __attribute__((ext_vector_type(2))) _Float16 f16x2;
 template <bool BF16>
 __device__ __forceinline__ uint32_t pack2(float a, float b) {
-    if constexpr (BF16)
-        return (uint32_t)f32_to_bf16(a) | ((uint32_t)f32_to_bf16(b) << 16);
-    else
-        return (uint32_t)__builtin_bit_cast(uint16_t, (_Float16)a) |
-               ((uint32_t)__builtin_bit_cast(uint16_t, (_Float16)b) << 16);
+    if constexpr (BF16) {
+        bf16x2 r = {(__bf16)a, (__bf16)b};
+        return __builtin_bit_cast(uint32_t, r);
+    } else {
+        f16x2 r = {(_Float16)a, (_Float16)b};
+        return __builtin_bit_cast(uint32_t, r);
+    }
 }
 
 __device__ __forceinline__ float fast_exp2(float x) { return __builtin_amdgcn_exp2f(x); }
+
+// Raw buffer resource over [base, base + bytes): loads at or past `bytes` return zeros and
+// touch no memory, which lets a loop issue every load unconditionally.
+constexpr int kBufferConfig = 0x00020000; // gfx9 raw buffer, 32-bit data format
+__device__ __forceinline__ __amdgpu_buffer_rsrc_t make_rsrc(const void *base, uint32_t bytes) {
+    return __builtin_amdgcn_make_buffer_rsrc(const_cast<void *>(base), (short)0, (int)bytes,
+                                             kBufferConfig);
+}
+
+__device__ __forceinline__ u32x4 buffer_load16(__amdgpu_buffer_rsrc_t r, uint32_t voffset) {
+    return __builtin_bit_cast(u32x4, __builtin_amdgcn_raw_buffer_load_b128(r, (int)voffset, 0, 0));
+}
 
 } // namespace lia
