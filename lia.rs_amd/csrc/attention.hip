@@ -25,8 +25,6 @@
 
 namespace lia {
 
-constexpr int kWaves = 4;                         // wavefronts per attention workgroup
-constexpr uint32_t kThreads = kWaves * 64;
 
 // Unit descriptor written by the plan kernel (32 bytes).
 struct UnitDesc {
@@ -147,31 +145,42 @@ __global__ __launch_bounds__(256) void plan_kernel(uint32_t n_seqs, const uint32
 }
 
 // ------------------------------------------------------------------ the attention kernel
+//
+// A workgroup has D/32 wavefronts; wave w owns head_dim slice [32w, 32w+32).  Every wave
+// walks every 32-token chunk of the workgroup's block range: it loads its 32-dim slice of
+// K (registers, MFMA A operand) and V (direct-to-LDS), computes its partial S^T = K_w Q_w^T
+// with one MFMA per 16-token tile, and the partial scores are summed across the waves
+// through LDS (one barrier per chunk).  Each wave then runs the same online softmax on the
+// same scores and accumulates O^T for its own d slice.  Work inside a workgroup is
+// therefore split evenly whatever the segment lengths, and no end-of-segment merge is
+// needed: each wave writes its own slice of the output or of the split record.
 
 template <int D, int KVT>
 struct Cfg {
     static constexpr bool FP8 = KVT == LIA_FP8_E4M3;
-    static constexpr bool MBF16 = KVT == LIA_BF16;        // MFMA operand type
-    static constexpr int EB = FP8 ? 1 : 2;                // bytes per stored KV element
-    static constexpr int KS = D / 32;                     // MFMA k-steps over head_dim
-    static constexpr int DT = D / 16;                     // 16-wide d tiles of the output
-    static constexpr int KQ = D * EB / 4 / 16;            // 16-byte K loads per lane per tile
-    static constexpr int CPT = D * EB / 16;               // 16-byte V chunks per token
-    static constexpr int NVL = 32 * CPT / 64;             // 16-byte V loads per lane
-    static constexpr int PITCH = D + 16;                  // LDS row pitch (16-bit elements)
+    static constexpr bool MBF16 = KVT == LIA_BF16;  // MFMA operand type (f16 for f16 and FP8)
+    static constexpr int EB = FP8 ? 1 : 2;          // bytes per stored KV element
+    static constexpr int WAVES = D / 32;            // one wave per 32-dim slice
+    static constexpr int THREADS = WAVES * 64;
+    static constexpr int SLICE = 32 * EB;           // bytes of one token's slice (one head)
+    static constexpr int STAGE = 32 * 32;           // staged V per wave: [32 tokens][32] 16-bit
 };
+
+// Staged V rows hold 32 16-bit values (4 chunks of 16 bytes); chunk c of row r sits in
+// slot c ^ swz(r), which keeps the transpose reads of a 16-lane group (rows 4q..4q+3,
+// chunks {2n, 2n+1}) on distinct banks.
+__device__ __forceinline__ uint32_t swz(uint32_t row) { return 2 * ((row >> 1) & 1); }
 
 template <int D, int KVT>
 struct Chunk {
-    u32x4 k[2][Cfg<D, KVT>::KQ];
-    u32x4 v[Cfg<D, KVT>::NVL];
+    uint32_t k[2][Cfg<D, KVT>::FP8 ? 2 : 4]; // A operand words of the two 16-token tiles
+    u32x4 v;                                   // FP8 only: the wave's V slice, staged later
     float ks[2], vs[2];
 };
 
-// Page ids of a segment live in the lanes of the wave: lane i holds the physical page
-// of logical page base + i, so the chunk loop gets page ids with v_readlane (no memory
-// round trip between consecutive K/V loads; a dependent vector load there would also
-// drain every load issued before it, vmcnt being in order).
+// Page ids of a segment live in the lanes of the wave: lane i holds the physical page of
+// logical page base + i, so the chunk loop gets page ids with v_readlane and issues no
+// metadata loads.
 struct PageWindow {
     uint32_t base;  // first logical page covered (wave-uniform)
     uint32_t page;  // per lane: physical page of logical page base + lane (0 past the end)
@@ -191,121 +200,160 @@ __device__ __forceinline__ void window_load(const AttnParams &p, PageWindow &w,
     }
 }
 
-// Loads one 32-token chunk starting at token t (t is a multiple of 32, pages hold >= 16
-// tokens, so each 16-token tile lies in one page) with buffer loads bounded to the live
+// Wait until at most `n` vector-memory operations of this wave are outstanding.
+template <int n>
+__device__ __forceinline__ void wait_vmcnt() {
+    static_assert(n >= 0 && n < 64, "vmcnt range");
+    __builtin_amdgcn_s_waitcnt((n & 0xF) | ((n >> 4) << 14) | (0x7 << 4) | (0xF << 8));
+}
+
+// Vector-memory operations one load_chunk issues (the pipeline waits on this count).
+template <int D, int KVT>
+constexpr int kLoadsPerChunk = 4; // two K loads + two V loads
+
+// Loads chunk t (32 tokens, t a multiple of 32; pages hold >= 16 tokens so each 16-token
+// tile lies in one page) of this wave's d slice.  Buffer loads are bounded to the live
 // tokens [.., tlim) of the tile's page: rows past tlim read as zeros without touching
-// memory, so the loop issues every load unconditionally (no waitcnt joins) and the V rows
-// of masked tokens are zero.
+// memory, so every load is issued unconditionally and masked V rows are zero.
 template <int D, int KVT>
 __device__ __forceinline__ void load_chunk(const AttnParams &p, Chunk<D, KVT> &c, uint32_t t,
-                                           const PageWindow &w, uint32_t hk, uint32_t tlim) {
+                                           const PageWindow &w, uint32_t hk, uint32_t tlim,
+                                           uint32_t wave, uint16_t *stage) {
     using C = Cfg<D, KVT>;
     const uint32_t lane = lane_id(), g = lane >> 4, li = lane & 15;
     const uint32_t P = 1u << p.page_shift;
     const uint32_t row_bytes = p.hkv * D * C::EB; // bytes per slot (all KV heads)
-    const uint32_t head_off = hk * D * C::EB;
-    __amdgpu_buffer_rsrc_t kr[2], vr[2];
+    const uint32_t slice_off = (hk * D + 32 * wave) * C::EB;
+    __amdgpu_buffer_rsrc_t r[2];
 #pragma unroll
     for (int j = 0; j < 2; j++) {
         const uint32_t t0 = t + 16 * j;
         const uint32_t rel = (t0 >> p.page_shift) - w.base;
         const uint32_t page = (uint32_t)__builtin_amdgcn_readlane((int)w.page, (int)(rel & 63));
-        const uint32_t pstart = t0 & ~(P - 1);           // first token of the page
+        const uint32_t pstart = t0 & ~(P - 1);
         const uint32_t live = (rel < 64 && tlim > pstart) ? min(tlim - pstart, P) : 0u;
         const size_t base = (size_t)page * P * row_bytes;
-        kr[j] = make_rsrc((const uint8_t *)p.kc + base, live * row_bytes);
-        vr[j] = make_rsrc((const uint8_t *)p.vc + base, live * row_bytes);
+        r[j] = make_rsrc((const uint8_t *)p.kc + base, live * row_bytes);
         if constexpr (C::FP8) {
             c.ks[j] = __builtin_bit_cast(float, __builtin_amdgcn_readlane(__builtin_bit_cast(int, w.ks), (int)(rel & 63)));
             c.vs[j] = __builtin_bit_cast(float, __builtin_amdgcn_readlane(__builtin_bit_cast(int, w.vs), (int)(rel & 63)));
         }
     }
+    // K: lane (g, li) of tile j reads token 16j+li, dims 32w + 8g .. +7 (the four groups
+    // of a token cover its 32-dim slice contiguously).
 #pragma unroll
     for (int j = 0; j < 2; j++) {
-        // instruction s, lane group g reads the 16-byte piece 4s+g of the token's head row:
-        // the four groups of a token cover 64 contiguous bytes per instruction
-        uint32_t off = (((t + 16 * j) & (P - 1)) + li) * row_bytes + head_off + 16 * g;
-#pragma unroll
-        for (int s = 0; s < C::KQ; s++) c.k[j][s] = buffer_load16(kr[j], off + 64 * s);
+        const uint32_t off = (((t + 16 * j) & (P - 1)) + li) * row_bytes + slice_off + 8 * g * C::EB;
+        if constexpr (C::FP8) {
+            auto x = __builtin_amdgcn_raw_buffer_load_b64(r[j], (int)off, 0, 0);
+            c.k[j][0] = x[0];
+            c.k[j][1] = x[1];
+        } else {
+            u32x4 x = buffer_load16(r[j], off);
+            c.k[j][0] = x.x; c.k[j][1] = x.y; c.k[j][2] = x.z; c.k[j][3] = x.w;
+        }
     }
+    if constexpr (C::FP8) {
+        // V slice (32 bytes per token) into registers: lane l reads token l/2, bytes
+        // 16*(l%2) .. +16, through a descriptor over the V plane bounded like K's.
+        const uint32_t tok = lane >> 1;
+        __amdgpu_buffer_rsrc_t vr[2];
 #pragma unroll
-    for (int s = 0; s < C::NVL; s++) {
-        uint32_t item = s * 64 + lane;
-        uint32_t tl = item / C::CPT, chunk = item % C::CPT;
-        constexpr int dummy = 0;
-        (void)dummy;
-        const int tile = (s * 64) / C::CPT / 16; // wave-uniform: one tile per instruction
-        uint32_t off = (((t + 16 * tile) & (P - 1)) + (tl & 15)) * row_bytes + head_off + chunk * 16;
-        c.v[s] = buffer_load16(vr[tile], off);
+        for (int jj = 0; jj < 2; jj++) {
+            const uint32_t t0 = t + 16 * jj;
+            const uint32_t rel = (t0 >> p.page_shift) - w.base;
+            const uint32_t page = (uint32_t)__builtin_amdgcn_readlane((int)w.page, (int)(rel & 63));
+            const uint32_t pstart = t0 & ~(P - 1);
+            const uint32_t live = (rel < 64 && tlim > pstart) ? min(tlim - pstart, P) : 0u;
+            vr[jj] = make_rsrc((const uint8_t *)p.vc + (size_t)page * P * row_bytes, live * row_bytes);
+        }
+        const uint32_t off = (((t + 16 * (tok >> 4)) & (P - 1)) + (tok & 15)) * row_bytes + slice_off +
+                             16 * (lane & 1);
+        // lanes 0-31 read tile 0, lanes 32-63 tile 1: two loads, each with half the lanes live
+        const u32x4 a = buffer_load16(vr[0], tok < 16 ? off : 0xFFFFFFF0u);
+        const u32x4 b = buffer_load16(vr[1], tok >= 16 ? off : 0xFFFFFFF0u);
+        c.v = tok < 16 ? a : b;
+    } else {
+        // V slice goes straight to this wave's LDS stage: instruction s fills rows
+        // 16s .. 16s+15, lane l writes slot l%4 of row 16s + l/4 with the swizzled chunk.
+        __builtin_amdgcn_s_waitcnt(0xC07F); // lgkmcnt(0): earlier reads of this stage are done
+#pragma unroll
+        for (int s = 0; s < 2; s++) {
+            const uint32_t t0 = t + 16 * s;
+            const uint32_t rel = (t0 >> p.page_shift) - w.base;
+            const uint32_t page = (uint32_t)__builtin_amdgcn_readlane((int)w.page, (int)(rel & 63));
+            const uint32_t pstart = t0 & ~(P - 1);
+            const uint32_t live = (rel < 64 && tlim > pstart) ? min(tlim - pstart, P) : 0u;
+            const __amdgpu_buffer_rsrc_t vr =
+                make_rsrc((const uint8_t *)p.vc + (size_t)page * P * row_bytes, live * row_bytes);
+            const uint32_t row = 16 * s + (lane >> 2);
+            const uint32_t chunk = (lane & 3) ^ swz(row);
+            const uint32_t off = ((t0 & (P - 1)) + (row & 15)) * row_bytes + slice_off + 16 * chunk;
+            __builtin_amdgcn_raw_ptr_buffer_load_lds(
+                vr, (__attribute__((address_space(3))) void *)(stage + s * 512), 16, off, 0, 0, 0);
+        }
     }
+    __builtin_amdgcn_sched_barrier(0);
 }
 
-// Query operand for one 16-column tile: lane (g, col) holds, for MFMA k-step ks, the eight
-// head_dim elements the K loads put in the same k slots: d = 8*(4*ks + g) + j for 16-bit
-// K, d = 16*(4*(ks/2) + g) + 8*(ks%2) + j for FP8 K (a 16-byte FP8 piece spans two k-steps).
+// Query operand of one 16-column tile for this wave's d slice: lane (g, col) holds
+// q[col][32w + 8g .. +7] - the dims the K loads put in the same k slots.
 template <int D, int KVT>
-__device__ __forceinline__ uint32_t q_dim(uint32_t ks, uint32_t g) {
-    if constexpr (Cfg<D, KVT>::FP8) return 16 * (4 * (ks / 2) + g) + 8 * (ks % 2);
-    else return 8 * (4 * ks + g);
-}
-
-template <int D, int KVT>
-__device__ __forceinline__ void load_q(const AttnParams &p, u32x4 *qr, uint32_t row, uint32_t head,
-                                       bool valid) {
+__device__ __forceinline__ u32x4 load_q(const AttnParams &p, uint32_t row, uint32_t head,
+                                        bool valid, uint32_t wave) {
     using C = Cfg<D, KVT>;
     const uint32_t g = lane_id() >> 4;
-    const size_t base = ((size_t)row * p.hq + head) * D;
+    const size_t at = ((size_t)row * p.hq + head) * D + 32 * wave + 8 * g;
+    float x[8];
+    if (!valid) {
 #pragma unroll
-    for (int s = 0; s < C::KS; s++) {
-        const size_t at = base + q_dim<D, KVT>(s, g);
-        float x[8];
-        if (!valid) {
+        for (int e = 0; e < 8; e++) x[e] = 0.0f;
+    } else if (p.q_f32) {
+        const float4 *src = (const float4 *)((const float *)p.q + at);
+        float4 a = src[0], b = src[1];
+        x[0] = a.x; x[1] = a.y; x[2] = a.z; x[3] = a.w;
+        x[4] = b.x; x[5] = b.y; x[6] = b.z; x[7] = b.w;
+    } else {
+        u32x4 w = *(const u32x4 *)((const uint16_t *)p.q + at);
+        if constexpr (C::MBF16) return w;
 #pragma unroll
-            for (int e = 0; e < 8; e++) x[e] = 0.0f;
-        } else if (p.q_f32) {
-            const float4 *src = (const float4 *)((const float *)p.q + at);
-            float4 a = src[0], b = src[1];
-            x[0] = a.x; x[1] = a.y; x[2] = a.z; x[3] = a.w;
-            x[4] = b.x; x[5] = b.y; x[6] = b.z; x[7] = b.w;
-        } else {
-            u32x4 w = *(const u32x4 *)((const uint16_t *)p.q + at);
-            if constexpr (C::MBF16) { qr[s] = w; continue; }
-#pragma unroll
-            for (int e = 0; e < 4; e++) {
-                x[2 * e] = bf16_to_f32(w[e] & 0xffffu);
-                x[2 * e + 1] = bf16_to_f32(w[e] >> 16);
-            }
+        for (int e = 0; e < 4; e++) {
+            x[2 * e] = bf16_to_f32(w[e] & 0xffffu);
+            x[2 * e + 1] = bf16_to_f32(w[e] >> 16);
         }
-        qr[s] = u32x4{pack2<C::MBF16>(x[0], x[1]), pack2<C::MBF16>(x[2], x[3]),
-                      pack2<C::MBF16>(x[4], x[5]), pack2<C::MBF16>(x[6], x[7])};
     }
+    return u32x4{pack2<C::MBF16>(x[0], x[1]), pack2<C::MBF16>(x[2], x[3]),
+                 pack2<C::MBF16>(x[4], x[5]), pack2<C::MBF16>(x[6], x[7])};
 }
 
 template <int D, int NT, int KVT>
+struct State {
+    u32x4 qr[NT];
+    uint32_t lim[NT];
+    float m[NT], l[NT];
+    f32x4 o[NT][2];
+};
+
+// One chunk: partial scores for this wave's d slice, cross-wave sum through LDS, online
+// softmax (identical in every wave), O^T += V^T P^T for the wave's two 16-dim tiles.
+template <int D, int NT, int KVT>
 __device__ __forceinline__ void compute_chunk(const AttnParams &p, const Chunk<D, KVT> &c,
-                                              uint32_t t, const u32x4 (&qr)[NT][Cfg<D, KVT>::KS],
-                                              const uint32_t (&lim)[NT], float (&m)[NT],
-                                              float (&l)[NT], f32x4 (&o)[NT][Cfg<D, KVT>::DT],
-                                              uint16_t *vlds) {
+                                              uint32_t t, State<D, NT, KVT> &st,
+                                              uint16_t *stage, f32x4 *sx, uint32_t wave) {
     using C = Cfg<D, KVT>;
     const uint32_t lane = lane_id(), g = lane >> 4, li = lane & 15;
-
-    // Stage V (natural [token][d] layout) into LDS while the scores are computed.
-#pragma unroll
-    for (int s = 0; s < C::NVL; s++) {
-        uint32_t item = s * 64 + lane;
-        uint32_t tl = item / C::CPT, chunk = item % C::CPT;
-        if constexpr (C::FP8) {
-            u32x2 lo0 = e4m3x4_to_f16x4_scaled(c.v[s].x), lo1 = e4m3x4_to_f16x4_scaled(c.v[s].y);
-            u32x2 hi0 = e4m3x4_to_f16x4_scaled(c.v[s].z), hi1 = e4m3x4_to_f16x4_scaled(c.v[s].w);
-            u32x4 *dst = (u32x4 *)(vlds + tl * C::PITCH + chunk * 16);
-            dst[0] = u32x4{lo0.x, lo0.y, lo1.x, lo1.y};
-            dst[1] = u32x4{hi0.x, hi0.y, hi1.x, hi1.y};
-        } else {
-            *(u32x4 *)(vlds + tl * C::PITCH + chunk * 8) = c.v[s];
-        }
+    if constexpr (C::FP8) {
+        // convert the wave's FP8 V slice (16 values per lane) to f16 and stage it swizzled
+        const uint32_t row = lane >> 1;
+        u32x2 a = e4m3x4_to_f16x4_scaled(c.v.x), b = e4m3x4_to_f16x4_scaled(c.v.y);
+        u32x2 e = e4m3x4_to_f16x4_scaled(c.v.z), f = e4m3x4_to_f16x4_scaled(c.v.w);
+        uint16_t *dst = stage + row * 32;
+        const uint32_t c0 = 2 * (lane & 1);
+        *(u32x4 *)(dst + ((c0 ^ swz(row)) * 8)) = u32x4{a.x, a.y, b.x, b.y};
+        *(u32x4 *)(dst + (((c0 + 1) ^ swz(row)) * 8)) = u32x4{e.x, e.y, f.x, f.y};
+    } else {
+        wait_vmcnt<kLoadsPerChunk<D, KVT>>(); // this chunk's V is in LDS
     }
-
     float kscale[2] = {p.scale_log2, p.scale_log2};
     float vscale[2] = {1.0f, 1.0f};
     if constexpr (C::FP8) {
@@ -315,82 +363,104 @@ __device__ __forceinline__ void compute_chunk(const AttnParams &p, const Chunk<D
             vscale[j] = c.vs[j] * 256.0f;
         }
     }
-
+    // partial scores of this wave's slice -> LDS
+#pragma unroll
+    for (int nt = 0; nt < NT; nt++) {
+#pragma unroll
+        for (int j = 0; j < 2; j++) {
+            u32x4 a;
+            if constexpr (C::FP8) {
+                u32x2 x0 = e4m3x4_to_f16x4_scaled(c.k[j][0]), x1 = e4m3x4_to_f16x4_scaled(c.k[j][1]);
+                a = u32x4{x0.x, x0.y, x1.x, x1.y};
+            } else {
+                a = u32x4{c.k[j][0], c.k[j][1], c.k[j][2], c.k[j][3]};
+            }
+            f32x4 sp = mfma16x16x32<C::MBF16>(a, st.qr[nt], f32x4{0.0f, 0.0f, 0.0f, 0.0f});
+            sx[((wave * NT + nt) * 2 + j) * 64 + lane] = sp;
+        }
+    }
+    // Only the LDS score exchange needs ordering: wait for this wave's LDS writes and meet
+    // at a bare barrier (a full __syncthreads fence would also drain the prefetch loads).
+    __builtin_amdgcn_s_waitcnt(0xC07F); // lgkmcnt(0)
+    __builtin_amdgcn_s_barrier();
 #pragma unroll
     for (int nt = 0; nt < NT; nt++) {
         f32x4 s[2];
 #pragma unroll
         for (int j = 0; j < 2; j++) {
-            s[j] = f32x4{0.0f, 0.0f, 0.0f, 0.0f};
+            s[j] = sx[((0 * NT + nt) * 2 + j) * 64 + lane];
 #pragma unroll
-            for (int ks = 0; ks < C::KS; ks++) {
-                u32x4 a;
-                if constexpr (C::FP8) {
-                    // k-step ks uses half ks%2 of 16-byte load ks/2 (see q_dim)
-                    const u32x4 &raw = c.k[j][ks / 2];
-                    uint32_t w0 = (ks & 1) ? raw.z : raw.x, w1 = (ks & 1) ? raw.w : raw.y;
-                    u32x2 x0 = e4m3x4_to_f16x4_scaled(w0), x1 = e4m3x4_to_f16x4_scaled(w1);
-                    a = u32x4{x0.x, x0.y, x1.x, x1.y};
-                } else {
-                    a = c.k[j][ks];
-                }
-                s[j] = mfma16x16x32<C::MBF16>(a, qr[nt][ks], s[j]);
-            }
+            for (int w = 1; w < C::WAVES; w++) s[j] += sx[((w * NT + nt) * 2 + j) * 64 + lane];
         }
         // Online softmax for column nt*16 + li over tokens t + 16j + 4g + i, with a lazily
         // updated reference maximum: exponentials are taken against m, which is raised
-        // (and O, l rescaled) only when a score exceeds it by more than 2^8.  Numerator and
-        // denominator share the reference, so the normalised result is unchanged.
+        // (and O, l rescaled) only when a score exceeds it by more than 2^8.  Numerator
+        // and denominator share the reference, so the normalised result is unchanged.
         float x[2][4];
         float mx = -INFINITY;
 #pragma unroll
         for (int j = 0; j < 2; j++)
 #pragma unroll
             for (int i = 0; i < 4; i++) {
-                uint32_t tok = t + 16 * j + 4 * g + i;
-                float v = tok < lim[nt] ? s[j][i] * kscale[j] : -INFINITY;
+                const uint32_t tok = t + 16 * j + 4 * g + i;
+                const float v = tok < st.lim[nt] ? s[j][i] * kscale[j] : -INFINITY;
                 x[j][i] = v;
                 mx = fmaxf(mx, v);
             }
         mx = fmaxf(mx, shfl_xor(mx, 16));
         mx = fmaxf(mx, shfl_xor(mx, 32));
-        const bool first = m[nt] == -INFINITY;
-        const bool raise = !first && mx > m[nt] + 8.0f;
+        const bool first = st.m[nt] == -INFINITY;
+        const bool raise = !first && mx > st.m[nt] + 8.0f;
         if (__builtin_amdgcn_ballot_w64(raise)) { // wave-uniform: rare after the first chunk
-            float factor = raise ? fast_exp2(m[nt] - mx) : 1.0f;
-            l[nt] *= factor;
-#pragma unroll
-            for (int n = 0; n < C::DT; n++) o[nt][n] *= factor;
+            const float factor = raise ? fast_exp2(st.m[nt] - mx) : 1.0f;
+            st.l[nt] *= factor;
+            st.o[nt][0] *= factor;
+            st.o[nt][1] *= factor;
         }
-        if (first || raise) m[nt] = mx;
-        const float muse = m[nt] == -INFINITY ? 0.0f : m[nt];
+        if (first || raise) st.m[nt] = mx;
+        const float muse = st.m[nt] == -INFINITY ? 0.0f : st.m[nt];
         float pr[2][4];
         float sum = 0.0f;
 #pragma unroll
         for (int j = 0; j < 2; j++)
 #pragma unroll
             for (int i = 0; i < 4; i++) {
-                float e = fast_exp2(x[j][i] - muse);
+                const float e = fast_exp2(x[j][i] - muse);
                 sum += e;
                 pr[j][i] = e * vscale[j];
             }
-        l[nt] += sum;
-        u32x4 pb = u32x4{pack2<C::MBF16>(pr[0][0], pr[0][1]), pack2<C::MBF16>(pr[0][2], pr[0][3]),
-                         pack2<C::MBF16>(pr[1][0], pr[1][1]), pack2<C::MBF16>(pr[1][2], pr[1][3])};
+        st.l[nt] += sum;
+        const u32x4 pb = u32x4{pack2<C::MBF16>(pr[0][0], pr[0][1]), pack2<C::MBF16>(pr[0][2], pr[0][3]),
+                               pack2<C::MBF16>(pr[1][0], pr[1][1]), pack2<C::MBF16>(pr[1][2], pr[1][3])};
 #pragma unroll
-        for (int n = 0; n < C::DT; n++) {
-            // V^T operand: rows 16n .. 16n+15 of d, k slots = tokens {4g..4g+3, 16+4g..16+4g+3}.
-            const uint16_t *r0 = vlds + (4 * g + li / 4) * C::PITCH + 16 * n + 4 * (li & 3);
-            const uint16_t *r1 = r0 + 16 * C::PITCH;
+        for (int n = 0; n < 2; n++) {
+            // V^T operand: d rows 16n .. 16n+15 of the slice, k slots = tokens
+            // {4g..4g+3, 16+4g..16+4g+3} (transpose reads of the staged rows).
+            const uint32_t row0 = 4 * g + li / 4, ch = 2 * n + ((li & 3) >> 1);
+            const uint16_t *r0 = stage + row0 * 32 + ((ch ^ swz(row0)) * 8) + (li & 1) * 4;
+            const uint16_t *r1 = r0 + 16 * 32; // row0 + 16 has the same swizzle
             s16x4 a0 = __builtin_amdgcn_ds_read_tr16_b64_v4i16(
                 (__attribute__((address_space(3))) s16x4 *)(r0));
             s16x4 a1 = __builtin_amdgcn_ds_read_tr16_b64_v4i16(
                 (__attribute__((address_space(3))) s16x4 *)(r1));
             u32x2 b0 = __builtin_bit_cast(u32x2, a0), b1 = __builtin_bit_cast(u32x2, a1);
-            u32x4 av = u32x4{b0.x, b0.y, b1.x, b1.y};
-            o[nt][n] = mfma16x16x32<C::MBF16>(av, pb, o[nt][n]);
+            st.o[nt][n] = mfma16x16x32<C::MBF16>(u32x4{b0.x, b0.y, b1.x, b1.y}, pb, st.o[nt][n]);
         }
     }
+}
+
+// One pipeline step: issue the loads of chunk `tn` into stage `sn` (registers cn), then
+// compute chunk `tc` from stage `sc` (registers cc).  The two stages are restrict
+// parameters: the transpose reads of `sc` are then known not to alias the direct-to-LDS
+// loads still in flight into `sn`, so no full vmcnt drain is needed before them.
+template <int D, int NT, int KVT>
+__device__ __forceinline__ void pipeline_step(const AttnParams &p, Chunk<D, KVT> &cn, uint32_t tn,
+                                              uint16_t *__restrict__ sn, const Chunk<D, KVT> &cc,
+                                              uint32_t tc, uint16_t *__restrict__ sc,
+                                              const PageWindow &win, uint32_t hk, uint32_t tlim,
+                                              uint32_t wave, State<D, NT, KVT> &st, f32x4 *sx) {
+    load_chunk<D, KVT>(p, cn, tn, win, hk, tlim, wave, sn);
+    compute_chunk<D, NT, KVT>(p, cc, tc, st, sc, sx, wave);
 }
 
 __device__ __forceinline__ uint32_t owner_of(uint32_t blk, uint32_t N, uint32_t B) {
@@ -398,29 +468,27 @@ __device__ __forceinline__ uint32_t owner_of(uint32_t blk, uint32_t N, uint32_t 
 }
 
 template <int D, int NT, int KVT>
-struct Smem {
-    static constexpr uint32_t COLS = 16 * NT;
-    static constexpr uint32_t STAGE = kWaves * 32 * Cfg<D, KVT>::PITCH * 2; // V staging bytes
-    static constexpr uint32_t MERGE = kWaves * COLS * (D + 2) * 4;            // merge bytes
-    static constexpr uint32_t BYTES = STAGE > MERGE ? STAGE : MERGE;
-};
-
-template <int D, int NT, int KVT>
-__global__ __launch_bounds__(kThreads) void attention_kernel(AttnParams p) {
+__global__ __launch_bounds__(D / 32 * 64) void attention_kernel(AttnParams p) {
     using C = Cfg<D, KVT>;
-    using S = Smem<D, NT, KVT>;
-    constexpr uint32_t COLS = S::COLS;
-    __shared__ __attribute__((aligned(16))) uint8_t smem[S::BYTES];
+    constexpr uint32_t COLS = 16 * NT;
+    // Two distinct LDS objects for the two V stages, so the compiler can tell a transpose
+    // read of one stage from the direct-to-LDS loads in flight into the other; partial
+    // scores are exchanged through two alternating buffers (one barrier per chunk).
+    __shared__ __attribute__((aligned(16))) uint16_t vst0[C::WAVES * C::STAGE];
+    __shared__ __attribute__((aligned(16))) uint16_t vst1[C::WAVES * C::STAGE];
+    __shared__ f32x4 sxb[2][C::WAVES * NT * 2 * 64];
     const uint32_t wg = blockIdx.x;
     const uint32_t N = p.header[2];
     if (wg >= N) return;
     const uint32_t tid = threadIdx.x, lane = tid & 63;
-    const uint32_t wave = (uint32_t)__builtin_amdgcn_readfirstlane((int)(tid >> 6)); // uniform: SGPR
+    const uint32_t wave = (uint32_t)__builtin_amdgcn_readfirstlane((int)(tid >> 6)); // SGPR
     const uint32_t g = lane >> 4, li = lane & 15;
-    uint16_t *vlds = (uint16_t *)smem + wave * 32 * C::PITCH;
+    uint16_t *stage0 = vst0 + wave * C::STAGE;
+    uint16_t *stage1 = vst1 + wave * C::STAGE;
     const uint4 wd = p.wg_desc[wg];
     uint32_t u = wd.x, lo = wd.y;
     const uint32_t hi = wd.z, U = p.header[0];
+    uint32_t parity = 0; // alternates the score-exchange buffer across all chunks
 
     while (lo < hi && u < U) {
         const UnitDesc ud = p.units[u];
@@ -432,104 +500,80 @@ __global__ __launch_bounds__(kThreads) void attention_kernel(AttnParams p) {
         const uint32_t kend = ud.kend;
         const uint32_t ncols = ud.nrows * p.group;
 
-        u32x4 qr[NT][C::KS];
-        uint32_t lim[NT];
-        float m[NT], l[NT];
-        f32x4 o[NT][C::DT];
+        State<D, NT, KVT> st;
 #pragma unroll
         for (int nt = 0; nt < NT; nt++) {
             const uint32_t col = nt * 16 + li;
             const bool valid = col < ncols;
             const uint32_t ri = valid ? col / p.group : 0;
-            lim[nt] = valid ? ud.pos0 + ri + 1 : 0;
-            load_q<D, KVT>(p, qr[nt], ud.rowbeg + ri, hk * p.group + col % p.group, valid);
-            m[nt] = -INFINITY;
-            l[nt] = 0.0f;
-#pragma unroll
-            for (int n = 0; n < C::DT; n++) o[nt][n] = f32x4{0.0f, 0.0f, 0.0f, 0.0f};
+            st.lim[nt] = valid ? ud.pos0 + ri + 1 : 0;
+            st.qr[nt] = load_q<D, KVT>(p, ud.rowbeg + ri, hk * p.group + col % p.group, valid, wave);
+            st.m[nt] = -INFINITY;
+            st.l[nt] = 0.0f;
+            st.o[nt][0] = st.o[nt][1] = f32x4{0.0f, 0.0f, 0.0f, 0.0f};
         }
 
         const uint32_t tbeg = (lo - ud.block_start) * 32;
         const uint32_t tend = min((seg_end - ud.block_start) * 32, kend);
         const uint32_t page_limit = (kend + (1u << p.page_shift) - 1) >> p.page_shift;
-        // Windows of at most 64 pages: each lane holds one page id, so the chunk loop issues
-        // no metadata loads.  Wave k takes chunks k, k + kWaves, ... of each window.
+        // Windows of at most 64 pages: each lane holds one page id.
         for (uint32_t wbeg = tbeg; wbeg < tend;) {
             const uint32_t wend = min(tend, ((wbeg >> p.page_shift) + 64) << p.page_shift);
-            const uint32_t t0 = wbeg + 32 * wave;
-            if (t0 < wend) {
-                PageWindow win;
-                window_load<C::FP8>(p, win, table, wbeg >> p.page_shift, page_limit, hk);
-                constexpr uint32_t step = 32 * kWaves;
-                Chunk<D, KVT> c0, c1;
-                load_chunk<D, KVT>(p, c0, t0, win, hk, wend);
-                for (uint32_t t = t0;; t += 2 * step) {
-                    load_chunk<D, KVT>(p, c1, t + step, win, hk, wend); // past wend: no traffic
-                    compute_chunk<D, NT, KVT>(p, c0, t, qr, lim, m, l, o, vlds);
-                    if (t + step >= wend) break;
-                    load_chunk<D, KVT>(p, c0, t + 2 * step, win, hk, wend);
-                    compute_chunk<D, NT, KVT>(p, c1, t + step, qr, lim, m, l, o, vlds);
-                    if (t + 2 * step >= wend) break;
-                }
+            PageWindow win;
+            window_load<C::FP8>(p, win, table, wbeg >> p.page_shift, page_limit, hk);
+            Chunk<D, KVT> c0, c1;
+            load_chunk<D, KVT>(p, c0, wbeg, win, hk, wend, wave, stage0);
+            for (uint32_t t = wbeg;; t += 64) {
+                // loads past wend carry no traffic
+                pipeline_step<D, NT, KVT>(p, c1, t + 32, stage1, c0, t, stage0, win, hk, wend, wave,
+                                          st, sxb[parity]);
+                parity ^= 1;
+                if (t + 32 >= wend) break;
+                pipeline_step<D, NT, KVT>(p, c0, t + 64, stage0, c1, t + 32, stage1, win, hk, wend,
+                                          wave, st, sxb[parity]);
+                parity ^= 1;
+                if (t + 64 >= wend) break;
             }
+            wait_vmcnt<0>(); // the trailing (empty) loads target a stage about to be reused
             wbeg = wend;
         }
 
-        // Merge the waves' states through LDS: O^T, reference max and mass per column.
-        float *mo = (float *)smem;                       // [wave][COLS][D]
-        float *mml = mo + kWaves * COLS * D;             // [wave][COLS][2]
-        __syncthreads(); // every wave is done with its V staging
+        // Finalise this wave's d slice: normalised output or a split record.
+        const bool whole = lo == ud.block_start && seg_end == uend;
+        const uint32_t rec = wg + u;
 #pragma unroll
         for (int nt = 0; nt < NT; nt++) {
-            float lt = l[nt];
+            float lt = st.l[nt];
             lt += shfl_xor(lt, 16);
             lt += shfl_xor(lt, 32);
             const uint32_t col = nt * 16 + li;
-            float *dst = mo + ((size_t)wave * COLS + col) * D + 4 * g;
-#pragma unroll
-            for (int n = 0; n < C::DT; n++) *(f32x4 *)(dst + 16 * n) = o[nt][n];
-            if (g == 0) {
-                mml[(wave * COLS + col) * 2] = m[nt];
-                mml[(wave * COLS + col) * 2 + 1] = lt;
-            }
-        }
-        __syncthreads();
-        const bool whole = lo == ud.block_start && seg_end == uend;
-        const uint32_t rec = wg + u;
-        for (uint32_t e = tid; e < COLS * D; e += kThreads) {
-            const uint32_t col = e / D, d = e % D;
             if (col >= ncols) continue;
-            float M = -INFINITY;
-#pragma unroll
-            for (int k = 0; k < kWaves; k++)
-                if (mml[(k * COLS + col) * 2 + 1] > 0.0f) M = fmaxf(M, mml[(k * COLS + col) * 2]);
-            float num = 0.0f, den = 0.0f;
-#pragma unroll
-            for (int k = 0; k < kWaves; k++) {
-                const float mass = mml[(k * COLS + col) * 2 + 1];
-                if (mass > 0.0f) {
-                    const float w = fast_exp2(mml[(k * COLS + col) * 2] - M);
-                    den = fmaf(w, mass, den);
-                    num = fmaf(w, mo[((size_t)k * COLS + col) * D + d], num);
-                }
-            }
+            const uint32_t row = ud.rowbeg + col / p.group;
+            const uint32_t head = hk * p.group + col % p.group;
             if (whole) {
-                const uint32_t row = ud.rowbeg + col / p.group;
-                const uint32_t head = hk * p.group + col % p.group;
-                const size_t at = ((size_t)row * p.hq + head) * D + d;
-                const float v = den > 0.0f ? num / den : 0.0f;
-                if (p.out_f32) ((float *)p.out)[at] = v;
-                else ((uint16_t *)p.out)[at] = f32_to_bf16(v);
+                const float inv = lt > 0.0f ? 1.0f / lt : 0.0f;
+                const size_t base = ((size_t)row * p.hq + head) * D + 32 * wave + 4 * g;
+#pragma unroll
+                for (int n = 0; n < 2; n++) {
+                    const f32x4 v = st.o[nt][n] * inv;
+                    if (p.out_f32) {
+                        *(f32x4 *)((float *)p.out + base + 16 * n) = v;
+                    } else {
+                        *(u32x2 *)((uint16_t *)p.out + base + 16 * n) =
+                            u32x2{pack2<true>(v.x, v.y), pack2<true>(v.z, v.w)};
+                    }
+                }
             } else {
                 const size_t rb = (size_t)rec * COLS + col;
-                p.part_o[rb * D + d] = num;
-                if (d == 0) {
-                    p.part_ml[rb * 2] = M;
-                    p.part_ml[rb * 2 + 1] = den;
+                float *po = p.part_o + rb * D + 32 * wave + 4 * g;
+#pragma unroll
+                for (int n = 0; n < 2; n++) *(f32x4 *)(po + 16 * n) = st.o[nt][n];
+                if (wave == 0 && g == 0) {
+                    p.part_ml[rb * 2] = st.m[nt];
+                    p.part_ml[rb * 2 + 1] = lt;
                 }
             }
         }
-        __syncthreads(); // LDS is reused by the next segment
         lo = seg_end;
         u++;
     }
@@ -673,18 +717,51 @@ extern "C" uint32_t lia_device_cus(void) {
     return g_cus;
 }
 
-// Attention workgroups per launch: one per compute unit (a unit never spans more
-// records than the combine holds).
-static uint32_t workgroups_for_device() {
+// Upper bound on attention workgroups per launch: sizes the plan and the record area.
+static uint32_t max_workgroups() {
     uint32_t cus = lia_device_cus();
     if (!cus) cus = 256;
-    uint32_t n = cus * 1;
+    uint32_t n = cus * 4;
     return n < kCombineMaxRecords ? n : kCombineMaxRecords;
+}
+
+template <int D, int NT, int KVT>
+static uint32_t resident_workgroups() {
+    // workgroups of this instantiation that fit on one CU at once (registers and LDS)
+    static uint32_t cached = 0;
+    if (!cached) {
+        int per_cu = 0;
+        if (hipOccupancyMaxActiveBlocksPerMultiprocessor(
+                &per_cu, reinterpret_cast<const void *>(&attention_kernel<D, NT, KVT>),
+                Cfg<D, KVT>::THREADS, 0) !=
+                hipSuccess || per_cu < 1)
+            per_cu = 1;
+        cached = (uint32_t)per_cu;
+    }
+    return cached;
+}
+
+template <int D, int NT>
+static uint32_t resident_kv(int kv) {
+    if (kv == LIA_BF16) return resident_workgroups<D, NT, LIA_BF16>();
+    if (kv == LIA_F16) return resident_workgroups<D, NT, LIA_F16>();
+    return resident_workgroups<D, NT, LIA_FP8_E4M3>();
+}
+
+// Workgroups of one launch: every CU filled once with resident workgroups.
+static uint32_t workgroups_for(uint32_t d, uint32_t nt, int kv) {
+    uint32_t cus = lia_device_cus();
+    if (!cus) cus = 256;
+    uint32_t per = d == 128 ? (nt == 1 ? resident_kv<128, 1>(kv) : resident_kv<128, 2>(kv))
+                            : (nt == 1 ? resident_kv<64, 1>(kv) : resident_kv<64, 2>(kv));
+    uint32_t n = cus * per;
+    uint32_t cap = max_workgroups();
+    return n < cap ? n : cap;
 }
 
 extern "C" size_t lia_attention_workspace_bytes(const lia_attention_config *c) {
     if (!c || !c->num_kv_heads) return 0;
-    return layout_for(c, workgroups_for_device()).total;
+    return layout_for(c, max_workgroups()).total;
 }
 
 static int validate(const lia_attention_config *c) {
@@ -705,7 +782,7 @@ static int validate(const lia_attention_config *c) {
 
 template <int D, int NT, int KVT>
 static void launch_partial(const AttnParams &p, uint32_t n_wg, hipStream_t s) {
-    hipLaunchKernelGGL((attention_kernel<D, NT, KVT>), dim3(n_wg), dim3(kThreads), 0, s, p);
+    hipLaunchKernelGGL((attention_kernel<D, NT, KVT>), dim3(n_wg), dim3(Cfg<D, KVT>::THREADS), 0, s, p);
 }
 
 template <int D, int NT>
@@ -737,12 +814,12 @@ static int run_stages(int stages, const lia_attention_config *c, uint32_t n_seqs
         if (c->kv_dtype == LIA_FP8_E4M3 && (!k_scales || !v_scales)) return LIA_E_ARG;
         if (((uintptr_t)q | (uintptr_t)kc | (uintptr_t)vc) & 15) return LIA_E_ALIGN;
     }
-    const uint32_t n_wg = workgroups_for_device();
-    Layout L = layout_for(c, n_wg);
+    Layout L = layout_for(c, max_workgroups());
     if (workspace_bytes < L.total) return LIA_E_WORKSPACE;
     if ((uintptr_t)workspace & 255) return LIA_E_ALIGN;
     const uint32_t group = c->num_q_heads / c->num_kv_heads;
     const uint32_t NT = nt_for(n_rows, n_seqs, group);
+    const uint32_t n_wg = workgroups_for(c->head_dim, NT, c->kv_dtype);
     const uint32_t rpc = (16 * NT) / group;
     uint8_t *ws = (uint8_t *)workspace;
     AttnParams p;
