@@ -5,13 +5,15 @@ Workload: ragged bf16 decode, batch 8, contexts U[1024,
 permutation, N(0,1) data, 40 layers as independent KV slices.
 
 One step = device packing of the batch (cu_seqlens, positions, slot mapping), the work
-plan, then per layer: KV append of the 8 new tokens, the split attention kernel and the
-split combine.  The step is captured once as a HIP graph and replayed (the reference
+plan, then per layer: the split attention kernel with the KV append of the 8 new tokens
+fused in (lia_attention_partial_append: the new keys are read from the step's rows and
+scattered into the pool by the same launch) and the split combine.  The step is captured once as a HIP graph and replayed (the reference
 replays CUDA graphs of the paged forward, src/inference/paging.rs:238-259).
 
 value = decode tokens/s of the whole step (8 tokens per step).  The roofline object
 covers the dominant kernel (the split attention kernel), timed alone with HIP events on
-its stream; its algorithmic bytes are K/V of every attended key + Q + O + block table.
+its stream; its algorithmic bytes are K/V of every attended key + Q + O + block table +
+the appended rows it writes.
 """
 import argparse
 import json
@@ -90,19 +92,16 @@ def main():
     cfg = lia.AttentionConfig(g.hq, g.hkv, g.d, P, b.pool_pages, b.stride, g.q_dtype, g.kv_dtype,
                               g.out_dtype, g.scale, b.n_seqs, rows, int(b.ctx.max()))
     ws = torch.zeros(lia.workspace_bytes(cfg), dtype=torch.uint8, device=dev)
-    layout = lia.KVLayout(g.hkv, g.d, P, b.pool_pages, g.kv_dtype)
     context = b.stride * P
     torch.cuda.synchronize()
 
     def step():
         lia.pack_device(seq_slots, q_lens, cached, flat, b.stride, P, b.pool_pages, context, rows,
                         cu, positions, sequences, slots, status)
-        lia.attention_plan(cfg, b.n_seqs, rows, cu, positions, sequences, ws)
+        lia.attention_plan(cfg, b.n_seqs, rows, cu, positions, sequences, ws, pages=flat)
         for layer in range(L):
-            lia.kv_append(layout, newk[layer], newv[layer], kpool[layer], vpool[layer],
-                          slot_mapping=slots)
-            lia.attention_partial(cfg, b.n_seqs, flat, qs[layer], kpool[layer], vpool[layer],
-                                  outs[layer], ws)
+            lia.attention_partial_append(cfg, b.n_seqs, flat, slots, qs[layer], newk[layer],
+                                         newv[layer], kpool[layer], vpool[layer], outs[layer], ws)
             lia.attention_merge(cfg, b.n_seqs, rows, outs[layer], ws)
 
     # eager step once (validates arguments, checks the packing status)
@@ -130,14 +129,15 @@ def main():
     ms_step = start.elapsed_time(stop) / args.steps
     log(f"step: {ms_step:.4f} ms (wall {wall * 1e3 / args.steps:.4f} ms)")
 
-    # ---- dominant kernel alone: one graph of L split-attention launches
+    # ---- dominant kernel alone: one graph of L fused append + split-attention launches
     kgraph = torch.cuda.CUDAGraph()
     stream = torch.cuda.Stream()
     with torch.cuda.stream(stream):
         with torch.cuda.graph(kgraph, stream=stream):
             for layer in range(L):
-                lia.attention_partial(cfg, b.n_seqs, flat, qs[layer], kpool[layer],
-                                      vpool[layer], outs[layer], ws)
+                lia.attention_partial_append(cfg, b.n_seqs, flat, slots, qs[layer], newk[layer],
+                                             newv[layer], kpool[layer], vpool[layer],
+                                             outs[layer], ws)
     torch.cuda.synchronize()
     for _ in range(3):
         kgraph.replay()
@@ -150,9 +150,11 @@ def main():
     ke.record(cur)
     torch.cuda.synchronize()
     kernel_us = ks.elapsed_time(ke) * 1e3 / (args.kernel_reps * L)
-    layer_bytes = b.algorithmic_bytes()
+    # attended K/V (the new keys read from the step's rows) + Q + O + table, plus the
+    # appended K/V rows the fused launch writes into the pool
+    layer_bytes = b.algorithmic_bytes() + rows * g.hkv * g.d * 2 * 2
     achieved = layer_bytes / (kernel_us * 1e-6) / 1e9
-    step_bytes = layer_bytes * L + rows * g.hkv * g.d * 2 * 2 * L  # + appended K/V rows
+    step_bytes = layer_bytes * L
     step_gbps = step_bytes / (ms_step * 1e-3) / 1e9
     log(f"attention kernel: {kernel_us:.2f} us/launch, {achieved:.1f} GB/s "
         f"({achieved / PEAK_HBM_GBPS:.1%} of peak), layer bytes {layer_bytes}")
@@ -199,8 +201,8 @@ def main():
         "config": {
             "workload": "BASELINE config 2: ragged bf16 paged decode, batch 8, ctx U[1024,32768] "
                         "seed %d, 16q/2kv heads, head_dim 128, page 16, %d layers as independent "
-                        "KV slices; step = device pack + plan + per layer (KV append + split "
-                        "attention + combine), HIP-graph replay" % (args.seed, L),
+                        "KV slices; step = device pack + plan + per layer (split attention with "
+                        "the KV append fused in + combine), HIP-graph replay" % (args.seed, L),
             "batch": b.n_seqs, "layers": L, "ctx": b.ctx.tolist(), "sum_ctx": int(b.ctx.sum()),
             "page_size": P, "pool_pages": b.pool_pages,
             "step_hbm_GBps": round(step_gbps, 1),
@@ -209,7 +211,7 @@ def main():
         "roofline": {
             "bound": "hbm", "achieved": round(achieved, 1), "peak": PEAK_HBM_GBPS, "unit": "GB/s",
             "frac": round(achieved / PEAK_HBM_GBPS, 4), "traffic": None,
-            "kernel": "attention_kernel<128,1,bf16>", "kernel_us": round(kernel_us, 3),
+            "kernel": "attention_kernel<128,1,bf16> (fused append)", "kernel_us": round(kernel_us, 3),
             "bytes_per_launch": layer_bytes,
         },
         "cpu_baseline": cpu,

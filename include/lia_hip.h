@@ -205,8 +205,11 @@ int lia_paged_attention(const lia_attention_config *config, uint32_t n_seqs, uin
  *   lia_attention_plan:    builds the step's work list in the workspace from cu_seqlens,
  *                          positions and sequences (replaces the host planning of
  *                          llama_plan::tiles, src/inference/llama_plan.rs:16-101); the
- *                          other two stages read the per-row metadata from it.
- *   lia_attention_partial: the split attention kernel; units covered by one wavefront are
+ *                          other two stages read the per-row metadata from it.  When pages
+ *                          is not NULL the plan also copies the first block-table entries of
+ *                          every workgroup's range into the work list, so the table must not
+ *                          change between the plan and the partial calls that use it.
+ *   lia_attention_partial: the split attention kernel; units covered by one workgroup are
  *                          written normalised to out, the others leave partial records
  *                          (replaces gpu::llama_attention::partial, llama_attention.rs:24-159).
  *   lia_attention_merge:   combines the partial records into out (replaces
@@ -215,14 +218,33 @@ int lia_paged_attention(const lia_attention_config *config, uint32_t n_seqs, uin
  */
 int lia_attention_plan(const lia_attention_config *config, uint32_t n_seqs, uint32_t n_rows,
                        const uint32_t *cu_seqlens, const uint32_t *positions,
-                       const uint32_t *sequences, void *workspace, size_t workspace_bytes,
-                       lia_stream_t stream);
+                       const uint32_t *sequences, const uint32_t *pages, void *workspace,
+                       size_t workspace_bytes, lia_stream_t stream);
 int lia_attention_partial(const lia_attention_config *config, uint32_t n_seqs, uint32_t n_rows,
                           const uint32_t *pages, const void *q, const void *kc, const void *vc,
                           const float *k_scales, const float *v_scales, void *workspace,
                           size_t workspace_bytes, void *out, lia_stream_t stream);
 int lia_attention_merge(const lia_attention_config *config, uint32_t n_seqs, uint32_t n_rows,
                         void *workspace, size_t workspace_bytes, void *out, lia_stream_t stream);
+
+/*
+ * lia_kv_append of this step's rows (slot_mapping form, source dtype = pool dtype) fused
+ * into lia_attention_partial: one launch does both.  Replaces the per-layer pair
+ * llama_cache_paged + paged attention of the reference forward (src/gpu/kernels/llama.rs:162-183
+ * followed by src/inference/llama.rs:253-288).  new_k / new_v: [n_rows][num_kv_heads][head_dim]
+ * in the pool dtype (LIA_F16 or LIA_BF16; FP8 pools return LIA_E_UNSUPPORTED), 16-byte
+ * aligned.  The plan must come from the same packed rows: the first row of each sequence
+ * sits at the sequence's cached length and its rows' keys are read from new_k / new_v, the
+ * cached keys from the pool.  The pool afterwards holds the same bytes lia_kv_append
+ * writes.  No cached key of any sequence may live in a slot this step writes (the
+ * reference's page ownership guarantees it: packing rejects duplicate slots and new rows
+ * go to the sequence's own pages).
+ */
+int lia_attention_partial_append(const lia_attention_config *config, uint32_t n_seqs,
+                                 uint32_t n_rows, const uint32_t *pages,
+                                 const uint32_t *slot_mapping, const void *q, const void *new_k,
+                                 const void *new_v, void *kc, void *vc, void *workspace,
+                                 size_t workspace_bytes, void *out, lia_stream_t stream);
 
 /* Number of compute units the library schedules decode work for (device 0 unless
  * lia_init selected another).  0 on failure. */

@@ -99,8 +99,12 @@ EXPORTS = {
                                       C.c_void_p, C.c_void_p, C.c_size_t, C.c_void_p,
                                       C.c_void_p]),
     "lia_attention_plan": (C.c_int, [C.POINTER(AttentionConfig), C.c_uint32, C.c_uint32,
-                                     C.c_void_p, C.c_void_p, C.c_void_p, C.c_void_p, C.c_size_t,
-                                     C.c_void_p]),
+                                     C.c_void_p, C.c_void_p, C.c_void_p, C.c_void_p, C.c_void_p,
+                                     C.c_size_t, C.c_void_p]),
+    "lia_attention_partial_append": (C.c_int, [C.POINTER(AttentionConfig), C.c_uint32,
+                                               C.c_uint32, C.c_void_p, C.c_void_p, C.c_void_p,
+                                               C.c_void_p, C.c_void_p, C.c_void_p, C.c_void_p,
+                                               C.c_void_p, C.c_size_t, C.c_void_p, C.c_void_p]),
     "lia_attention_partial": (C.c_int, [C.POINTER(AttentionConfig), C.c_uint32, C.c_uint32,
                                         C.c_void_p, C.c_void_p, C.c_void_p, C.c_void_p,
                                         C.c_void_p, C.c_void_p, C.c_void_p, C.c_size_t,
@@ -246,10 +250,12 @@ def paged_attention(config, n_seqs, cu_seqlens, positions, sequences, pages, q, 
 
 
 def attention_plan(config, n_seqs, n_rows, cu_seqlens, positions, sequences, workspace,
-                   stream=None):
-    """Stage 1: the step's work list (shared by every layer of the step)."""
+                   pages=None, stream=None):
+    """Stage 1: the step's work list (shared by every layer of the step).  With `pages`
+    the plan also records the first table entries of every workgroup's range."""
     st = lib().lia_attention_plan(C.byref(config), n_seqs, n_rows, _dptr(cu_seqlens),
-                                  _dptr(positions), _dptr(sequences), _dptr(workspace),
+                                  _dptr(positions), _dptr(sequences), _dptr(pages),
+                                  _dptr(workspace),
                                   workspace.numel() * workspace.element_size(), _stream(stream))
     _check(st, "attention_plan")
 
@@ -263,6 +269,18 @@ def attention_partial(config, n_seqs, pages, q, kc, vc, out, workspace, k_scales
                                      workspace.numel() * workspace.element_size(), _dptr(out),
                                      _stream(stream))
     _check(st, "attention_partial")
+
+
+def attention_partial_append(config, n_seqs, pages, slot_mapping, q, new_k, new_v, kc, vc, out,
+                             workspace, stream=None):
+    """Stage 2 with this step's KV append fused in (lia_attention_partial_append): new_k /
+    new_v are the step's rows in the pool dtype."""
+    st = lib().lia_attention_partial_append(C.byref(config), n_seqs, q.shape[0], _dptr(pages),
+                                            _dptr(slot_mapping), _dptr(q), _dptr(new_k),
+                                            _dptr(new_v), _dptr(kc), _dptr(vc), _dptr(workspace),
+                                            workspace.numel() * workspace.element_size(),
+                                            _dptr(out), _stream(stream))
+    _check(st, "attention_partial_append")
 
 
 def attention_merge(config, n_seqs, n_rows, out, workspace, stream=None):

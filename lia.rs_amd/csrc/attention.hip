@@ -15,6 +15,13 @@
 // (src/gpu/kernels/llama_flash_kernel.rs:321-376, src/gpu/kernels/llama_merge.rs:10-76)
 // with splits chosen for load balance instead of a batch-uniform span.
 //
+// Keys of a unit come from two sources: the keys cached before this step, [0, kcache), are
+// read through the block table from the pool, and the keys of this step's own rows,
+// [kcache, kend), are blocked separately.  The plain entry points read both from the pool
+// (the rows were appended first); the fused-append entry point reads the new keys straight
+// from the caller's new K/V rows and scatters those rows into the pool in the same launch,
+// so no work of the launch ever reads a slot the launch writes.
+//
 // Per 32-token chunk a wave computes S^T = K * Q^T with K straight from HBM (bounded
 // buffer loads) as the MFMA A operand (16 tokens x 32 dims per instruction) and Q^T
 // resident in registers, runs the online softmax in the log2 domain per column, stages V
@@ -26,16 +33,33 @@
 namespace lia {
 
 
-// Unit descriptor written by the plan kernel (32 bytes).
+// Unit descriptor written by the plan kernel (32 bytes).  Rows of a sequence have
+// consecutive positions (validated by packing), so positions[rowbeg] = kend - nrows and
+// the sequence's first packed row is rowbeg - (positions[rowbeg] - kcache).
 struct UnitDesc {
     uint32_t block_start; // first block in the flattened block order
-    uint32_t nblocks;     // 32-token blocks of keys the unit attends
+    uint32_t nblocks;     // cblocks + ceil((kend - kcache) / 32)
+    uint32_t cblocks;     // ceil(kcache / 32): blocks of the keys cached before this step
     uint32_t rowbeg;      // first packed row of the column block
-    uint32_t nrows;       // rows in the column block
+    uint32_t nrows_hk;    // rows in the column block | KV head << 16
     uint32_t kend;        // keys attended by the last row (positions[last] + 1)
     uint32_t table_row;   // block-table row of the sequence
-    uint32_t hk;          // KV head
-    uint32_t pos0;        // positions[rowbeg]; rows of a sequence have consecutive positions
+    uint32_t kcache;      // position of the sequence's first packed row
+};
+
+__device__ __forceinline__ uint32_t unit_rows(const UnitDesc &u) { return u.nrows_hk & 0xffffu; }
+__device__ __forceinline__ uint32_t unit_head(const UnitDesc &u) { return u.nrows_hk >> 16; }
+
+// Per-workgroup work descriptor (64 bytes): the block range, a copy of the descriptor of
+// the range's first unit and the physical pages of the first four logical pages the range
+// reads, so a workgroup issues its first K/V loads one dependent load after launch.
+constexpr uint32_t kPrePages = 4;
+struct WorkDesc {
+    uint32_t unit;            // first unit of the range
+    uint32_t lo, hi;          // block range [lo, hi)
+    uint32_t npre;            // pre[] valid (the range starts in the unit's cached keys)
+    UnitDesc first;           // units[unit]
+    uint4 pre;                // pages of logical pages (32 * (lo - first.block_start)) / P + 0..3
 };
 
 struct AttnParams {
@@ -50,13 +74,19 @@ struct AttnParams {
     const uint32_t *pages;
     void *out;
     const UnitDesc *units;   // [U + 1]; units[U].block_start = B
-    const uint4 *wg_desc;    // per workgroup: {first unit, first block, end block, 0}
+    const WorkDesc *work;    // per workgroup
     const uint32_t *header;  // {U, B, N (workgroups with work), overflow}
     float *part_o;           // [records][cols][D]
     float *part_ml;          // [records][cols][2]
     uint32_t hq, hkv, group, stride, page_shift, n_wg, rpc;
     float scale_log2;        // softmax scale * log2(e)
     int q_f32, out_f32;
+    // fused append (null when the new rows are already in the pool)
+    const void *newk;        // [n_rows][hkv][D] in the pool dtype
+    const void *newv;
+    const uint32_t *slots;   // slot_mapping[n_rows]
+    void *kc_w, *vc_w;       // the pool planes, written by the append
+    uint32_t n_rows;
 };
 
 // ------------------------------------------------------------------ plan
@@ -64,12 +94,19 @@ struct AttnParams {
 // One workgroup builds the unit list of a step and the block range of every attention
 // workgroup.  Positions within a sequence are consecutive (validated by packing,
 // src/inference/paging.rs:167-172), so the key count of a column block follows from the
-// position of its first row.
+// position of its first row.  A unit's keys are blocked in two runs: the keys cached before
+// the step, [0, kcache) with kcache the position of the sequence's first row, then the
+// keys of the step's own rows, [kcache, kend).
+__device__ __forceinline__ uint32_t unit_blocks(uint32_t p0, uint32_t new_keys) {
+    return (p0 + 31) / 32 + (new_keys + 31) / 32;
+}
+
 __global__ __launch_bounds__(256) void plan_kernel(uint32_t n_seqs, const uint32_t *cu,
                                                    const uint32_t *positions,
-                                                   const uint32_t *sequences, uint32_t rpc,
+                                                   const uint32_t *sequences, const uint32_t *pages,
+                                                   uint32_t stride, uint32_t page_shift, uint32_t rpc,
                                                    uint32_t hkv, uint32_t max_units,
-                                                   uint32_t n_wg, UnitDesc *units, uint4 *wg_desc,
+                                                   uint32_t n_wg, UnitDesc *units, WorkDesc *work,
                                                    uint32_t *header) {
     __shared__ uint32_t s_units[256], s_blocks[256];
     __shared__ uint32_t carry_units, carry_blocks, overflow;
@@ -87,7 +124,7 @@ __global__ __launch_bounds__(256) void plan_kernel(uint32_t n_seqs, const uint32
                 trow = sequences[r0];
                 uint32_t ncb = (nr + rpc - 1) / rpc;
                 nu = ncb * hkv;
-                for (uint32_t cb = 0; cb < ncb; cb++) nb += (p0 + min((cb + 1) * rpc, nr) + 31) / 32;
+                for (uint32_t cb = 0; cb < ncb; cb++) nb += unit_blocks(p0, min((cb + 1) * rpc, nr));
                 nb *= hkv;
             }
         }
@@ -106,13 +143,14 @@ __global__ __launch_bounds__(256) void plan_kernel(uint32_t n_seqs, const uint32
         if (nu && u + nu > max_units) overflow = 1;
         if (nu && u + nu <= max_units) {
             uint32_t ncb = nu / hkv;
+            const uint32_t cblocks = (p0 + 31) / 32;
             for (uint32_t cb = 0; cb < ncb; cb++) {
                 uint32_t rows = min(rpc, nr - cb * rpc);
                 uint32_t kend = p0 + cb * rpc + rows;
-                uint32_t blocks = (kend + 31) / 32;
+                uint32_t blocks = unit_blocks(p0, kend - p0);
                 for (uint32_t h = 0; h < hkv; h++) {
-                    units[u++] = UnitDesc{blk, blocks, r0 + cb * rpc, rows, kend, trow, h,
-                                          p0 + cb * rpc};
+                    units[u++] = UnitDesc{blk, blocks, cblocks, r0 + cb * rpc, rows | (h << 16),
+                                          kend, trow, p0};
                     blk += blocks;
                 }
             }
@@ -132,6 +170,7 @@ __global__ __launch_bounds__(256) void plan_kernel(uint32_t n_seqs, const uint32
     }
     __threadfence();
     __syncthreads();
+    const uint32_t P = 1u << page_shift;
     for (uint32_t w = t; w < N; w += 256) {
         uint32_t lo = (uint32_t)((uint64_t)w * B / N), hi = (uint32_t)((uint64_t)(w + 1) * B / N);
         uint32_t a = 0, e = U; // last unit whose first block <= lo
@@ -140,7 +179,27 @@ __global__ __launch_bounds__(256) void plan_kernel(uint32_t n_seqs, const uint32
             if (units[mid].block_start <= lo) a = mid; else e = mid;
         }
         while (a + 1 < U && units[a].block_start + units[a].nblocks <= lo) a++;
-        wg_desc[w] = make_uint4(a, lo, hi, 0);
+        WorkDesc d;
+        d.unit = a;
+        d.lo = lo;
+        d.hi = hi;
+        d.first = units[a];
+        d.npre = 0;
+        const uint32_t rel = lo - d.first.block_start;
+        d.pre = make_uint4(0, 0, 0, 0);
+        if (pages && rel < d.first.cblocks) {
+            // logical pages the range starts with; the unfused launch reads a range that
+            // begins in the cached keys on into the new keys from the same table, so the
+            // pages of every attended key qualify
+            const uint32_t lp = (32 * rel) >> page_shift;
+            const uint32_t lend = (d.first.kend + P - 1) >> page_shift;
+            const uint32_t *row = pages + (size_t)d.first.table_row * stride;
+            uint32_t v[kPrePages];
+            for (uint32_t i = 0; i < kPrePages; i++) v[i] = lp + i < lend ? row[lp + i] : 0u;
+            d.pre = make_uint4(v[0], v[1], v[2], v[3]);
+            d.npre = 1;
+        }
+        work[w] = d;
     }
 }
 
@@ -178,9 +237,10 @@ struct Chunk {
     float ks[2], vs[2];
 };
 
-// Page ids of a segment live in the lanes of the wave: lane i holds the physical page of
+// Page ids of a key range live in the lanes of the wave: lane i holds the physical page of
 // logical page base + i, so the chunk loop gets page ids with v_readlane and issues no
-// metadata loads.
+// metadata loads.  A range over the new rows of the step uses identity pages (logical page
+// i of the rows is "page" i of a base pointer at the sequence's first new row).
 struct PageWindow {
     uint32_t base;  // first logical page covered (wave-uniform)
     uint32_t page;  // per lane: physical page of logical page base + lane (0 past the end)
@@ -193,11 +253,64 @@ __device__ __forceinline__ void window_load(const AttnParams &p, PageWindow &w,
                                             uint32_t hk) {
     const uint32_t idx = first + lane_id();
     w.base = first;
+    if (!table) { // identity pages of the new rows
+        w.page = idx;
+        w.ks = w.vs = 1.0f;
+        return;
+    }
     w.page = idx < limit ? table[idx] : 0u;
     if constexpr (FP8) {
         w.ks = idx < limit ? p.k_scales[(size_t)w.page * p.hkv + hk] : 0.0f;
         w.vs = idx < limit ? p.v_scales[(size_t)w.page * p.hkv + hk] : 0.0f;
     }
+}
+
+// Physical page, live-token count and FP8 scales of the two 16-token tiles of chunk t
+// (pages hold >= 16 tokens, so a tile lies in one page).  Tokens at or past tlim are not
+// live: their loads return zeros and move no data.
+struct TilePages {
+    uint32_t page[2], live[2];
+    float ks[2], vs[2];
+};
+
+template <bool FP8>
+__device__ __forceinline__ TilePages tile_pages(const PageWindow &w, uint32_t t, uint32_t shift,
+                                                uint32_t tlim) {
+    TilePages tp;
+    const uint32_t P = 1u << shift;
+#pragma unroll
+    for (int j = 0; j < 2; j++) {
+        const uint32_t t0 = t + 16 * j;
+        const uint32_t rel = (t0 >> shift) - w.base;
+        tp.page[j] = (uint32_t)__builtin_amdgcn_readlane((int)w.page, (int)(rel & 63));
+        const uint32_t pstart = t0 & ~(P - 1);
+        tp.live[j] = (rel < 64 && tlim > pstart) ? min(tlim - pstart, P) : 0u;
+        if constexpr (FP8) {
+            tp.ks[j] = __builtin_bit_cast(float, __builtin_amdgcn_readlane(__builtin_bit_cast(int, w.ks), (int)(rel & 63)));
+            tp.vs[j] = __builtin_bit_cast(float, __builtin_amdgcn_readlane(__builtin_bit_cast(int, w.vs), (int)(rel & 63)));
+        } else {
+            tp.ks[j] = tp.vs[j] = 1.0f;
+        }
+    }
+    return tp;
+}
+
+// The same from pages preloaded by the plan: pre[i] is the page of logical page lp0 + i
+// (wave-uniform values, selected without indexing).
+__device__ __forceinline__ TilePages tile_pages_pre(uint4 pre, uint32_t lp0, uint32_t t,
+                                                    uint32_t shift, uint32_t tlim) {
+    TilePages tp;
+    const uint32_t P = 1u << shift;
+#pragma unroll
+    for (int j = 0; j < 2; j++) {
+        const uint32_t t0 = t + 16 * j;
+        const uint32_t rel = (t0 >> shift) - lp0;
+        const uint32_t pstart = t0 & ~(P - 1);
+        tp.page[j] = rel == 0 ? pre.x : rel == 1 ? pre.y : rel == 2 ? pre.z : pre.w;
+        tp.live[j] = (rel < kPrePages && tlim > pstart) ? min(tlim - pstart, P) : 0u;
+        tp.ks[j] = tp.vs[j] = 1.0f;
+    }
+    return tp;
 }
 
 // Wait until at most `n` vector-memory operations of this wave are outstanding.
@@ -211,14 +324,15 @@ __device__ __forceinline__ void wait_vmcnt() {
 template <int D, int KVT>
 constexpr int kLoadsPerChunk = 4; // two K loads + two V loads
 
-// Loads chunk t (32 tokens, t a multiple of 32; pages hold >= 16 tokens so each 16-token
-// tile lies in one page) of this wave's d slice.  Buffer loads are bounded to the live
-// tokens [.., tlim) of the tile's page: rows past tlim read as zeros without touching
-// memory, so every load is issued unconditionally and masked V rows are zero.
+// Loads chunk t (32 tokens, t a multiple of 32) of this wave's d slice from the planes at
+// kbase / vbase (the pool, or the step's new rows).  Buffer loads are bounded to each
+// tile's live tokens: rows past them read as zeros without touching memory, so every load
+// is issued unconditionally and masked V rows are zero.
 template <int D, int KVT>
 __device__ __forceinline__ void load_chunk(const AttnParams &p, Chunk<D, KVT> &c, uint32_t t,
-                                           const PageWindow &w, uint32_t hk, uint32_t tlim,
-                                           uint32_t wave, uint16_t *stage) {
+                                           const TilePages &tp, const uint8_t *kbase,
+                                           const uint8_t *vbase, uint32_t hk, uint32_t wave,
+                                           uint16_t *stage) {
     using C = Cfg<D, KVT>;
     const uint32_t lane = lane_id(), g = lane >> 4, li = lane & 15;
     const uint32_t P = 1u << p.page_shift;
@@ -227,16 +341,10 @@ __device__ __forceinline__ void load_chunk(const AttnParams &p, Chunk<D, KVT> &c
     __amdgpu_buffer_rsrc_t r[2];
 #pragma unroll
     for (int j = 0; j < 2; j++) {
-        const uint32_t t0 = t + 16 * j;
-        const uint32_t rel = (t0 >> p.page_shift) - w.base;
-        const uint32_t page = (uint32_t)__builtin_amdgcn_readlane((int)w.page, (int)(rel & 63));
-        const uint32_t pstart = t0 & ~(P - 1);
-        const uint32_t live = (rel < 64 && tlim > pstart) ? min(tlim - pstart, P) : 0u;
-        const size_t base = (size_t)page * P * row_bytes;
-        r[j] = make_rsrc((const uint8_t *)p.kc + base, live * row_bytes);
+        r[j] = make_rsrc(kbase + (size_t)tp.page[j] * P * row_bytes, tp.live[j] * row_bytes);
         if constexpr (C::FP8) {
-            c.ks[j] = __builtin_bit_cast(float, __builtin_amdgcn_readlane(__builtin_bit_cast(int, w.ks), (int)(rel & 63)));
-            c.vs[j] = __builtin_bit_cast(float, __builtin_amdgcn_readlane(__builtin_bit_cast(int, w.vs), (int)(rel & 63)));
+            c.ks[j] = tp.ks[j];
+            c.vs[j] = tp.vs[j];
         }
     }
     // K: lane (g, li) of tile j reads token 16j+li, dims 32w + 8g .. +7 (the four groups
@@ -259,14 +367,8 @@ __device__ __forceinline__ void load_chunk(const AttnParams &p, Chunk<D, KVT> &c
         const uint32_t tok = lane >> 1;
         __amdgpu_buffer_rsrc_t vr[2];
 #pragma unroll
-        for (int jj = 0; jj < 2; jj++) {
-            const uint32_t t0 = t + 16 * jj;
-            const uint32_t rel = (t0 >> p.page_shift) - w.base;
-            const uint32_t page = (uint32_t)__builtin_amdgcn_readlane((int)w.page, (int)(rel & 63));
-            const uint32_t pstart = t0 & ~(P - 1);
-            const uint32_t live = (rel < 64 && tlim > pstart) ? min(tlim - pstart, P) : 0u;
-            vr[jj] = make_rsrc((const uint8_t *)p.vc + (size_t)page * P * row_bytes, live * row_bytes);
-        }
+        for (int jj = 0; jj < 2; jj++)
+            vr[jj] = make_rsrc(vbase + (size_t)tp.page[jj] * P * row_bytes, tp.live[jj] * row_bytes);
         const uint32_t off = (((t + 16 * (tok >> 4)) & (P - 1)) + (tok & 15)) * row_bytes + slice_off +
                              16 * (lane & 1);
         // lanes 0-31 read tile 0, lanes 32-63 tile 1: two loads, each with half the lanes live
@@ -280,12 +382,8 @@ __device__ __forceinline__ void load_chunk(const AttnParams &p, Chunk<D, KVT> &c
 #pragma unroll
         for (int s = 0; s < 2; s++) {
             const uint32_t t0 = t + 16 * s;
-            const uint32_t rel = (t0 >> p.page_shift) - w.base;
-            const uint32_t page = (uint32_t)__builtin_amdgcn_readlane((int)w.page, (int)(rel & 63));
-            const uint32_t pstart = t0 & ~(P - 1);
-            const uint32_t live = (rel < 64 && tlim > pstart) ? min(tlim - pstart, P) : 0u;
             const __amdgpu_buffer_rsrc_t vr =
-                make_rsrc((const uint8_t *)p.vc + (size_t)page * P * row_bytes, live * row_bytes);
+                make_rsrc(vbase + (size_t)tp.page[s] * P * row_bytes, tp.live[s] * row_bytes);
             const uint32_t row = 16 * s + (lane >> 2);
             const uint32_t chunk = (lane & 3) ^ swz(row);
             const uint32_t off = ((t0 & (P - 1)) + (row & 15)) * row_bytes + slice_off + 16 * chunk;
@@ -329,7 +427,8 @@ __device__ __forceinline__ u32x4 load_q(const AttnParams &p, uint32_t row, uint3
 template <int D, int NT, int KVT>
 struct State {
     u32x4 qr[NT];
-    uint32_t lim[NT];
+    uint32_t lo;       // first key of the current range (wave-uniform)
+    uint32_t lim[NT];  // per column: live keys of the range, counted from lo
     float m[NT], l[NT];
     f32x4 o[NT][2];
 };
@@ -392,7 +491,8 @@ __device__ __forceinline__ void compute_chunk(const AttnParams &p, const Chunk<D
 #pragma unroll
             for (int w = 1; w < C::WAVES; w++) s[j] += sx[((w * NT + nt) * 2 + j) * 64 + lane];
         }
-        // Online softmax for column nt*16 + li over tokens t + 16j + 4g + i, with a lazily
+        // Online softmax for column nt*16 + li over tokens t + 16j + 4g + i (live when
+        // lo <= token < lo + lim, one unsigned compare), with a lazily
         // updated reference maximum: exponentials are taken against m, which is raised
         // (and O, l rescaled) only when a score exceeds it by more than 2^8.  Numerator
         // and denominator share the reference, so the normalised result is unchanged.
@@ -403,7 +503,7 @@ __device__ __forceinline__ void compute_chunk(const AttnParams &p, const Chunk<D
 #pragma unroll
             for (int i = 0; i < 4; i++) {
                 const uint32_t tok = t + 16 * j + 4 * g + i;
-                const float v = tok < st.lim[nt] ? s[j][i] * kscale[j] : -INFINITY;
+                const float v = tok - st.lo < st.lim[nt] ? s[j][i] * kscale[j] : -INFINITY;
                 x[j][i] = v;
                 mx = fmaxf(mx, v);
             }
@@ -455,16 +555,110 @@ __device__ __forceinline__ void compute_chunk(const AttnParams &p, const Chunk<D
 // loads still in flight into `sn`, so no full vmcnt drain is needed before them.
 template <int D, int NT, int KVT>
 __device__ __forceinline__ void pipeline_step(const AttnParams &p, Chunk<D, KVT> &cn, uint32_t tn,
-                                              uint16_t *__restrict__ sn, const Chunk<D, KVT> &cc,
-                                              uint32_t tc, uint16_t *__restrict__ sc,
-                                              const PageWindow &win, uint32_t hk, uint32_t tlim,
-                                              uint32_t wave, State<D, NT, KVT> &st, f32x4 *sx) {
-    load_chunk<D, KVT>(p, cn, tn, win, hk, tlim, wave, sn);
+                                              const TilePages &tpn, uint16_t *__restrict__ sn,
+                                              const Chunk<D, KVT> &cc, uint32_t tc,
+                                              uint16_t *__restrict__ sc, const uint8_t *kbase,
+                                              const uint8_t *vbase, uint32_t hk, uint32_t wave,
+                                              State<D, NT, KVT> &st, f32x4 *sx) {
+    load_chunk<D, KVT>(p, cn, tn, tpn, kbase, vbase, hk, wave, sn);
     compute_chunk<D, NT, KVT>(p, cc, tc, st, sc, sx, wave);
+}
+
+// Attends keys [s_lo, s_hi) of one source (coordinates of that source: token index in the
+// pool, or new-row index) into the running state.  Windows of at most 64 pages; the
+// first two chunks of the workgroup's first range take their pages from the plan.
+template <int D, int NT, int KVT>
+__device__ __forceinline__ void run_range(const AttnParams &p, const uint8_t *kbase,
+                                          const uint8_t *vbase, const uint32_t *table,
+                                          uint32_t s_lo, uint32_t s_hi, bool use_pre,
+                                          uint4 pre, uint32_t hk, uint32_t wave, State<D, NT, KVT> &st,
+                                          uint16_t *stage0, uint16_t *stage1, f32x4 *sxb,
+                                          uint32_t &parity) {
+    using C = Cfg<D, KVT>;
+    constexpr uint32_t SX = C::WAVES * NT * 2 * 64;
+    const uint32_t shift = p.page_shift;
+    const uint32_t page_limit = (s_hi + (1u << shift) - 1) >> shift;
+    for (uint32_t wbeg = s_lo & ~31u; wbeg < s_hi;) {
+        const uint32_t wend = min(s_hi, ((wbeg >> shift) + 64) << shift);
+        PageWindow win;
+        window_load<C::FP8>(p, win, table, wbeg >> shift, page_limit, hk);
+        Chunk<D, KVT> c0, c1;
+        // prologue: chunks wbeg and wbeg + 32 in flight, chunk wbeg computed
+        TilePages tp0, tp1;
+        if (!C::FP8 && use_pre) {
+            tp0 = tile_pages_pre(pre, wbeg >> shift, wbeg, shift, wend);
+            tp1 = tile_pages_pre(pre, wbeg >> shift, wbeg + 32, shift, wend);
+            use_pre = false;
+        } else {
+            tp0 = tile_pages<C::FP8>(win, wbeg, shift, wend);
+            tp1 = tile_pages<C::FP8>(win, wbeg + 32, shift, wend);
+        }
+        load_chunk<D, KVT>(p, c0, wbeg, tp0, kbase, vbase, hk, wave, stage0);
+        pipeline_step<D, NT, KVT>(p, c1, wbeg + 32, tp1, stage1, c0, wbeg, stage0, kbase, vbase, hk,
+                                  wave, st, sxb + parity * SX);
+        parity ^= 1;
+        if (wbeg + 32 < wend) {
+            for (uint32_t t = wbeg + 32;; t += 64) {
+                // loads past wend carry no traffic
+                pipeline_step<D, NT, KVT>(p, c0, t + 32, tile_pages<C::FP8>(win, t + 32, shift, wend),
+                                          stage0, c1, t, stage1, kbase, vbase, hk, wave, st,
+                                          sxb + parity * SX);
+                parity ^= 1;
+                if (t + 32 >= wend) break;
+                pipeline_step<D, NT, KVT>(p, c1, t + 64, tile_pages<C::FP8>(win, t + 64, shift, wend),
+                                          stage1, c0, t + 32, stage0, kbase, vbase, hk, wave, st,
+                                          sxb + parity * SX);
+                parity ^= 1;
+                if (t + 64 >= wend) break;
+            }
+        }
+        wait_vmcnt<0>(); // the trailing (empty) loads target a stage about to be reused
+        wbeg = wend;
+    }
 }
 
 __device__ __forceinline__ uint32_t owner_of(uint32_t blk, uint32_t N, uint32_t B) {
     return (uint32_t)((((uint64_t)blk + 1) * N - 1) / B);
+}
+
+// Canonical NaN of a 16-bit pool element, as a round trip through f32 produces it (the
+// append converts every element src -> f32 -> pool dtype with round-to-nearest-even).
+template <int KVT>
+__device__ __forceinline__ uint32_t canon16x2(uint32_t w) {
+    uint32_t r = 0;
+#pragma unroll
+    for (int h = 0; h < 2; h++) {
+        const uint32_t x = (w >> (16 * h)) & 0xffffu;
+        uint32_t y = x;
+        if constexpr (KVT == LIA_BF16) {
+            if ((x & 0x7fffu) > 0x7f80u) y = (x & 0x8000u) | 0x7fc0u;
+        } else {
+            if ((x & 0x7fffu) > 0x7c00u) y = (x & 0x8000u) | 0x7e00u;
+        }
+        r |= y << (16 * h);
+    }
+    return r;
+}
+
+// Fused append: scatter the step's new K/V rows into the pool (16-byte pieces spread over
+// the launch's workgroups).  No workgroup of the launch reads these slots: every range over
+// the new keys reads the caller's rows.
+template <int D, int KVT>
+__device__ __forceinline__ void append_rows(const AttnParams &p, uint32_t wg, uint32_t N) {
+    using C = Cfg<D, KVT>;
+    const uint32_t row_bytes = p.hkv * D * C::EB;
+    const uint32_t pieces = row_bytes / 16;
+    const uint32_t total = p.n_rows * pieces * 2;
+    for (uint32_t i = wg * C::THREADS + threadIdx.x; i < total; i += N * C::THREADS) {
+        const uint32_t plane = i / (p.n_rows * pieces), rem = i % (p.n_rows * pieces);
+        const uint32_t r = rem / pieces, k = rem % pieces;
+        const uint32_t slot = p.slots[r];
+        if (slot == kNone) continue;
+        const u32x4 *src = (const u32x4 *)((const uint8_t *)(plane ? p.newv : p.newk) + (size_t)r * row_bytes) + k;
+        u32x4 *dst = (u32x4 *)((uint8_t *)(plane ? p.vc_w : p.kc_w) + (size_t)slot * row_bytes) + k;
+        u32x4 x = *src;
+        *dst = u32x4{canon16x2<KVT>(x.x), canon16x2<KVT>(x.y), canon16x2<KVT>(x.z), canon16x2<KVT>(x.w)};
+    }
 }
 
 template <int D, int NT, int KVT>
@@ -476,7 +670,7 @@ __global__ __launch_bounds__(D / 32 * 64) void attention_kernel(AttnParams p) {
     // scores are exchanged through two alternating buffers (one barrier per chunk).
     __shared__ __attribute__((aligned(16))) uint16_t vst0[C::WAVES * C::STAGE];
     __shared__ __attribute__((aligned(16))) uint16_t vst1[C::WAVES * C::STAGE];
-    __shared__ f32x4 sxb[2][C::WAVES * NT * 2 * 64];
+    __shared__ f32x4 sxb[2 * C::WAVES * NT * 2 * 64];
     const uint32_t wg = blockIdx.x;
     const uint32_t N = p.header[2];
     if (wg >= N) return;
@@ -485,61 +679,82 @@ __global__ __launch_bounds__(D / 32 * 64) void attention_kernel(AttnParams p) {
     const uint32_t g = lane >> 4, li = lane & 15;
     uint16_t *stage0 = vst0 + wave * C::STAGE;
     uint16_t *stage1 = vst1 + wave * C::STAGE;
-    const uint4 wd = p.wg_desc[wg];
-    uint32_t u = wd.x, lo = wd.y;
-    const uint32_t hi = wd.z, U = p.header[0];
+    const WorkDesc wd = p.work[wg];
+    uint32_t u = wd.unit, lo = wd.lo;
+    const uint32_t hi = wd.hi, U = p.header[0];
+    const bool fused = p.newk != nullptr;
+    const uint32_t row_bytes = p.hkv * D * C::EB;
     uint32_t parity = 0; // alternates the score-exchange buffer across all chunks
+    bool first = true;
 
     while (lo < hi && u < U) {
-        const UnitDesc ud = p.units[u];
-        const uint32_t uend = ud.block_start + ud.nblocks;
+        UnitDesc ud;
+        if (first) ud = wd.first;
+        else ud = p.units[u];
+        const bool use_pre = first && wd.npre;
+        first = false;
+        const uint32_t bs = ud.block_start, uend = bs + ud.nblocks;
         if (uend <= lo) { u++; continue; }
         const uint32_t seg_end = min(hi, uend);
-        const uint32_t hk = ud.hk;
+        const uint32_t hk = unit_head(ud), nrows = unit_rows(ud);
         const uint32_t *table = p.pages + (size_t)ud.table_row * p.stride;
-        const uint32_t kend = ud.kend;
-        const uint32_t ncols = ud.nrows * p.group;
+        const uint32_t kend = ud.kend, kcache = ud.kcache, cb = ud.cblocks;
+        const uint32_t pos0 = kend - nrows;
+        const uint32_t ncols = nrows * p.group;
 
         State<D, NT, KVT> st;
+        uint32_t climit[NT]; // per column: keys it attends (causal limit), 0 for padding
 #pragma unroll
         for (int nt = 0; nt < NT; nt++) {
             const uint32_t col = nt * 16 + li;
             const bool valid = col < ncols;
             const uint32_t ri = valid ? col / p.group : 0;
-            st.lim[nt] = valid ? ud.pos0 + ri + 1 : 0;
+            climit[nt] = valid ? pos0 + ri + 1 : 0;
             st.qr[nt] = load_q<D, KVT>(p, ud.rowbeg + ri, hk * p.group + col % p.group, valid, wave);
             st.m[nt] = -INFINITY;
             st.l[nt] = 0.0f;
             st.o[nt][0] = st.o[nt][1] = f32x4{0.0f, 0.0f, 0.0f, 0.0f};
         }
-
-        const uint32_t tbeg = (lo - ud.block_start) * 32;
-        const uint32_t tend = min((seg_end - ud.block_start) * 32, kend);
-        const uint32_t page_limit = (kend + (1u << p.page_shift) - 1) >> p.page_shift;
-        // Windows of at most 64 pages: each lane holds one page id.
-        for (uint32_t wbeg = tbeg; wbeg < tend;) {
-            const uint32_t wend = min(tend, ((wbeg >> p.page_shift) + 64) << p.page_shift);
-            PageWindow win;
-            window_load<C::FP8>(p, win, table, wbeg >> p.page_shift, page_limit, hk);
-            Chunk<D, KVT> c0, c1;
-            load_chunk<D, KVT>(p, c0, wbeg, win, hk, wend, wave, stage0);
-            for (uint32_t t = wbeg;; t += 64) {
-                // loads past wend carry no traffic
-                pipeline_step<D, NT, KVT>(p, c1, t + 32, stage1, c0, t, stage0, win, hk, wend, wave,
-                                          st, sxb[parity]);
-                parity ^= 1;
-                if (t + 32 >= wend) break;
-                pipeline_step<D, NT, KVT>(p, c0, t + 64, stage0, c1, t + 32, stage1, win, hk, wend,
-                                          wave, st, sxb[parity]);
-                parity ^= 1;
-                if (t + 64 >= wend) break;
+        // Block i of the unit covers keys [32i, 32i+32) of the cached run for i < cb and
+        // [kcache + 32(i-cb), ...) of the new run otherwise.
+        const uint32_t a = lo - bs, e = seg_end - bs;
+        auto key_of = [&](uint32_t i) { return i < cb ? 32 * i : min(kcache + 32 * (i - cb), kend); };
+        auto set_limits = [&](uint32_t r_lo, uint32_t r_hi, uint32_t origin) {
+            st.lo = r_lo;
+#pragma unroll
+            for (int nt = 0; nt < NT; nt++) {
+                const int w = (int)min(climit[nt] - origin, r_hi) - (int)r_lo;
+                st.lim[nt] = climit[nt] && w > 0 ? (uint32_t)w : 0u;
             }
-            wait_vmcnt<0>(); // the trailing (empty) loads target a stage about to be reused
-            wbeg = wend;
+        };
+        const uint8_t *kpool = (const uint8_t *)p.kc, *vpool = (const uint8_t *)p.vc;
+        if (!fused) {
+            // both runs from the pool: one contiguous key range
+            const uint32_t r_lo = key_of(a), r_hi = min(key_of(e), kend);
+            set_limits(r_lo, r_hi, 0);
+            run_range<D, NT, KVT>(p, kpool, vpool, table, r_lo, r_hi, use_pre, wd.pre, hk, wave, st,
+                                  stage0, stage1, sxb, parity);
+        } else {
+            if (a < cb) {
+                const uint32_t r_lo = 32 * a, r_hi = min(32 * min(e, cb), kcache);
+                set_limits(r_lo, r_hi, 0);
+                run_range<D, NT, KVT>(p, kpool, vpool, table, r_lo, r_hi, use_pre, wd.pre, hk, wave,
+                                      st, stage0, stage1, sxb, parity);
+            }
+            if (e > cb) {
+                // new keys: row kcache + i of the sequence is packed row r0 + i
+                const uint32_t r0 = ud.rowbeg - (pos0 - kcache);
+                const uint32_t r_lo = 32 * (max(a, cb) - cb), r_hi = min(32 * (e - cb), kend - kcache);
+                set_limits(r_lo, r_hi, kcache);
+                run_range<D, NT, KVT>(p, (const uint8_t *)p.newk + (size_t)r0 * row_bytes,
+                                      (const uint8_t *)p.newv + (size_t)r0 * row_bytes, nullptr,
+                                      r_lo, r_hi, false, wd.pre, hk, wave, st, stage0, stage1, sxb,
+                                      parity);
+            }
         }
 
         // Finalise this wave's d slice: normalised output or a split record.
-        const bool whole = lo == ud.block_start && seg_end == uend;
+        const bool whole = lo == bs && seg_end == uend;
         const uint32_t rec = wg + u;
 #pragma unroll
         for (int nt = 0; nt < NT; nt++) {
@@ -577,6 +792,9 @@ __global__ __launch_bounds__(D / 32 * 64) void attention_kernel(AttnParams p) {
         lo = seg_end;
         u++;
     }
+    if constexpr (!C::FP8) {
+        if (fused) append_rows<D, KVT>(p, wg, N);
+    }
 }
 
 // Merge the partial records of every unit that was split across workgroups.  Weights
@@ -600,7 +818,7 @@ __global__ __launch_bounds__(kCombineThreads) void combine_kernel(AttnParams p) 
     const uint32_t wf = owner_of(ud.block_start, N, B);
     const uint32_t wl = owner_of(ud.block_start + ud.nblocks - 1, N, B);
     if (wf == wl) return; // written directly by its only workgroup
-    if (col >= ud.nrows * p.group) return;
+    if (col >= unit_rows(ud) * p.group) return;
     constexpr uint32_t COLS = 16 * NT;
     const uint32_t n = wl - wf + 1;
     const uint32_t rec0 = wf + u;
@@ -653,7 +871,7 @@ __global__ __launch_bounds__(kCombineThreads) void combine_kernel(AttnParams p) 
     if (grp != 0) return;
     for (uint32_t k = 1; k < GROUPS; k++) num += red[k * D + d];
     const float v = den > 0.0f ? num / den : 0.0f;
-    const uint32_t row = ud.rowbeg + col / p.group, head = ud.hk * p.group + col % p.group;
+    const uint32_t row = ud.rowbeg + col / p.group, head = unit_head(ud) * p.group + col % p.group;
     const size_t at = ((size_t)row * p.hq + head) * D + d;
     if (p.out_f32) ((float *)p.out)[at] = v;
     else ((uint16_t *)p.out)[at] = f32_to_bf16(v);
@@ -662,7 +880,7 @@ __global__ __launch_bounds__(kCombineThreads) void combine_kernel(AttnParams p) 
 // ------------------------------------------------------------------ host side
 
 struct Layout {
-    size_t header, units, wg_desc, part_ml, part_o, total;
+    size_t header, units, work, part_ml, part_o, total;
     uint32_t max_units, max_records;
 };
 
@@ -682,7 +900,7 @@ static Layout layout_for(const lia_attention_config *c, uint32_t n_wg) {
     L.header = off; off += 256;
     L.units = off; off += ((size_t)L.max_units + 1) * sizeof(UnitDesc);
     off = (off + 255) & ~(size_t)255;
-    L.wg_desc = off; off += (size_t)n_wg * sizeof(uint4);
+    L.work = off; off += (size_t)n_wg * sizeof(WorkDesc);
     off = (off + 255) & ~(size_t)255;
     L.part_ml = off; off += (size_t)L.max_records * 32 * 2 * sizeof(float);
     off = (off + 255) & ~(size_t)255;
@@ -794,12 +1012,18 @@ static void launch_partial_kv(int kv, const AttnParams &p, uint32_t n_wg, hipStr
 
 enum Stage { kPlan = 1, kPartial = 2, kMerge = 4 };
 
+// New rows appended by the attention launch itself (lia_attention_partial_append).
+struct FusedAppend {
+    const void *k, *v;
+    const uint32_t *slots;
+};
+
 static int run_stages(int stages, const lia_attention_config *c, uint32_t n_seqs, uint32_t n_rows,
                       const uint32_t *cu_seqlens, const uint32_t *positions,
                       const uint32_t *sequences, const uint32_t *pages, const void *q,
                       const void *kc, const void *vc, const float *k_scales,
                       const float *v_scales, void *workspace, size_t workspace_bytes, void *out,
-                      lia_stream_t stream) {
+                      lia_stream_t stream, const FusedAppend *fa = nullptr) {
     int st = validate(c);
     if (st) return st;
     if (n_seqs == 0 || n_seqs > c->max_seqs || n_rows == 0 || n_rows > c->max_rows) return LIA_E_ARG;
@@ -808,6 +1032,11 @@ static int run_stages(int stages, const lia_attention_config *c, uint32_t n_seqs
     if (stages & (kPartial | kMerge)) {
         if (!out) return LIA_E_ARG;
         if ((uintptr_t)out & 15) return LIA_E_ALIGN;
+    }
+    if (fa) {
+        if (c->kv_dtype == LIA_FP8_E4M3) return LIA_E_UNSUPPORTED;
+        if (!fa->k || !fa->v || !fa->slots) return LIA_E_ARG;
+        if (((uintptr_t)fa->k | (uintptr_t)fa->v) & 15) return LIA_E_ALIGN;
     }
     if (stages & kPartial) {
         if (!pages || !q || !kc || !vc) return LIA_E_ARG;
@@ -827,7 +1056,7 @@ static int run_stages(int stages, const lia_attention_config *c, uint32_t n_seqs
     p.cu = cu_seqlens; p.positions = positions; p.sequences = sequences; p.pages = pages;
     p.out = out;
     p.units = (const UnitDesc *)(ws + L.units);
-    p.wg_desc = (const uint4 *)(ws + L.wg_desc);
+    p.work = (const WorkDesc *)(ws + L.work);
     p.header = (const uint32_t *)(ws + L.header);
     p.part_o = (float *)(ws + L.part_o);
     p.part_ml = (float *)(ws + L.part_ml);
@@ -838,11 +1067,17 @@ static int run_stages(int stages, const lia_attention_config *c, uint32_t n_seqs
     p.scale_log2 = c->scale * 1.4426950408889634f;
     p.q_f32 = c->q_dtype == LIA_F32;
     p.out_f32 = c->out_dtype == LIA_F32;
+    p.newk = fa ? fa->k : nullptr;
+    p.newv = fa ? fa->v : nullptr;
+    p.slots = fa ? fa->slots : nullptr;
+    p.kc_w = const_cast<void *>(kc);
+    p.vc_w = const_cast<void *>(vc);
+    p.n_rows = n_rows;
     hipStream_t s = (hipStream_t)stream;
     if (stages & kPlan)
         hipLaunchKernelGGL(plan_kernel, dim3(1), dim3(256), 0, s, n_seqs, cu_seqlens, positions,
-                           sequences, rpc, c->num_kv_heads, L.max_units, n_wg,
-                           (UnitDesc *)(ws + L.units), (uint4 *)(ws + L.wg_desc),
+                           sequences, pages, c->stride, p.page_shift, rpc, c->num_kv_heads,
+                           L.max_units, n_wg, (UnitDesc *)(ws + L.units), (WorkDesc *)(ws + L.work),
                            (uint32_t *)(ws + L.header));
     if (stages & kPartial) {
         if (c->head_dim == 128) {
@@ -879,9 +1114,9 @@ extern "C" int lia_paged_attention(const lia_attention_config *c, uint32_t n_seq
 
 extern "C" int lia_attention_plan(const lia_attention_config *c, uint32_t n_seqs, uint32_t n_rows,
                                   const uint32_t *cu_seqlens, const uint32_t *positions,
-                                  const uint32_t *sequences, void *workspace,
-                                  size_t workspace_bytes, lia_stream_t stream) {
-    return run_stages(kPlan, c, n_seqs, n_rows, cu_seqlens, positions, sequences, nullptr,
+                                  const uint32_t *sequences, const uint32_t *pages,
+                                  void *workspace, size_t workspace_bytes, lia_stream_t stream) {
+    return run_stages(kPlan, c, n_seqs, n_rows, cu_seqlens, positions, sequences, pages,
                       nullptr, nullptr, nullptr, nullptr, nullptr, workspace, workspace_bytes,
                       nullptr, stream);
 }
@@ -895,6 +1130,18 @@ extern "C" int lia_attention_partial(const lia_attention_config *c, uint32_t n_s
     static const uint32_t dummy = 0;
     return run_stages(kPartial, c, n_seqs, n_rows, &dummy, &dummy, nullptr, pages, q, kc, vc,
                       k_scales, v_scales, workspace, workspace_bytes, out, stream);
+}
+
+extern "C" int lia_attention_partial_append(const lia_attention_config *c, uint32_t n_seqs,
+                                            uint32_t n_rows, const uint32_t *pages,
+                                            const uint32_t *slot_mapping, const void *q,
+                                            const void *new_k, const void *new_v, void *kc,
+                                            void *vc, void *workspace, size_t workspace_bytes,
+                                            void *out, lia_stream_t stream) {
+    static const uint32_t dummy = 0;
+    const FusedAppend fa{new_k, new_v, slot_mapping};
+    return run_stages(kPartial, c, n_seqs, n_rows, &dummy, &dummy, nullptr, pages, q, kc, vc,
+                      nullptr, nullptr, workspace, workspace_bytes, out, stream, &fa);
 }
 
 extern "C" int lia_attention_merge(const lia_attention_config *c, uint32_t n_seqs, uint32_t n_rows,

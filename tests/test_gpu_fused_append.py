@@ -1,0 +1,134 @@
+"""GPU parity of lia_attention_partial_append (KV append fused into the attention launch).
+
+Each case takes a batch whose pool already holds every key (the CPU oracle's input), lifts
+the step's new rows out of the pool into new_k / new_v, overwrites their pool slots with
+garbage on the device and runs plan -> partial_append -> merge.  The output must match the
+float64 oracle on the original pool (same tolerances as the unfused path) and the pool
+afterwards must equal the original bytes, i.e. what lia_kv_append writes."""
+import numpy as np
+import pytest
+import torch
+
+import gpu_data as G
+from gpu_data import BF16, F16, F32, FP8
+
+pytestmark = pytest.mark.gpu
+
+TOL = {BF16: (2e-2, 2e-3), F16: (2e-2, 2e-3)}
+
+
+def _run_fused(case, lia, seed, garbage=True):
+    b, g = case.batch, case.g
+    dev = case.device()
+    W = g.hkv * g.d
+    slots = b.slot_mapping().astype(np.int64)
+    kc = case.kc.reshape(-1, W)
+    vc = case.vc.reshape(-1, W)
+    newk, newv = kc[slots].copy(), vc[slots].copy()
+    dkc, dvc = dev["kc"].view(-1, W), dev["vc"].view(-1, W)
+    if garbage:
+        rng = np.random.default_rng(seed + 7)
+        junk = rng.integers(0, 65535, newk.shape).astype(np.uint16)
+        idx = torch.from_numpy(slots).cuda()
+        dkc[idx] = G.to_dev(junk, torch.int16)
+        dvc[idx] = G.to_dev(junk[::-1].copy(), torch.int16)
+    cfg = case.config(lia)
+    ws = torch.zeros(lia.workspace_bytes(cfg), dtype=torch.uint8, device="cuda")
+    odt = torch.float32 if g.out_dtype == F32 else torch.bfloat16
+    out = torch.full((b.n_rows, g.hq, g.d), float("nan"), dtype=odt, device="cuda")
+    lia.attention_plan(cfg, b.n_seqs, b.n_rows, dev["cu"], dev["positions"], dev["sequences"], ws,
+                       pages=dev["pages"])
+    lia.attention_partial_append(cfg, b.n_seqs, dev["pages"], G.u32_dev(slots), dev["q"],
+                                 G.to_dev(newk, torch.int16), G.to_dev(newv, torch.int16),
+                                 dev["kc"], dev["vc"], out, ws)
+    lia.attention_merge(cfg, b.n_seqs, b.n_rows, out, ws)
+    torch.cuda.synchronize()
+    return (out.float().cpu().numpy(), dev["kc"].cpu().numpy().view(np.uint16),
+            dev["vc"].cpu().numpy().view(np.uint16))
+
+
+def _check(case, lia, label, seed):
+    print(f"[case] fused {label}: seqs={case.batch.n_seqs} rows={case.batch.n_rows} "
+          f"ctx={case.batch.ctx.tolist()[:8]} q_len={case.batch.q_len.tolist()[:8]}", flush=True)
+    got, kpool, vpool = _run_fused(case, lia, seed)
+    ref = case.f64()
+    mx, mean = G.errors(got, ref)
+    print(f"[case] fused {label}: max_abs={mx:.3e} mean_abs={mean:.3e}", flush=True)
+    assert np.all(np.isfinite(got)), label
+    tol_max, tol_mean = TOL[case.g.kv_dtype]
+    assert mx < tol_max and mean < tol_mean, (label, mx, mean)
+    assert np.array_equal(kpool, case.kc) and np.array_equal(vpool, case.vc), label
+
+
+def test_fused_config2_decode(lia, wl):
+    _check(G.Case(wl.config2(seed=0, layers=1), seed=0), lia, "cfg2", 0)
+
+
+@pytest.mark.parametrize("kv", [BF16, F16])
+@pytest.mark.parametrize("d,hq,hkv,page", [(128, 16, 2, 16), (64, 8, 2, 32), (128, 32, 2, 64)])
+def test_fused_decode_edge_contexts(lia, wl, kv, d, hq, hkv, page):
+    ctx = [1, 2, 15, 16, 17, 31, 32, 33, 63, 64, 65, 100, 511, 1000, 2049, 4097]
+    g = wl.Geometry(hq=hq, hkv=hkv, d=d, page_size=page, kv_dtype=kv, q_dtype=F32, out_dtype=F32)
+    b = wl.custom(ctx, [1] * len(ctx), geom=g, seed=13)
+    _check(G.Case(b, seed=13), lia, f"edge kv={kv} d={d} page={page}", 13)
+
+
+def test_fused_mtp_verify(lia, wl):
+    rng = np.random.default_rng(14)
+    k = rng.integers(1, 4, size=12)
+    ctx = rng.integers(20, 3000, size=12)
+    _check(G.Case(wl.custom(ctx, 1 + k, seed=14), seed=14), lia, "mtp", 14)
+
+
+@pytest.mark.parametrize("hq,hkv", [(16, 2), (8, 8), (32, 2), (16, 1)])
+def test_fused_prefill_chunks(lia, wl, hq, hkv):
+    """Prefill from scratch (no cached keys), prefix-cached chunks whose new keys span
+    many blocks and column blocks, and decode rows in one batch."""
+    g = wl.Geometry(hq=hq, hkv=hkv, d=128)
+    ctx = [64, 300 + 130, 1000 + 200, 777, 1500, 33, 97]
+    q = [64, 130, 200, 1, 1, 1, 97]
+    _check(G.Case(wl.custom(ctx, q, geom=g, seed=15), seed=15), lia, f"prefill hq={hq} hkv={hkv}", 15)
+
+
+def test_fused_matches_unfused(lia, wl):
+    """Same output as kv_append + partial + merge to within accumulation order."""
+    b = wl.custom([5000, 17, 900, 64], [1, 1, 3, 64], seed=16)
+    case = G.Case(b, seed=16)
+    fused, _, _ = _run_fused(case, lia, 16)
+    plain = case.run(lia)
+    assert np.max(np.abs(fused - plain)) < 1e-2
+
+
+@pytest.mark.parametrize("kv", [BF16, F16])
+def test_fused_append_canonicalises_nan_like_kv_append(lia, wl, O, kv):
+    """NaN payloads in the new rows land in the pool exactly as lia_kv_append stores
+    them (canonical quiet NaN with the sign kept); other values are copied unchanged."""
+    g = wl.Geometry(hq=16, hkv=2, d=128, kv_dtype=kv)
+    b = wl.custom([40, 700], [3, 1], geom=g, seed=17)
+    case = G.Case(b, seed=17)
+    W = g.hkv * g.d
+    slots = b.slot_mapping().astype(np.int64)
+    rng = np.random.default_rng(17)
+    newk = case.kc.reshape(-1, W)[slots].copy()
+    newv = case.vc.reshape(-1, W)[slots].copy()
+    nan = 0x7f81 if kv == BF16 else 0x7c01
+    for arr in (newk, newv):
+        pick = rng.choice(arr.size, 50, replace=False)
+        arr.reshape(-1)[pick] = (nan + rng.integers(0, 60, 50)) | (rng.integers(0, 2, 50) << 15)
+    # expected pool: the oracle append (src dtype = pool dtype) into the original pool
+    kexp, vexp = case.kc.copy(), case.vc.copy()
+    layout = O.KVLayout(g.hkv, g.d, g.page_size, b.pool_pages, kv)
+    O.kv_append(layout, b.positions(), b.sequences(), b.flat_table(), b.stride, newk, newv,
+                kexp, vexp, src_dtype=kv, slot_mapping=b.slot_mapping())
+    dev = case.device()
+    cfg = case.config(lia)
+    ws = torch.zeros(lia.workspace_bytes(cfg), dtype=torch.uint8, device="cuda")
+    out = torch.empty((b.n_rows, g.hq, g.d), dtype=torch.bfloat16, device="cuda")
+    lia.attention_plan(cfg, b.n_seqs, b.n_rows, dev["cu"], dev["positions"], dev["sequences"], ws,
+                       pages=dev["pages"])
+    lia.attention_partial_append(cfg, b.n_seqs, dev["pages"], G.u32_dev(b.slot_mapping()),
+                                 dev["q"], G.to_dev(newk, torch.int16), G.to_dev(newv, torch.int16),
+                                 dev["kc"], dev["vc"], out, ws)
+    torch.cuda.synchronize()
+    assert np.array_equal(dev["kc"].cpu().numpy().view(np.uint16), kexp)
+    assert np.array_equal(dev["vc"].cpu().numpy().view(np.uint16), vexp)

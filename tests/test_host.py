@@ -124,3 +124,23 @@ def test_workload_shapes(wl):
     assert list(b1.ctx) == [17, 64, 200, 511]
     used = np.concatenate(b1.tables)
     assert len(np.unique(used)) == len(used) == 2 + 4 + 13 + 32
+
+
+def test_partial_append_validates_before_launch(lia):
+    """The fused-append entry point rejects FP8 pools, missing rows and unaligned rows
+    before it touches the device."""
+    F16, FP8 = 1, 3
+    ws = (C.c_uint8 * 4096)()
+    fake = C.c_void_p(0x10000)
+    odd = C.c_void_p(0x10008)
+
+    def call(kv, new_k, slots):
+        cfg = lia.AttentionConfig(16, 2, 128, 16, 64, 8, 2, kv, 2, 0.088, 4, 4, 128)
+        return lia.lib().lia_attention_partial_append(
+            C.byref(cfg), 2, 2, fake, slots, fake, new_k, fake, fake, fake, C.cast(ws, C.c_void_p),
+            4096, fake, None)
+
+    assert call(FP8, fake, fake) == -23
+    assert call(F16, None, fake) == -20
+    assert call(F16, fake, None) == -20
+    assert call(F16, odd, fake) == -21
