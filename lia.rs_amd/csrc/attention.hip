@@ -62,6 +62,14 @@ struct WorkDesc {
     uint4 pre;                // pages of logical pages (32 * (lo - first.block_start)) / P + 0..3
 };
 
+// Per-unit merge descriptor (16 bytes): the records the combine reads, n = 0 when one
+// workgroup wrote the unit directly (or the unit does not exist in this plan).
+struct MergeDesc {
+    uint32_t rec0, n;     // records rec0 .. rec0 + n - 1
+    uint32_t rowbeg;      // as in UnitDesc
+    uint32_t nrows_hk;
+};
+
 struct AttnParams {
     const void *q;
     const void *kc;
@@ -74,11 +82,12 @@ struct AttnParams {
     const uint32_t *pages;
     void *out;
     const UnitDesc *units;   // [U + 1]; units[U].block_start = B
-    const WorkDesc *work;    // per workgroup
+    const WorkDesc *work;    // per launched workgroup (empty ranges past the planned count)
+    const MergeDesc *merge;  // per unit slot of the workspace
     const uint32_t *header;  // {U, B, N (workgroups with work), overflow}
     float *part_o;           // [records][cols][D]
     float *part_ml;          // [records][cols][2]
-    uint32_t hq, hkv, group, stride, page_shift, n_wg, rpc;
+    uint32_t hq, hkv, group, stride, page_shift, n_wg, rpc, pool_pages;
     float scale_log2;        // softmax scale * log2(e)
     int q_f32, out_f32;
     // fused append (null when the new rows are already in the pool)
@@ -107,7 +116,7 @@ __global__ __launch_bounds__(256) void plan_kernel(uint32_t n_seqs, const uint32
                                                    uint32_t stride, uint32_t page_shift, uint32_t rpc,
                                                    uint32_t hkv, uint32_t max_units,
                                                    uint32_t n_wg, UnitDesc *units, WorkDesc *work,
-                                                   uint32_t *header) {
+                                                   MergeDesc *merge, uint32_t *header) {
     __shared__ uint32_t s_units[256], s_blocks[256];
     __shared__ uint32_t carry_units, carry_blocks, overflow;
     const uint32_t t = threadIdx.x;
@@ -171,6 +180,20 @@ __global__ __launch_bounds__(256) void plan_kernel(uint32_t n_seqs, const uint32
     __threadfence();
     __syncthreads();
     const uint32_t P = 1u << page_shift;
+    for (uint32_t w = N + t; w < n_wg; w += 256) { // launched workgroups without work
+        WorkDesc d = {};
+        work[w] = d;
+    }
+    for (uint32_t u = t; u < max_units; u += 256) {
+        MergeDesc m = {0, 0, 0, 0};
+        if (u < U) {
+            const UnitDesc ud = units[u];
+            const uint32_t wf = (uint32_t)((((uint64_t)ud.block_start + 1) * N - 1) / B);
+            const uint32_t wl = (uint32_t)((((uint64_t)ud.block_start + ud.nblocks) * N - 1) / B);
+            if (wf != wl) m = MergeDesc{wf + u, wl - wf + 1, ud.rowbeg, ud.nrows_hk};
+        }
+        merge[u] = m;
+    }
     for (uint32_t w = t; w < N; w += 256) {
         uint32_t lo = (uint32_t)((uint64_t)w * B / N), hi = (uint32_t)((uint64_t)(w + 1) * B / N);
         uint32_t a = 0, e = U; // last unit whose first block <= lo
@@ -247,6 +270,8 @@ struct PageWindow {
     float ks, vs;   // per lane: FP8 scales of that page
 };
 
+// Unconditional bounded loads (entries past `limit` read as zero): a load under a branch
+// would be waited for at the branch's join, ahead of the first K/V loads.
 template <bool FP8>
 __device__ __forceinline__ void window_load(const AttnParams &p, PageWindow &w,
                                             const uint32_t *table, uint32_t first, uint32_t limit,
@@ -258,10 +283,12 @@ __device__ __forceinline__ void window_load(const AttnParams &p, PageWindow &w,
         w.ks = w.vs = 1.0f;
         return;
     }
-    w.page = idx < limit ? table[idx] : 0u;
+    w.page = (uint32_t)__builtin_amdgcn_raw_buffer_load_b32(make_rsrc(table, limit * 4), (int)(idx * 4), 0, 0);
     if constexpr (FP8) {
-        w.ks = idx < limit ? p.k_scales[(size_t)w.page * p.hkv + hk] : 0.0f;
-        w.vs = idx < limit ? p.v_scales[(size_t)w.page * p.hkv + hk] : 0.0f;
+        const uint32_t n = p.pool_pages * p.hkv * 4;
+        const uint32_t off = idx < limit ? (w.page * p.hkv + hk) * 4 : 0x80000000u;
+        w.ks = __builtin_bit_cast(float, __builtin_amdgcn_raw_buffer_load_b32(make_rsrc(p.k_scales, n), (int)off, 0, 0));
+        w.vs = __builtin_bit_cast(float, __builtin_amdgcn_raw_buffer_load_b32(make_rsrc(p.v_scales, n), (int)off, 0, 0));
     }
 }
 
@@ -395,24 +422,27 @@ __device__ __forceinline__ void load_chunk(const AttnParams &p, Chunk<D, KVT> &c
 }
 
 // Query operand of one 16-column tile for this wave's d slice: lane (g, col) holds
-// q[col][32w + 8g .. +7] - the dims the K loads put in the same k slots.
+// q[col][32w + 8g .. +7] - the dims the K loads put in the same k slots.  Padding columns
+// load from an out-of-range offset (zeros) so the loads are unconditional.
 template <int D, int KVT>
 __device__ __forceinline__ u32x4 load_q(const AttnParams &p, uint32_t row, uint32_t head,
                                         bool valid, uint32_t wave) {
     using C = Cfg<D, KVT>;
     const uint32_t g = lane_id() >> 4;
-    const size_t at = ((size_t)row * p.hq + head) * D + 32 * wave + 8 * g;
+    const uint32_t at = (row * p.hq + head) * D + 32 * wave + 8 * g;
+    const uint32_t qb = p.q_f32 ? 4 : 2;
+    const __amdgpu_buffer_rsrc_t r = make_rsrc(p.q, p.n_rows * p.hq * D * qb);
+    const uint32_t off = valid ? at * qb : 0x80000000u;
     float x[8];
-    if (!valid) {
-#pragma unroll
-        for (int e = 0; e < 8; e++) x[e] = 0.0f;
-    } else if (p.q_f32) {
-        const float4 *src = (const float4 *)((const float *)p.q + at);
-        float4 a = src[0], b = src[1];
+    if (p.q_f32) {
+        // Cast the whole vector: with this toolchain, bit-casting single elements of a
+        // 128-bit buffer load to float narrows the load to its first dword.
+        const f32x4 a = __builtin_bit_cast(f32x4, buffer_load16(r, off));
+        const f32x4 b = __builtin_bit_cast(f32x4, buffer_load16(r, off + 16));
         x[0] = a.x; x[1] = a.y; x[2] = a.z; x[3] = a.w;
         x[4] = b.x; x[5] = b.y; x[6] = b.z; x[7] = b.w;
     } else {
-        u32x4 w = *(const u32x4 *)((const uint16_t *)p.q + at);
+        const u32x4 w = buffer_load16(r, off);
         if constexpr (C::MBF16) return w;
 #pragma unroll
         for (int e = 0; e < 4; e++) {
@@ -617,10 +647,6 @@ __device__ __forceinline__ void run_range(const AttnParams &p, const uint8_t *kb
     }
 }
 
-__device__ __forceinline__ uint32_t owner_of(uint32_t blk, uint32_t N, uint32_t B) {
-    return (uint32_t)((((uint64_t)blk + 1) * N - 1) / B);
-}
-
 // Canonical NaN of a 16-bit pool element, as a round trip through f32 produces it (the
 // append converts every element src -> f32 -> pool dtype with round-to-nearest-even).
 template <int KVT>
@@ -672,22 +698,21 @@ __global__ __launch_bounds__(D / 32 * 64) void attention_kernel(AttnParams p) {
     __shared__ __attribute__((aligned(16))) uint16_t vst1[C::WAVES * C::STAGE];
     __shared__ f32x4 sxb[2 * C::WAVES * NT * 2 * 64];
     const uint32_t wg = blockIdx.x;
-    const uint32_t N = p.header[2];
-    if (wg >= N) return;
+    const WorkDesc wd = p.work[wg]; // the only load before the first K/V loads
     const uint32_t tid = threadIdx.x, lane = tid & 63;
     const uint32_t wave = (uint32_t)__builtin_amdgcn_readfirstlane((int)(tid >> 6)); // SGPR
     const uint32_t g = lane >> 4, li = lane & 15;
     uint16_t *stage0 = vst0 + wave * C::STAGE;
     uint16_t *stage1 = vst1 + wave * C::STAGE;
-    const WorkDesc wd = p.work[wg];
     uint32_t u = wd.unit, lo = wd.lo;
-    const uint32_t hi = wd.hi, U = p.header[0];
+    const uint32_t hi = wd.hi;
     const bool fused = p.newk != nullptr;
     const uint32_t row_bytes = p.hkv * D * C::EB;
     uint32_t parity = 0; // alternates the score-exchange buffer across all chunks
     bool first = true;
 
-    while (lo < hi && u < U) {
+    // the plan guarantees a unit covers every block of a non-empty range
+    while (lo < hi) {
         UnitDesc ud;
         if (first) ud = wd.first;
         else ud = p.units[u];
@@ -793,94 +818,113 @@ __global__ __launch_bounds__(D / 32 * 64) void attention_kernel(AttnParams p) {
         u++;
     }
     if constexpr (!C::FP8) {
-        if (fused) append_rows<D, KVT>(p, wg, N);
+        if (fused) append_rows<D, KVT>(p, wg, gridDim.x);
     }
 }
 
 // Merge the partial records of every unit that was split across workgroups.  Weights
 // follow the reference merge: a record with zero mass contributes nothing, the others
 // are scaled by 2^(m_r - M) (m in the log2 domain here), out = sum w o / sum w l
-// (src/gpu/kernels/llama.rs:201-290).  One workgroup per (unit, column): the record
-// weights are reduced in parallel, then kCombineThreads / D groups of threads each
-// accumulate a strided subset of the records for every head_dim element.
-constexpr uint32_t kCombineThreads = 512;
-constexpr uint32_t kCombineMaxRecords = 4096;
+// (src/gpu/kernels/llama.rs:201-290).  One workgroup per (unit, column): D/4 lanes cover a
+// record's row as float4 quads, so 256 threads hold 1024/D records per pass, and a batch of
+// kCombinePasses passes is loaded at once (every load independent of the weights).  Each
+// batch raises the running reference maximum to the batch's, rescaling what came before;
+// the record groups are summed through LDS at the end.
+constexpr uint32_t kCombineThreads = 256;
+constexpr uint32_t kCombinePasses = 8;
+
+__device__ __forceinline__ float wave_max(float v) {
+#pragma unroll
+    for (int m = 32; m >= 1; m >>= 1) v = fmaxf(v, shfl_xor(v, m));
+    return v;
+}
 
 template <int D, int NT>
 __global__ __launch_bounds__(kCombineThreads) void combine_kernel(AttnParams p) {
-    __shared__ float wts[kCombineMaxRecords];
-    __shared__ float red[kCombineThreads];
-    const uint32_t u = blockIdx.x, col = blockIdx.y, t = threadIdx.x;
-    const uint32_t U = p.header[0], B = p.header[1], N = p.header[2];
-    if (u >= U) return;
-    const UnitDesc ud = p.units[u];
-    if (ud.nblocks == 0) return;
-    const uint32_t wf = owner_of(ud.block_start, N, B);
-    const uint32_t wl = owner_of(ud.block_start + ud.nblocks - 1, N, B);
-    if (wf == wl) return; // written directly by its only workgroup
-    if (col >= unit_rows(ud) * p.group) return;
+    constexpr uint32_t Q = D / 4;                  // float4 quads per record row
+    constexpr uint32_t RPP = kCombineThreads / Q;  // records per pass
     constexpr uint32_t COLS = 16 * NT;
-    const uint32_t n = wl - wf + 1;
-    const uint32_t rec0 = wf + u;
-    float M = -INFINITY;
-    for (uint32_t r = t; r < n; r += kCombineThreads) {
-        const size_t rb = (size_t)(rec0 + r) * COLS + col;
-        if (p.part_ml[rb * 2 + 1] > 0.0f) M = fmaxf(M, p.part_ml[rb * 2]);
-    }
-    red[t] = M;
-    __syncthreads();
-    for (uint32_t off = kCombineThreads / 2; off > 0; off >>= 1) {
-        if (t < off) red[t] = fmaxf(red[t], red[t + off]);
+    __shared__ float4 s_num[RPP][Q];
+    __shared__ float s_den[RPP][Q];
+    __shared__ float s_max[2][kCombineThreads / 64];
+    const uint32_t u = blockIdx.x, col = blockIdx.y, t = threadIdx.x;
+    const MergeDesc md = p.merge[u];
+    if (md.n == 0) return; // written directly by its only workgroup, or no such unit
+    if (col >= (md.nrows_hk & 0xffffu) * p.group) return;
+    const uint32_t n = md.n, rec0 = md.rec0;
+    const uint32_t q = t % Q, rg = t / Q;
+    const float4 *po = (const float4 *)p.part_o;
+    float M = -INFINITY, den = 0.0f;
+    float4 num = make_float4(0.0f, 0.0f, 0.0f, 0.0f);
+    uint32_t parity = 0;
+    for (uint32_t base = 0; base < n; base += RPP * kCombinePasses) {
+        float4 o[kCombinePasses];
+        float m[kCombinePasses], l[kCombinePasses];
+#pragma unroll
+        for (uint32_t k = 0; k < kCombinePasses; k++) {
+            // unconditional loads (a clamped index past the end, weighted zero): loads under
+            // a branch would each be waited for at the branch's join
+            const uint32_t r = base + k * RPP + rg;
+            const size_t rb = (size_t)(rec0 + min(r, n - 1)) * COLS + col;
+            o[k] = po[rb * Q + q];
+            const float2 ml = ((const float2 *)p.part_ml)[rb];
+            m[k] = ml.x;
+            l[k] = r < n ? ml.y : 0.0f;
+        }
+        float bm = -INFINITY;
+#pragma unroll
+        for (uint32_t k = 0; k < kCombinePasses; k++)
+            if (l[k] > 0.0f) bm = fmaxf(bm, m[k]);
+        bm = wave_max(bm);
+        if ((t & 63) == 0) s_max[parity][t >> 6] = bm;
         __syncthreads();
+#pragma unroll
+        for (uint32_t w = 0; w < kCombineThreads / 64; w++) bm = fmaxf(bm, s_max[parity][w]);
+        parity ^= 1;
+        const float nm = fmaxf(M, bm);
+        if (nm != M) {
+            const float f = M == -INFINITY ? 0.0f : fast_exp2(M - nm);
+            num.x *= f; num.y *= f; num.z *= f; num.w *= f;
+            den *= f;
+            M = nm;
+        }
+#pragma unroll
+        for (uint32_t k = 0; k < kCombinePasses; k++) {
+            const float w = l[k] > 0.0f ? fast_exp2(m[k] - M) : 0.0f;
+            num.x = fmaf(w, o[k].x, num.x);
+            num.y = fmaf(w, o[k].y, num.y);
+            num.z = fmaf(w, o[k].z, num.z);
+            num.w = fmaf(w, o[k].w, num.w);
+            den = fmaf(w, l[k], den);
+        }
     }
-    M = red[0];
+    // record groups rg share the quad q: sum them (den likewise counts every record once)
+    s_num[rg][q] = num;
+    s_den[rg][q] = den;
     __syncthreads();
-    float den = 0.0f;
-    for (uint32_t r = t; r < n; r += kCombineThreads) {
-        const size_t rb = (size_t)(rec0 + r) * COLS + col;
-        const float mass = p.part_ml[rb * 2 + 1];
-        const float w = mass > 0.0f ? fast_exp2(p.part_ml[rb * 2] - M) : 0.0f;
-        wts[r] = w;
-        den = fmaf(w, mass, den);
+    if (rg != 0) return;
+#pragma unroll
+    for (uint32_t g = 1; g < RPP; g++) {
+        const float4 x = s_num[g][q];
+        num.x += x.x; num.y += x.y; num.z += x.z; num.w += x.w;
+        den += s_den[g][q];
     }
-    red[t] = den;
-    __syncthreads();
-    for (uint32_t off = kCombineThreads / 2; off > 0; off >>= 1) {
-        if (t < off) red[t] += red[t + off];
-        __syncthreads();
+    const float inv = den > 0.0f ? 1.0f / den : 0.0f;
+    const uint32_t row = md.rowbeg + col / p.group, head = (md.nrows_hk >> 16) * p.group + col % p.group;
+    const size_t at = ((size_t)row * p.hq + head) * D + 4 * q;
+    if (p.out_f32) {
+        *(float4 *)((float *)p.out + at) = make_float4(num.x * inv, num.y * inv, num.z * inv, num.w * inv);
+    } else {
+        *(u32x2 *)((uint16_t *)p.out + at) =
+            u32x2{(uint32_t)f32_to_bf16(num.x * inv) | ((uint32_t)f32_to_bf16(num.y * inv) << 16),
+                  (uint32_t)f32_to_bf16(num.z * inv) | ((uint32_t)f32_to_bf16(num.w * inv) << 16)};
     }
-    den = red[0];
-    __syncthreads();
-    constexpr uint32_t GROUPS = kCombineThreads / D;
-    const uint32_t d = t % D, grp = t / D;
-    float num = 0.0f;
-    const float *po = p.part_o + ((size_t)rec0 * COLS + col) * D + d;
-    const size_t step = (size_t)COLS * D;
-    uint32_t r = grp;
-    for (; r + 3 * GROUPS < n; r += 4 * GROUPS) {
-        const float a0 = po[(r + 0 * GROUPS) * step], a1 = po[(r + 1 * GROUPS) * step];
-        const float a2 = po[(r + 2 * GROUPS) * step], a3 = po[(r + 3 * GROUPS) * step];
-        num = fmaf(wts[r + 0 * GROUPS], a0, num);
-        num = fmaf(wts[r + 1 * GROUPS], a1, num);
-        num = fmaf(wts[r + 2 * GROUPS], a2, num);
-        num = fmaf(wts[r + 3 * GROUPS], a3, num);
-    }
-    for (; r < n; r += GROUPS) num = fmaf(wts[r], po[r * step], num);
-    red[t] = num;
-    __syncthreads();
-    if (grp != 0) return;
-    for (uint32_t k = 1; k < GROUPS; k++) num += red[k * D + d];
-    const float v = den > 0.0f ? num / den : 0.0f;
-    const uint32_t row = ud.rowbeg + col / p.group, head = unit_head(ud) * p.group + col % p.group;
-    const size_t at = ((size_t)row * p.hq + head) * D + d;
-    if (p.out_f32) ((float *)p.out)[at] = v;
-    else ((uint16_t *)p.out)[at] = f32_to_bf16(v);
 }
 
 // ------------------------------------------------------------------ host side
 
 struct Layout {
-    size_t header, units, work, part_ml, part_o, total;
+    size_t header, units, work, merge, part_ml, part_o, total;
     uint32_t max_units, max_records;
 };
 
@@ -901,6 +945,8 @@ static Layout layout_for(const lia_attention_config *c, uint32_t n_wg) {
     L.units = off; off += ((size_t)L.max_units + 1) * sizeof(UnitDesc);
     off = (off + 255) & ~(size_t)255;
     L.work = off; off += (size_t)n_wg * sizeof(WorkDesc);
+    off = (off + 255) & ~(size_t)255;
+    L.merge = off; off += (size_t)L.max_units * sizeof(MergeDesc);
     off = (off + 255) & ~(size_t)255;
     L.part_ml = off; off += (size_t)L.max_records * 32 * 2 * sizeof(float);
     off = (off + 255) & ~(size_t)255;
@@ -935,12 +981,22 @@ extern "C" uint32_t lia_device_cus(void) {
     return g_cus;
 }
 
+// Workgroups per CU: at most kMaxPerCU resident ones, times kOversub / 2 launched (an
+// oversubscribed grid lets the dispatcher hand later workgroups to whichever CU frees up).
+#ifndef LIA_MAX_WG_PER_CU
+#define LIA_MAX_WG_PER_CU 3
+#endif
+#ifndef LIA_WG_OVERSUB2
+#define LIA_WG_OVERSUB2 2
+#endif
+constexpr uint32_t kMaxPerCU = LIA_MAX_WG_PER_CU;
+constexpr uint32_t kOversub2 = LIA_WG_OVERSUB2;
+
 // Upper bound on attention workgroups per launch: sizes the plan and the record area.
 static uint32_t max_workgroups() {
     uint32_t cus = lia_device_cus();
     if (!cus) cus = 256;
-    uint32_t n = cus * 4;
-    return n < kCombineMaxRecords ? n : kCombineMaxRecords;
+    return cus * kMaxPerCU * kOversub2 / 2;
 }
 
 template <int D, int NT, int KVT>
@@ -972,7 +1028,8 @@ static uint32_t workgroups_for(uint32_t d, uint32_t nt, int kv) {
     if (!cus) cus = 256;
     uint32_t per = d == 128 ? (nt == 1 ? resident_kv<128, 1>(kv) : resident_kv<128, 2>(kv))
                             : (nt == 1 ? resident_kv<64, 1>(kv) : resident_kv<64, 2>(kv));
-    uint32_t n = cus * per;
+    if (per > kMaxPerCU) per = kMaxPerCU;
+    uint32_t n = cus * per * kOversub2 / 2;
     uint32_t cap = max_workgroups();
     return n < cap ? n : cap;
 }
@@ -1043,6 +1100,10 @@ static int run_stages(int stages, const lia_attention_config *c, uint32_t n_seqs
         if (c->kv_dtype == LIA_FP8_E4M3 && (!k_scales || !v_scales)) return LIA_E_ARG;
         if (((uintptr_t)q | (uintptr_t)kc | (uintptr_t)vc) & 15) return LIA_E_ALIGN;
     }
+    // q and the FP8 scale arrays are read through 32-bit buffer ranges
+    if ((uint64_t)c->max_rows * c->num_q_heads * c->head_dim * 4 >= (1ull << 31) ||
+        (uint64_t)c->pool_pages * c->num_kv_heads * 4 >= (1ull << 31))
+        return LIA_E_UNSUPPORTED;
     Layout L = layout_for(c, max_workgroups());
     if (workspace_bytes < L.total) return LIA_E_WORKSPACE;
     if ((uintptr_t)workspace & 255) return LIA_E_ALIGN;
@@ -1057,11 +1118,13 @@ static int run_stages(int stages, const lia_attention_config *c, uint32_t n_seqs
     p.out = out;
     p.units = (const UnitDesc *)(ws + L.units);
     p.work = (const WorkDesc *)(ws + L.work);
+    p.merge = (const MergeDesc *)(ws + L.merge);
     p.header = (const uint32_t *)(ws + L.header);
     p.part_o = (float *)(ws + L.part_o);
     p.part_ml = (float *)(ws + L.part_ml);
     p.hq = c->num_q_heads; p.hkv = c->num_kv_heads; p.group = group; p.stride = c->stride;
     p.page_shift = (uint32_t)__builtin_ctz(c->page_size);
+    p.pool_pages = c->pool_pages;
     p.n_wg = n_wg;
     p.rpc = rpc;
     p.scale_log2 = c->scale * 1.4426950408889634f;
@@ -1078,7 +1141,7 @@ static int run_stages(int stages, const lia_attention_config *c, uint32_t n_seqs
         hipLaunchKernelGGL(plan_kernel, dim3(1), dim3(256), 0, s, n_seqs, cu_seqlens, positions,
                            sequences, pages, c->stride, p.page_shift, rpc, c->num_kv_heads,
                            L.max_units, n_wg, (UnitDesc *)(ws + L.units), (WorkDesc *)(ws + L.work),
-                           (uint32_t *)(ws + L.header));
+                           (MergeDesc *)(ws + L.merge), (uint32_t *)(ws + L.header));
     if (stages & kPartial) {
         if (c->head_dim == 128) {
             if (NT == 1) launch_partial_kv<128, 1>(c->kv_dtype, p, n_wg, s);
