@@ -57,7 +57,7 @@ constexpr uint32_t kPrePages = 4;
 struct WorkDesc {
     uint32_t unit;            // first unit of the range
     uint32_t lo, hi;          // block range [lo, hi)
-    uint32_t npre;            // pre[] valid (the range starts in the unit's cached keys)
+    uint32_t flags;           // bit 0: pre[] valid
     UnitDesc first;           // units[unit]
     uint4 pre;                // pages of logical pages (32 * (lo - first.block_start)) / P + 0..3
 };
@@ -194,8 +194,9 @@ __global__ __launch_bounds__(256) void plan_kernel(uint32_t n_seqs, const uint32
         }
         merge[u] = m;
     }
+    auto range_lo = [&](uint32_t w) { return (uint32_t)((uint64_t)w * B / N); };
     for (uint32_t w = t; w < N; w += 256) {
-        uint32_t lo = (uint32_t)((uint64_t)w * B / N), hi = (uint32_t)((uint64_t)(w + 1) * B / N);
+        uint32_t lo = range_lo(w), hi = range_lo(w + 1);
         uint32_t a = 0, e = U; // last unit whose first block <= lo
         while (a + 1 < e) {
             uint32_t mid = (a + e) >> 1;
@@ -204,12 +205,12 @@ __global__ __launch_bounds__(256) void plan_kernel(uint32_t n_seqs, const uint32
         while (a + 1 < U && units[a].block_start + units[a].nblocks <= lo) a++;
         WorkDesc d;
         d.unit = a;
+        d.first = units[a];
+        d.flags = 0;
         d.lo = lo;
         d.hi = hi;
-        d.first = units[a];
-        d.npre = 0;
-        const uint32_t rel = lo - d.first.block_start;
         d.pre = make_uint4(0, 0, 0, 0);
+        const uint32_t rel = lo - d.first.block_start;
         if (pages && rel < d.first.cblocks) {
             // logical pages the range starts with; the unfused launch reads a range that
             // begins in the cached keys on into the new keys from the same table, so the
@@ -220,7 +221,7 @@ __global__ __launch_bounds__(256) void plan_kernel(uint32_t n_seqs, const uint32
             uint32_t v[kPrePages];
             for (uint32_t i = 0; i < kPrePages; i++) v[i] = lp + i < lend ? row[lp + i] : 0u;
             d.pre = make_uint4(v[0], v[1], v[2], v[3]);
-            d.npre = 1;
+            d.flags = 1;
         }
         work[w] = d;
     }
@@ -465,7 +466,7 @@ struct State {
 
 // One chunk: partial scores for this wave's d slice, cross-wave sum through LDS, online
 // softmax (identical in every wave), O^T += V^T P^T for the wave's two 16-dim tiles.
-template <int D, int NT, int KVT>
+template <int D, int NT, int KVT, int VW = kLoadsPerChunk<D, KVT>>
 __device__ __forceinline__ void compute_chunk(const AttnParams &p, const Chunk<D, KVT> &c,
                                               uint32_t t, State<D, NT, KVT> &st,
                                               uint16_t *stage, f32x4 *sx, uint32_t wave) {
@@ -481,7 +482,7 @@ __device__ __forceinline__ void compute_chunk(const AttnParams &p, const Chunk<D
         *(u32x4 *)(dst + ((c0 ^ swz(row)) * 8)) = u32x4{a.x, a.y, b.x, b.y};
         *(u32x4 *)(dst + (((c0 + 1) ^ swz(row)) * 8)) = u32x4{e.x, e.y, f.x, f.y};
     } else {
-        wait_vmcnt<kLoadsPerChunk<D, KVT>>(); // this chunk's V is in LDS
+        wait_vmcnt<VW>(); // this chunk's V is in LDS (VW = memory ops issued after its loads)
     }
     float kscale[2] = {p.scale_log2, p.scale_log2};
     float vscale[2] = {1.0f, 1.0f};
@@ -508,10 +509,9 @@ __device__ __forceinline__ void compute_chunk(const AttnParams &p, const Chunk<D
             sx[((wave * NT + nt) * 2 + j) * 64 + lane] = sp;
         }
     }
-    // Only the LDS score exchange needs ordering: wait for this wave's LDS writes and meet
-    // at a bare barrier (a full __syncthreads fence would also drain the prefetch loads).
-    __builtin_amdgcn_s_waitcnt(0xC07F); // lgkmcnt(0)
-    __builtin_amdgcn_s_barrier();
+    // Only the LDS score exchange needs ordering (a full __syncthreads would also drain the
+    // prefetch loads).
+    lds_barrier();
 #pragma unroll
     for (int nt = 0; nt < NT; nt++) {
         f32x4 s[2];
@@ -687,8 +687,26 @@ __device__ __forceinline__ void append_rows(const AttnParams &p, uint32_t wg, ui
     }
 }
 
+// One column's split record: unnormalised O for this wave's d slice, reference max and mass.
+template <int D>
+__device__ __forceinline__ void store_record(const AttnParams &p, size_t rb, const f32x4 (&o)[2],
+                                             float m, float l, uint32_t wave) {
+    const uint32_t g = lane_id() >> 4;
+    float *po = p.part_o + rb * D + 32 * wave + 4 * g;
+#pragma unroll
+    for (int n = 0; n < 2; n++) *(f32x4 *)(po + 16 * n) = o[n];
+    if (wave == 0 && g == 0) {
+        p.part_ml[rb * 2] = m;
+        p.part_ml[rb * 2 + 1] = l;
+    }
+}
+
+// Three workgroups per CU (one wave per SIMD each) is the measured best, so the kernel
+// may use the registers of 3 waves per SIMD (168) instead of squeezing into 4's (128).
+constexpr int kMinWavesPerEU = 3;
+
 template <int D, int NT, int KVT>
-__global__ __launch_bounds__(D / 32 * 64) void attention_kernel(AttnParams p) {
+__global__ __launch_bounds__(D / 32 * 64, kMinWavesPerEU) void attention_kernel(AttnParams p) {
     using C = Cfg<D, KVT>;
     constexpr uint32_t COLS = 16 * NT;
     // Two distinct LDS objects for the two V stages, so the compiler can tell a transpose
@@ -716,7 +734,7 @@ __global__ __launch_bounds__(D / 32 * 64) void attention_kernel(AttnParams p) {
         UnitDesc ud;
         if (first) ud = wd.first;
         else ud = p.units[u];
-        const bool use_pre = first && wd.npre;
+        const bool use_pre = first && (wd.flags & 1);
         first = false;
         const uint32_t bs = ud.block_start, uend = bs + ud.nblocks;
         if (uend <= lo) { u++; continue; }
@@ -804,14 +822,7 @@ __global__ __launch_bounds__(D / 32 * 64) void attention_kernel(AttnParams p) {
                     }
                 }
             } else {
-                const size_t rb = (size_t)rec * COLS + col;
-                float *po = p.part_o + rb * D + 32 * wave + 4 * g;
-#pragma unroll
-                for (int n = 0; n < 2; n++) *(f32x4 *)(po + 16 * n) = st.o[nt][n];
-                if (wave == 0 && g == 0) {
-                    p.part_ml[rb * 2] = st.m[nt];
-                    p.part_ml[rb * 2 + 1] = lt;
-                }
+                store_record<D>(p, (size_t)rec * COLS + col, st.o[nt], st.m[nt], lt, wave);
             }
         }
         lo = seg_end;

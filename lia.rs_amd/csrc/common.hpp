@@ -137,11 +137,25 @@ __device__ __forceinline__ uint32_t pack2(float a, float b) {
 
 __device__ __forceinline__ float fast_exp2(float x) { return __builtin_amdgcn_exp2f(x); }
 
+// Workgroup barrier for LDS exchanges: waits for this wave's LDS operations and meets the
+// other waves.  The memory clobber keeps the compiler from moving any memory access across
+// it (the s_barrier intrinsic alone does not); unlike __syncthreads - or an LDS-scoped
+// fence, which must cover direct-to-LDS loads - nothing waits for vector loads in flight.
+__device__ __forceinline__ void lds_barrier() {
+    asm volatile("s_waitcnt lgkmcnt(0)\n\ts_barrier" ::: "memory");
+}
+
 // Raw buffer resource over [base, base + bytes): loads at or past `bytes` return zeros and
 // touch no memory, which lets a loop issue every load unconditionally.
 constexpr int kBufferConfig = 0x00020000; // gfx9 raw buffer, 32-bit data format
+// Callers pass wave-uniform values; the readfirstlanes state it, so the descriptor lives in
+// SGPRs (a descriptor the compiler believes divergent costs a waterfall loop per load).
 __device__ __forceinline__ __amdgpu_buffer_rsrc_t make_rsrc(const void *base, uint32_t bytes) {
-    return __builtin_amdgcn_make_buffer_rsrc(const_cast<void *>(base), (short)0, (int)bytes,
+    const uint64_t a = (uint64_t)base;
+    const uint32_t lo = (uint32_t)__builtin_amdgcn_readfirstlane((int)(uint32_t)a);
+    const uint32_t hi = (uint32_t)__builtin_amdgcn_readfirstlane((int)(uint32_t)(a >> 32));
+    void *ub = (void *)(((uint64_t)hi << 32) | lo);
+    return __builtin_amdgcn_make_buffer_rsrc(ub, (short)0, __builtin_amdgcn_readfirstlane((int)bytes),
                                              kBufferConfig);
 }
 
