@@ -150,6 +150,34 @@ int lia_kv_append(const lia_kv_layout *layout, uint32_t rows, const uint32_t *po
                   lia_stream_t stream);
 
 /*
+ * RoPE coefficient table.  Replaces coefficients (src/gpu/kernels/llama_position.rs:36-47),
+ * generalised to head_dim 64 / 128: coefficients[r][i] = {cos, sin}(positions[r] * inv_i),
+ * inv_i = f32(1 / f32(base^(2i/head_dim))), i < head_dim/2 (the reference's rounded steps;
+ * pow/cos/sin evaluated in double and rounded once).  coefficients: [rows][head_dim/2][2]
+ * f32, 8-byte aligned.
+ */
+int lia_rope_coefficients(uint32_t rows, uint32_t head_dim, float base, const uint32_t *positions,
+                          float *coefficients, lia_stream_t stream);
+
+/*
+ * Fused RoPE + KV append.  Replaces rotary_cache (src/gpu/kernels/llama_position.rs:49-118),
+ * generalised to any head counts, head_dim 64 / 128 and every pool type.  input: rows of
+ * (num_q_heads + 2 * num_kv_heads) * head_dim f32 = q heads | k heads | v heads.  Each q and
+ * k head is rotated by the "rotate half" rule with the coefficient table:
+ *   x'[i]       = fma(x[i], cos_i, -f32(x[i + d/2] * sin_i))
+ *   x'[i + d/2] = fma(x[i + d/2], cos_i, f32(x[i] * sin_i))       (i < d/2)
+ * Rotated queries go to query ([rows][num_q_heads][head_dim], LIA_F32 or LIA_BF16); rotated
+ * K and unrotated V are appended exactly as lia_kv_append appends f32 rows (slot_mapping or
+ * positions/sequences/pages/stride; FP8 pools divide by the page scale).  input, query and
+ * coefficients 16-byte aligned.
+ */
+int lia_rope_kv_append(const lia_kv_layout *layout, uint32_t num_q_heads, uint32_t rows,
+                       const uint32_t *positions, const uint32_t *sequences, const uint32_t *pages,
+                       uint32_t stride, const uint32_t *slot_mapping, const float *coefficients,
+                       const float *input, void *query, int32_t query_dtype, void *kc, void *vc,
+                       const float *k_scales, const float *v_scales, lia_stream_t stream);
+
+/*
  * FP8 page quantisation: converts n_pages whole pages (page ids in page_ids) of K and V
  * given as [n_pages][page_size][num_kv_heads][head_dim] in src_dtype into the e4m3 pool,
  * computing each (page, head) scale as amax / 448 (1 when the page is all zero).

@@ -98,6 +98,12 @@ EXPORTS = {
                                       C.c_void_p, C.c_void_p, C.c_void_p, C.c_void_p,
                                       C.c_void_p, C.c_void_p, C.c_size_t, C.c_void_p,
                                       C.c_void_p]),
+    "lia_rope_coefficients": (C.c_int, [C.c_uint32, C.c_uint32, C.c_float, C.c_void_p,
+                                        C.c_void_p, C.c_void_p]),
+    "lia_rope_kv_append": (C.c_int, [C.POINTER(KVLayout), C.c_uint32, C.c_uint32, C.c_void_p,
+                                     C.c_void_p, C.c_void_p, C.c_uint32, C.c_void_p, C.c_void_p,
+                                     C.c_void_p, C.c_void_p, C.c_int32, C.c_void_p, C.c_void_p,
+                                     C.c_void_p, C.c_void_p, C.c_void_p]),
     "lia_attention_plan": (C.c_int, [C.POINTER(AttentionConfig), C.c_uint32, C.c_uint32,
                                      C.c_void_p, C.c_void_p, C.c_void_p, C.c_void_p, C.c_void_p,
                                      C.c_size_t, C.c_void_p]),
@@ -232,6 +238,25 @@ def kv_quantize_pages(layout, page_ids, k, v, kc, vc, k_scales, v_scales, stream
                                      torch_dtype_code(k.dtype), _dptr(k), _dptr(v), _dptr(kc),
                                      _dptr(vc), _dptr(k_scales), _dptr(v_scales), _stream(stream))
     _check(st, "kv_quantize_pages")
+
+
+def rope_coefficients(positions, head_dim, out, base=5e6, stream=None):
+    """RoPE table [rows][head_dim/2][2] (lia_rope_coefficients)."""
+    st = lib().lia_rope_coefficients(positions.numel(), head_dim, C.c_float(base), _dptr(positions),
+                                     _dptr(out), _stream(stream))
+    _check(st, "rope_coefficients")
+
+
+def rope_kv_append(layout, num_q_heads, coefficients, combined, query, kc, vc, slot_mapping=None,
+                   positions=None, sequences=None, pages=None, stride=0, k_scales=None,
+                   v_scales=None, stream=None):
+    """Fused RoPE + KV append (lia_rope_kv_append); combined rows are q | k | v heads in f32."""
+    st = lib().lia_rope_kv_append(C.byref(layout), num_q_heads, combined.shape[0],
+                                  _dptr(positions), _dptr(sequences), _dptr(pages), stride,
+                                  _dptr(slot_mapping), _dptr(coefficients), _dptr(combined),
+                                  _dptr(query), torch_dtype_code(query.dtype), _dptr(kc), _dptr(vc),
+                                  _dptr(k_scales), _dptr(v_scales), _stream(stream))
+    _check(st, "rope_kv_append")
 
 
 def workspace_bytes(config):

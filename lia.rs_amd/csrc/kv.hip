@@ -184,9 +184,159 @@ __global__ __launch_bounds__(256) void quantize_kernel(uint32_t P, uint32_t hkv,
     }
 }
 
+// RoPE coefficient table [rows][head_dim/2][2] = {cos, sin}(position * inv_i) with
+// inv_i = f32(1 / f32(base^(2i/head_dim))), the rounded steps of coefficients
+// (src/gpu/kernels/llama_position.rs:36-47).  pow, cos and sin are evaluated in double and
+// rounded once to f32.
+__global__ __launch_bounds__(256) void rope_coefficients_kernel(uint32_t rows, uint32_t head_dim,
+                                                                float base,
+                                                                const uint32_t *positions,
+                                                                float *out) {
+    const uint32_t half = head_dim / 2;
+    const uint32_t i = blockIdx.x * 256 + threadIdx.x;
+    if (i >= rows * half) return;
+    const float e = 2.0f * (float)(i % half) / (float)head_dim;
+    const float p = (float)pow((double)base, (double)e);
+    const float inv = 1.0f / p;
+    const float angle = (float)positions[i / half] * inv;
+    float2 cs;
+    cs.x = (float)cos((double)angle);
+    cs.y = (float)sin((double)angle);
+    ((float2 *)out)[i] = cs;
+}
+
+template <int KVT>
+__device__ __forceinline__ void store_pool4(void *pool, size_t at, float4 x, float scale) {
+    if constexpr (KVT == LIA_FP8_E4M3) {
+        const uint32_t w = (uint32_t)f32_to_e4m3(x.x / scale) | ((uint32_t)f32_to_e4m3(x.y / scale) << 8) |
+                           ((uint32_t)f32_to_e4m3(x.z / scale) << 16) | ((uint32_t)f32_to_e4m3(x.w / scale) << 24);
+        *(uint32_t *)((uint8_t *)pool + at) = w;
+    } else {
+        auto cv = [](float f) -> uint32_t { return KVT == LIA_BF16 ? f32_to_bf16(f) : f32_to_f16(f); };
+        *(u32x2 *)((uint16_t *)pool + at) = u32x2{cv(x.x) | (cv(x.y) << 16), cv(x.z) | (cv(x.w) << 16)};
+    }
+}
+
+// Fused RoPE + KV append: generalises rotary_cache (src/gpu/kernels/llama_position.rs:49-118)
+// to any head counts, head_dim 64 / 128, the three pool types and slot-mapping or table
+// addressing.  Input rows [rows][(hq + 2 hkv) * d] = q heads | k heads | v heads.  For
+// d' < d/2 with {c, s} = coefficients[row][d']: x'[d'] = fma(x[d'], c, -(x[d'+d/2] * s)),
+// x'[d'+d/2] = fma(x[d'+d/2], c, x[d'] * s), the products rounded (contraction off).  One
+// thread per (row, head, 4 consecutive d' < d/2).
+template <int KVT>
+__global__ __launch_bounds__(256) void rope_append_kernel(
+    uint32_t rows, uint32_t hq, uint32_t hkv, uint32_t d, const uint32_t *positions,
+    const uint32_t *sequences, const uint32_t *pages, uint32_t stride, uint32_t page_shift,
+    const uint32_t *slot_mapping, const float *coefficients, const float *input, void *query,
+    int query_bf16, void *kc, void *vc, const float *k_scales, const float *v_scales) {
+#pragma clang fp contract(off)
+    const uint32_t half = d / 2, quads = half / 4, heads = hq + hkv;
+    const uint32_t i = blockIdx.x * 256 + threadIdx.x; // the host bounds the grid to 32 bits
+    if (i >= rows * heads * quads) return;
+    const uint32_t r = i / (heads * quads);
+    const uint32_t h = i / quads % heads, d0 = 4 * (i % quads);
+    const float4 *cs = (const float4 *)(coefficients + ((size_t)r * half + d0) * 2);
+    const float4 c01 = cs[0], c23 = cs[1]; // {c0, s0, c1, s1}, {c2, s2, c3, s3}
+    const float c[4] = {c01.x, c01.z, c23.x, c23.z}, sn[4] = {c01.y, c01.w, c23.y, c23.w};
+    const size_t width = (size_t)(hq + 2 * hkv) * d;
+    const float *x = input + r * width + (size_t)h * d;
+    const float4 l4 = *(const float4 *)(x + d0), r4 = *(const float4 *)(x + half + d0);
+    const float l[4] = {l4.x, l4.y, l4.z, l4.w}, rr[4] = {r4.x, r4.y, r4.z, r4.w};
+    float a[4], b[4];
+#pragma unroll
+    for (int k = 0; k < 4; k++) {
+        const float rs = rr[k] * sn[k], ls = l[k] * sn[k];
+        a[k] = __builtin_fmaf(l[k], c[k], -rs);
+        b[k] = __builtin_fmaf(rr[k], c[k], ls);
+    }
+    const float4 av = make_float4(a[0], a[1], a[2], a[3]), bv = make_float4(b[0], b[1], b[2], b[3]);
+    if (h < hq) {
+        const size_t at = ((size_t)r * hq + h) * d + d0;
+        if (query_bf16) {
+            store_pool4<LIA_BF16>(query, at, av, 1.0f);
+            store_pool4<LIA_BF16>(query, at + half, bv, 1.0f);
+        } else {
+            *(float4 *)((float *)query + at) = av;
+            *(float4 *)((float *)query + at + half) = bv;
+        }
+        return;
+    }
+    const uint32_t kh = h - hq;
+    uint32_t slot;
+    if (slot_mapping) {
+        slot = slot_mapping[r];
+    } else {
+        const uint32_t pos = positions[r];
+        slot = pages[(size_t)sequences[r] * stride + (pos >> page_shift)] * (1u << page_shift) +
+               (pos & ((1u << page_shift) - 1));
+    }
+    if (slot == kNone) return;
+    float ks = 1.0f, vs = 1.0f;
+    if constexpr (KVT == LIA_FP8_E4M3) {
+        const size_t ps = (size_t)(slot >> page_shift) * hkv + kh;
+        ks = k_scales[ps];
+        vs = v_scales[ps];
+    }
+    const size_t at = ((size_t)slot * hkv + kh) * d + d0;
+    const float *v = input + r * width + (size_t)(hq + hkv + kh) * d;
+    store_pool4<KVT>(kc, at, av, ks);
+    store_pool4<KVT>(kc, at + half, bv, ks);
+    store_pool4<KVT>(vc, at, *(const float4 *)(v + d0), vs);
+    store_pool4<KVT>(vc, at + half, *(const float4 *)(v + half + d0), vs);
+}
+
 } // namespace lia
 
 using namespace lia;
+
+extern "C" int lia_rope_coefficients(uint32_t rows, uint32_t head_dim, float base,
+                                     const uint32_t *positions, float *coefficients,
+                                     lia_stream_t stream) {
+    if (!positions || !coefficients) return LIA_E_ARG;
+    if (head_dim != 64 && head_dim != 128) return LIA_E_UNSUPPORTED;
+    if (((uintptr_t)coefficients & 7) != 0) return LIA_E_ALIGN;
+    if (rows == 0) return LIA_OK;
+    const uint32_t n = rows * (head_dim / 2);
+    hipLaunchKernelGGL(rope_coefficients_kernel, dim3((n + 255) / 256), dim3(256), 0,
+                       (hipStream_t)stream, rows, head_dim, base, positions, coefficients);
+    return hipGetLastError() == hipSuccess ? LIA_OK : LIA_E_HIP;
+}
+
+extern "C" int lia_rope_kv_append(const lia_kv_layout *L, uint32_t num_q_heads, uint32_t rows,
+                                  const uint32_t *positions, const uint32_t *sequences,
+                                  const uint32_t *pages, uint32_t stride,
+                                  const uint32_t *slot_mapping, const float *coefficients,
+                                  const float *input, void *query, int32_t query_dtype, void *kc,
+                                  void *vc, const float *k_scales, const float *v_scales,
+                                  lia_stream_t stream) {
+    if (!L || !coefficients || !input || !query || !kc || !vc) return LIA_E_ARG;
+    if (L->head_dim != 64 && L->head_dim != 128) return LIA_E_UNSUPPORTED;
+    if (query_dtype != LIA_F32 && query_dtype != LIA_BF16) return LIA_E_UNSUPPORTED;
+    if (L->num_kv_heads == 0 || num_q_heads == 0) return LIA_E_ARG;
+    if (L->page_size == 0 || (L->page_size & (L->page_size - 1))) return LIA_E_ARG;
+    if (!slot_mapping && (!positions || !sequences || !pages || stride == 0)) return LIA_E_ARG;
+    if (L->dtype == LIA_FP8_E4M3 && (!k_scales || !v_scales)) return LIA_E_ARG;
+    if (((uintptr_t)coefficients | (uintptr_t)input | (uintptr_t)query) & 15) return LIA_E_ALIGN;
+    if (rows == 0) return LIA_OK;
+    const size_t n = (size_t)rows * (num_q_heads + L->num_kv_heads) * (L->head_dim / 8);
+    if (n >= (1ull << 32) - 256) return LIA_E_ARG;
+    const dim3 grid((uint32_t)((n + 255) / 256));
+    const uint32_t shift = (uint32_t)__builtin_ctz(L->page_size);
+    hipStream_t s = (hipStream_t)stream;
+    const int qb = query_dtype == LIA_BF16;
+#define LIA_ROPE(KVT)                                                                              \
+    hipLaunchKernelGGL(rope_append_kernel<KVT>, grid, dim3(256), 0, s, rows, num_q_heads,          \
+                       L->num_kv_heads, L->head_dim, positions, sequences, pages, stride, shift,   \
+                       slot_mapping, coefficients, input, query, qb, kc, vc, k_scales, v_scales)
+    switch (L->dtype) {
+    case LIA_F16: LIA_ROPE(LIA_F16); break;
+    case LIA_BF16: LIA_ROPE(LIA_BF16); break;
+    case LIA_FP8_E4M3: LIA_ROPE(LIA_FP8_E4M3); break;
+    default: return LIA_E_UNSUPPORTED;
+    }
+#undef LIA_ROPE
+    return hipGetLastError() == hipSuccess ? LIA_OK : LIA_E_HIP;
+}
 
 static int src_kind_of(int32_t dtype) {
     return dtype == LIA_F32 ? 0 : dtype == LIA_F16 ? 1 : dtype == LIA_BF16 ? 2 : -1;

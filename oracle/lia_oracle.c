@@ -22,8 +22,11 @@
  *   lo_coefficients / lo_rope /
  *   lo_rotary_cache ..................... pinned for addressing and the rounding order
  *                                          (fused == separate, llama_position.rs:128-239);
- *                                          cosf/sinf/powf bits are libm's: the bits of
- *                                          the reference's device math are parity unpinned
+ *                                          pow/cos/sin in double rounded once to f32 (a
+ *                                          float64 check pins the steps): the bits of the
+ *                                          reference's device math are parity unpinned
+ *   lo_rope_kv_append ................... pinned (equals lo_rotary_cache on the reference
+ *                                          geometry; equals rope + lo_kv_append elsewhere)
  *   exp bits (ex2.approx in the reference) parity unpinned, tolerance-pinned only
  */
 #include <math.h>
@@ -471,13 +474,25 @@ void lo_paged_attention_f32(const lo_geom *g, uint32_t rows, uint32_t span,
 /* 16 query heads, 2 KV heads, combined rows of 2560 floats.                              */
 /* ------------------------------------------------------------------------------------ */
 
-void lo_coefficients(uint32_t rows, float base, const uint32_t *positions, float *out) {
-    for (uint32_t i = 0; i < rows * 64; i++) {
-        float inv = 1.0f / powf(base, 2.0f * (float)(i % 64) / 128.0f);
-        float angle = (float)positions[i / 64] * inv;
-        out[i * 2] = cosf(angle);
-        out[i * 2 + 1] = sinf(angle);
+/* Generalised table [rows][head_dim/2][2] = {cos, sin}(position * inv_i) with
+ * inv_i = f32(1 / f32(base^(2i/head_dim))) (the reference's order of rounded steps).  The
+ * power and the trigonometric functions are evaluated in double and rounded once to f32 -
+ * a correctly rounded f32 restatement of powf/cosf/sinf in all but near-halfway cases. */
+void lo_rope_coefficients(uint32_t rows, uint32_t head_dim, float base, const uint32_t *positions,
+                          float *out) {
+    const uint32_t half = head_dim / 2;
+    for (uint32_t i = 0; i < rows * half; i++) {
+        float e = 2.0f * (float)(i % half) / (float)head_dim;
+        float p = (float)pow((double)base, (double)e);
+        float inv = 1.0f / p;
+        float angle = (float)positions[i / half] * inv;
+        out[i * 2] = (float)cos((double)angle);
+        out[i * 2 + 1] = (float)sin((double)angle);
     }
+}
+
+void lo_coefficients(uint32_t rows, float base, const uint32_t *positions, float *out) {
+    lo_rope_coefficients(rows, 128, base, positions, out);
 }
 
 /* llama_rope over input [rows][heads][128].  The reference source reads
@@ -488,11 +503,15 @@ void lo_rope(uint32_t heads, float base, uint32_t n, const uint32_t *positions, 
              float *output) {
     for (uint32_t i = 0; i < n; i++) {
         uint32_t d = i % 128, row = i / (heads * 128);
-        float angle = (float)positions[row] * (1.0f / powf(base, 2.0f * (float)(d % 64) / 128.0f));
+        float cs[2]; /* the steps of lo_rope_coefficients for index d % 64 */
+        float p = (float)pow((double)base, (double)(2.0f * (float)(d % 64) / 128.0f));
+        float angle = (float)positions[row] * (1.0f / p);
+        cs[0] = (float)cos((double)angle);
+        cs[1] = (float)sin((double)angle);
         uint32_t paired = d < 64 ? i + 64 : i - 64;
         float sign = d < 64 ? -1.0f : 1.0f;
-        volatile float b = input[paired] * sinf(angle);
-        output[i] = fmaf(input[i], cosf(angle), b * sign);
+        volatile float b = input[paired] * cs[1];
+        output[i] = fmaf(input[i], cs[0], b * sign);
     }
 }
 
@@ -522,6 +541,53 @@ void lo_rotary_cache(uint32_t rows, uint32_t stride, uint32_t page_size, const u
             values[at + 64] = lo_f32_to_f16(input[ko + 320 + d]);
         }
     }
+}
+
+/* Generalised rotary_cache (llama_position.rs:49-118): input rows [rows][(hq + 2 hkv) * d]
+ * hold q heads | k heads | v heads.  For d' < d/2 with {c, s} = coefficients[row][d']:
+ *   x'[d']       = fma(x[d'], c, -f32(x[d' + d/2] * s))
+ *   x'[d' + d/2] = fma(x[d' + d/2], c, f32(x[d'] * s))
+ * Queries go to query ([rows][hq][d], f32 or rounded to bf16); rotated K and unrotated V are
+ * appended exactly as lo_kv_append appends f32 rows (slot mapping or table, pool conversion). */
+void lo_rope_kv_append(const lia_kv_layout *L, uint32_t hq, uint32_t rows, const uint32_t *positions,
+                       const uint32_t *sequences, const uint32_t *pages, uint32_t stride,
+                       const uint32_t *slot_mapping, const float *coefficients, const float *input,
+                       void *query, int32_t query_dtype, void *kc, void *vc, const float *k_scales,
+                       const float *v_scales) {
+    const uint32_t d = L->head_dim, half = d / 2, hkv = L->num_kv_heads;
+    const size_t width = (size_t)(hq + 2 * hkv) * d;
+    float *kr = (float *)malloc((size_t)rows * hkv * d * sizeof(float));
+    float *vr = (float *)malloc((size_t)rows * hkv * d * sizeof(float));
+    for (uint32_t r = 0; r < rows; r++) {
+        const float *x = input + (size_t)r * width;
+        for (uint32_t h = 0; h < hq + hkv; h++) {
+            for (uint32_t i = 0; i < half; i++) {
+                float c = coefficients[((size_t)r * half + i) * 2];
+                float sn = coefficients[((size_t)r * half + i) * 2 + 1];
+                float left = x[h * d + i], right = x[h * d + i + half];
+                float a = fmaf(left, c, -(right * sn)), b = fmaf(right, c, left * sn);
+                if (h < hq) {
+                    size_t at = ((size_t)r * hq + h) * d + i;
+                    if (query_dtype == LIA_BF16) {
+                        ((uint16_t *)query)[at] = lo_f32_to_bf16(a);
+                        ((uint16_t *)query)[at + half] = lo_f32_to_bf16(b);
+                    } else {
+                        ((float *)query)[at] = a;
+                        ((float *)query)[at + half] = b;
+                    }
+                } else {
+                    size_t at = ((size_t)r * hkv + (h - hq)) * d + i;
+                    kr[at] = a;
+                    kr[at + half] = b;
+                }
+            }
+        }
+        memcpy(vr + (size_t)r * hkv * d, x + (size_t)(hq + hkv) * d, (size_t)hkv * d * sizeof(float));
+    }
+    lo_kv_append(L, rows, positions, sequences, pages, stride, slot_mapping, LIA_F32, kr, vr, kc, vc,
+                 k_scales, v_scales);
+    free(kr);
+    free(vr);
 }
 
 /* llama_gather_hidden, src/gpu/kernels/llama.rs:186-198 (generic width). */

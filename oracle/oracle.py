@@ -224,6 +224,26 @@ def coefficients(positions, base=5e6):
     return out
 
 
+def rope_coefficients(positions, head_dim, base=5e6):
+    positions = u32(positions)
+    out = np.zeros(positions.size * head_dim, np.float32)
+    lib().lo_rope_coefficients(positions.size, head_dim, C.c_float(base), ptr(positions), ptr(out))
+    return out
+
+
+def rope_kv_append(layout, hq, positions, sequences, pages, stride, coeffs, combined, query,
+                   query_dtype, kc, vc, slot_mapping=None, k_scales=None, v_scales=None):
+    """Generalised rotary_cache (llama_position.rs:49-118), in place on query/kc/vc."""
+    positions, sequences, pages = u32(positions), u32(sequences), u32(pages)
+    sm = u32(slot_mapping) if slot_mapping is not None else None
+    coeffs = np.ascontiguousarray(coeffs, dtype=np.float32)
+    combined = np.ascontiguousarray(combined, dtype=np.float32)
+    rows = positions.size
+    lib().lo_rope_kv_append(C.byref(layout), hq, rows, ptr(positions), ptr(sequences), ptr(pages),
+                            C.c_uint32(stride), ptr(sm), ptr(coeffs), ptr(combined), ptr(query),
+                            query_dtype, ptr(kc), ptr(vc), ptr(k_scales), ptr(v_scales))
+
+
 def rope(heads, positions, x, base=5e6):
     positions = u32(positions)
     x = np.ascontiguousarray(x, dtype=np.float32)

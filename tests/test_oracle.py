@@ -386,3 +386,90 @@ def test_coefficients_against_float64(O):
     angle = (positions[:, None].astype(np.float32) * inv[None, :]).astype(np.float32)
     assert np.max(np.abs(got[:, :, 0] - np.cos(angle.astype(np.float64)))) < 5e-7
     assert np.max(np.abs(got[:, :, 1] - np.sin(angle.astype(np.float64)))) < 5e-7
+
+
+def _rope_fixture(rows, hq, hkv, d, seed):
+    rng = np.random.default_rng(seed)
+    combined = rng.uniform(-4, 4, (rows, (hq + 2 * hkv) * d)).astype(np.float32)
+    return combined
+
+
+def test_rope_kv_append_equals_rotary_cache_on_reference_geometry(O):
+    """The generalised restatement reproduces rotary_cache's bits (16 q / 2 kv heads, d 128,
+    f16 pool in 32-token pages, f32 queries, llama_position.rs:49-118)."""
+    positions = np.array([0, 31, 32, 8191, 131071], np.uint32)
+    sequences = np.array([0, 1, 0, 1, 0], np.uint32)
+    tables = np.zeros(2 * 4096, np.uint32)
+    for row, page in enumerate([5, 3, 2, 7, 1]):
+        tables[sequences[row] * 4096 + positions[row] // 32] = page
+    combined = _rope_fixture(5, 16, 2, 128, 21)
+    coeffs = O.coefficients(positions)
+    q1 = np.zeros(5 * 2048, np.float32)
+    k1 = np.zeros(8 * 32 * 256, np.uint16)
+    v1 = np.zeros_like(k1)
+    O.rotary_cache(5, 4096, 32, positions, sequences, tables, coeffs, combined, q1, k1, v1)
+    layout = O.KVLayout(2, 128, 32, 8, 1)
+    q2 = np.zeros_like(q1)
+    k2 = np.zeros_like(k1)
+    v2 = np.zeros_like(v1)
+    O.rope_kv_append(layout, 16, positions, sequences, tables, 4096, coeffs, combined, q2, 0, k2, v2)
+    assert np.array_equal(q1.view(np.uint32), q2.view(np.uint32))
+    assert np.array_equal(k1, k2) and np.array_equal(v1, v2)
+
+
+def _fma32(a, b, c):
+    # f32 fma: the product of two f32 is exact in longdouble (64-bit significand)
+    L = np.longdouble
+    return (a.astype(L) * b.astype(L) + c.astype(L)).astype(np.float32)
+
+
+@pytest.mark.parametrize("hq,hkv,d,kv,qdt", [(8, 2, 64, 2, 2), (16, 1, 128, 1, 0), (4, 4, 64, 1, 0)])
+def test_rope_kv_append_generalised(O, hq, hkv, d, kv, qdt):
+    """Rotation restated in numpy (rounded products, fma in extended precision), queries
+    rounded to the requested type, K/V through the pinned lo_kv_append."""
+    rows, P, stride = 6, 16, 64
+    rng = np.random.default_rng(hq * 100 + d)
+    positions = rng.integers(0, stride * P, rows).astype(np.uint32)
+    sequences = np.zeros(rows, np.uint32)
+    positions = np.unique(positions)[:rows]
+    rows = positions.size
+    sequences = np.zeros(rows, np.uint32)
+    tables = rng.permutation(stride).astype(np.uint32)
+    combined = _rope_fixture(rows, hq, hkv, d, 22)
+    coeffs = O.rope_coefficients(positions, d).reshape(rows, d // 2, 2)
+    half = d // 2
+    x = combined.reshape(rows, hq + 2 * hkv, d)
+    c = coeffs[:, None, :, 0]
+    s = coeffs[:, None, :, 1]
+    left, right = x[:, :hq + hkv, :half], x[:, :hq + hkv, half:]
+    a = _fma32(left, np.broadcast_to(c, left.shape), -(right * s))
+    b = _fma32(right, np.broadcast_to(c, right.shape), left * s)
+    rot = np.concatenate([a, b], axis=2)
+    layout = O.KVLayout(hkv, d, P, stride, kv)
+    kexp = np.zeros(stride * P * hkv * d, np.uint16)
+    vexp = np.zeros_like(kexp)
+    O.kv_append(layout, positions, sequences, tables, stride, rot[:, hq:].reshape(rows, -1),
+                x[:, hq + hkv:].reshape(rows, -1), kexp, vexp)
+    qexp = rot[:, :hq].reshape(-1)
+    qout = np.zeros(rows * hq * d, np.uint16 if qdt == 2 else np.float32)
+    kc = np.zeros_like(kexp)
+    vc = np.zeros_like(vexp)
+    O.rope_kv_append(layout, hq, positions, sequences, tables, stride, coeffs, combined, qout, qdt,
+                     kc, vc)
+    if qdt == 2:
+        assert np.array_equal(qout, O.from_f32(qexp, 2))
+    else:
+        assert np.array_equal(qout.view(np.uint32), qexp.view(np.uint32))
+    assert np.array_equal(kc, kexp) and np.array_equal(vc, vexp)
+
+
+def test_rope_coefficients_generalise_the_reference_table(O):
+    positions = np.array([0, 5, 4095, 131071], np.uint32)
+    assert np.array_equal(O.rope_coefficients(positions, 128).view(np.uint32),
+                          O.coefficients(positions).view(np.uint32))
+    got = O.rope_coefficients(positions, 64).reshape(4, 32, 2)
+    x = (np.float32(2.0) * np.arange(32, dtype=np.float32)) / np.float32(64.0)
+    inv = (np.float32(1.0) / np.power(np.float64(5e6), x.astype(np.float64)).astype(np.float32)).astype(np.float32)
+    angle = (positions[:, None].astype(np.float32) * inv[None, :]).astype(np.float32)
+    assert np.array_equal(got[:, :, 0], np.cos(angle.astype(np.float64)).astype(np.float32))
+    assert np.array_equal(got[:, :, 1], np.sin(angle.astype(np.float64)).astype(np.float32))
