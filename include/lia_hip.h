@@ -187,6 +187,14 @@ int lia_kv_quantize_pages(const lia_kv_layout *layout, uint32_t n_pages, const u
                           int32_t src_dtype, const void *k, const void *v, void *kc, void *vc,
                           float *k_scales, float *v_scales, lia_stream_t stream);
 
+/*
+ * Output-row gather: dst[i] = src[indices[i]] for rows of `width` 32-bit words (count rows).
+ * Replaces llama_gather_hidden (src/gpu/kernels/llama.rs:186-198), which selects the hidden
+ * rows of the requested outputs before the LM head.  indices must lie inside src.
+ */
+int lia_gather_rows(uint32_t count, uint32_t width, const uint32_t *indices, const void *src,
+                    void *dst, lia_stream_t stream);
+
 /* Geometry and capacity of one paged-attention engine. */
 typedef struct lia_attention_config {
     uint32_t num_q_heads;

@@ -98,6 +98,8 @@ EXPORTS = {
                                       C.c_void_p, C.c_void_p, C.c_void_p, C.c_void_p,
                                       C.c_void_p, C.c_void_p, C.c_size_t, C.c_void_p,
                                       C.c_void_p]),
+    "lia_gather_rows": (C.c_int, [C.c_uint32, C.c_uint32, C.c_void_p, C.c_void_p, C.c_void_p,
+                                  C.c_void_p]),
     "lia_rope_coefficients": (C.c_int, [C.c_uint32, C.c_uint32, C.c_float, C.c_void_p,
                                         C.c_void_p, C.c_void_p]),
     "lia_rope_kv_append": (C.c_int, [C.POINTER(KVLayout), C.c_uint32, C.c_uint32, C.c_void_p,
@@ -257,6 +259,14 @@ def rope_kv_append(layout, num_q_heads, coefficients, combined, query, kc, vc, s
                                   _dptr(query), torch_dtype_code(query.dtype), _dptr(kc), _dptr(vc),
                                   _dptr(k_scales), _dptr(v_scales), _stream(stream))
     _check(st, "rope_kv_append")
+
+
+def gather_rows(indices, src, dst, stream=None):
+    """dst[i] = src[indices[i]] over rows of 32-bit words (lia_gather_rows)."""
+    width = src[0].numel() * src.element_size() // 4
+    st = lib().lia_gather_rows(indices.numel(), width, _dptr(indices), _dptr(src), _dptr(dst),
+                               _stream(stream))
+    _check(st, "gather_rows")
 
 
 def workspace_bytes(config):

@@ -285,9 +285,38 @@ __global__ __launch_bounds__(256) void rope_append_kernel(
     store_pool4<KVT>(vc, at + half, *(const float4 *)(v + half + d0), vs);
 }
 
+// Output-row gather: dst row i = src row indices[i], rows of `width` 32-bit words.
+// Generalises llama_gather_hidden (src/gpu/kernels/llama.rs:186-198, width 2048 f32).
+// One thread per 16 bytes when rows are a multiple of 4 words and 16-byte aligned.
+template <bool VEC>
+__global__ __launch_bounds__(256) void gather_kernel(uint32_t count, uint32_t width,
+                                                     const uint32_t *indices, const void *src,
+                                                     void *dst) {
+    const uint32_t per = VEC ? width / 4 : width;
+    const uint32_t i = blockIdx.x * 256 + threadIdx.x;
+    if (i >= count * per) return;
+    const uint32_t row = i / per, e = i % per;
+    const size_t from = (size_t)indices[row] * per + e;
+    if constexpr (VEC) ((u32x4 *)dst)[i] = ((const u32x4 *)src)[from];
+    else ((uint32_t *)dst)[i] = ((const uint32_t *)src)[from];
+}
+
 } // namespace lia
 
 using namespace lia;
+
+extern "C" int lia_gather_rows(uint32_t count, uint32_t width, const uint32_t *indices,
+                               const void *src, void *dst, lia_stream_t stream) {
+    if (!indices || !src || !dst || width == 0) return LIA_E_ARG;
+    if (count == 0) return LIA_OK;
+    if ((uint64_t)count * width >= (1ull << 32) - 256) return LIA_E_ARG;
+    const bool vec = width % 4 == 0 && (((uintptr_t)src | (uintptr_t)dst) & 15) == 0;
+    const uint32_t n = count * (vec ? width / 4 : width);
+    hipStream_t s = (hipStream_t)stream;
+    if (vec) hipLaunchKernelGGL(gather_kernel<true>, dim3((n + 255) / 256), dim3(256), 0, s, count, width, indices, src, dst);
+    else hipLaunchKernelGGL(gather_kernel<false>, dim3((n + 255) / 256), dim3(256), 0, s, count, width, indices, src, dst);
+    return hipGetLastError() == hipSuccess ? LIA_OK : LIA_E_HIP;
+}
 
 extern "C" int lia_rope_coefficients(uint32_t rows, uint32_t head_dim, float base,
                                      const uint32_t *positions, float *coefficients,

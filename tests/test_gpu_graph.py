@@ -1,0 +1,103 @@
+"""Graph capture of a whole paged step and the output-row gather.
+
+The step (device packing, plan, fused append + partial attention, merge) is captured once
+and replayed several times with new queries written between replays by ordinary eager work;
+every replay must equal the eager execution of the same step bit for bit (the reference
+replays captured paged graphs the same way, src/inference/paging.rs:215-259)."""
+import numpy as np
+import pytest
+import torch
+
+import gpu_data as G
+from gpu_data import BF16
+
+pytestmark = pytest.mark.gpu
+
+
+def _setup(lia, wl, seed):
+    b = wl.custom([300, 1200, 17, 5000, 64], [1, 1, 3, 1, 64], seed=seed)
+    case = G.Case(b, seed=seed)
+    g = b.geom
+    dev = case.device()
+    W = g.hkv * g.d
+    slots = b.slot_mapping().astype(np.int64)
+    newk = G.to_dev(case.kc.reshape(-1, W)[slots].copy(), torch.bfloat16)
+    newv = G.to_dev(case.vc.reshape(-1, W)[slots].copy(), torch.bfloat16)
+    cfg = case.config(lia)
+    ws = torch.zeros(lia.workspace_bytes(cfg), dtype=torch.uint8, device="cuda")
+    meta = dict(
+        seq_slots=G.u32_dev(np.arange(b.n_seqs)), q_lens=G.u32_dev(b.q_len), cached=G.u32_dev(b.cached),
+        cu=torch.zeros(b.n_seqs + 1, dtype=torch.int32, device="cuda"),
+        positions=torch.zeros(b.n_rows, dtype=torch.int32, device="cuda"),
+        sequences=torch.zeros(b.n_rows, dtype=torch.int32, device="cuda"),
+        slots=torch.zeros(b.n_rows, dtype=torch.int32, device="cuda"),
+        status=torch.zeros(1, dtype=torch.int32, device="cuda"))
+    out = torch.zeros((b.n_rows, g.hq, g.d), dtype=torch.bfloat16, device="cuda")
+
+    def step():
+        lia.pack_device(meta["seq_slots"], meta["q_lens"], meta["cached"], dev["pages"], b.stride,
+                        g.page_size, b.pool_pages, b.stride * g.page_size, b.n_rows, meta["cu"],
+                        meta["positions"], meta["sequences"], meta["slots"], meta["status"])
+        lia.attention_plan(cfg, b.n_seqs, b.n_rows, meta["cu"], meta["positions"], meta["sequences"],
+                           ws, pages=dev["pages"])
+        lia.attention_partial_append(cfg, b.n_seqs, dev["pages"], meta["slots"], dev["q"], newk, newv,
+                                     dev["kc"], dev["vc"], out, ws)
+        lia.attention_merge(cfg, b.n_seqs, b.n_rows, out, ws)
+    return b, case, dev, step, out, meta
+
+
+def test_graph_replays_equal_eager(lia, wl):
+    b, case, dev, step, out, meta = _setup(lia, wl, 31)
+    pool_k, pool_v = dev["kc"].clone(), dev["vc"].clone()
+    rng = np.random.default_rng(5)
+    qs = [G.to_dev(G.O.from_f32(rng.standard_normal(tuple(dev["q"].shape), dtype=np.float32), BF16),
+                   torch.bfloat16) for _ in range(4)]
+    # eager results per query set
+    expected = []
+    for q in qs:
+        dev["q"].copy_(q)
+        dev["kc"].copy_(pool_k)
+        dev["vc"].copy_(pool_v)
+        step()
+        torch.cuda.synchronize()
+        assert meta["status"].item() == 0
+        expected.append((out.clone(), dev["kc"].clone()))
+    graph = torch.cuda.CUDAGraph()
+    stream = torch.cuda.Stream()
+    torch.cuda.synchronize()
+    with torch.cuda.stream(stream):
+        with torch.cuda.graph(graph, stream=stream):
+            step()
+    torch.cuda.synchronize()
+    for i, q in enumerate(qs):
+        print(f"[case] graph replay {i}", flush=True)
+        dev["q"].copy_(q)
+        dev["kc"].copy_(pool_k)
+        dev["vc"].copy_(pool_v)
+        out.fill_(float("nan"))
+        torch.cuda.synchronize()
+        graph.replay()
+        torch.cuda.synchronize()
+        assert torch.equal(out.view(torch.int16), expected[i][0].view(torch.int16)), i
+        assert torch.equal(dev["kc"], expected[i][1]), i
+    # the replayed output is also right against the f64 oracle (last query set)
+    case.q_store = qs[-1].view(torch.int16).cpu().numpy().view(np.uint16)
+    case.q32 = G.O.to_f32(case.q_store, BF16)
+    mx, mean = G.errors(out.float().cpu().numpy(), case.f64())
+    assert mx < 2e-2 and mean < 2e-3
+
+
+@pytest.mark.parametrize("width,offset", [(2048, 0), (2048 + 4, 0), (7, 0), (256, 1)])
+def test_gather_rows(lia, O, width, offset):
+    """llama_gather_hidden generalised: vector path (rows of 4k words, aligned) and the
+    word path (odd widths, misaligned pointers)."""
+    rng = np.random.default_rng(width + offset)
+    rows, count = 37, 11
+    src = rng.standard_normal(rows * width + offset).astype(np.float32)
+    idx = rng.integers(0, rows, count).astype(np.uint32)
+    ref = O.gather(idx, src[offset:], width)
+    dsrc = G.to_dev(src)[offset:].view(rows, width)
+    dst = torch.zeros(count * width + offset, dtype=torch.float32, device="cuda")[offset:].view(count, width)
+    lia.gather_rows(G.u32_dev(idx), dsrc, dst)
+    torch.cuda.synchronize()
+    assert np.array_equal(dst.cpu().numpy().reshape(-1).view(np.uint32), ref.view(np.uint32))
