@@ -44,11 +44,40 @@ def parse():
     ap.add_argument("--cpu-seconds", type=float, default=10.0)
     ap.add_argument("--no-cpu", action="store_true")
     ap.add_argument("--kernel-reps", type=int, default=20)
+    ap.add_argument("--traffic", default=os.path.join(ROOT, "profiles",
+                                                    "attention_decode_cfg2_traffic.json"),
+                    help="HBM traffic per launch measured by rocprofv3 --pmc (JSON summary)")
+    ap.add_argument("--copy-calibration", type=int, default=0, metavar="MIB",
+                    help="only run device copies of MIB MiB (the counter calibration kernel)")
     return ap.parse_args()
+
+
+def copy_calibration(mib):
+    """A plain device-to-device copy of known size, for scaling the FETCH_SIZE / WRITE_SIZE
+    counters: 5 copies of `mib` MiB (each reads and writes mib MiB)."""
+    import torch
+    src = torch.ones(mib << 18, dtype=torch.float32, device="cuda")
+    dst = torch.empty_like(src)
+    for _ in range(5):
+        dst.copy_(src)
+    torch.cuda.synchronize()
+    log(f"copied {mib} MiB x 5")
+
+
+def load_traffic(path, kernel_us, layer_bytes):
+    """traffic = (FETCH_SIZE + WRITE_SIZE per dispatch of the kernel) x calibration factor."""
+    if not path or not os.path.exists(path):
+        return None
+    with open(path) as f:
+        t = json.load(f)
+    return round((t["fetch_kib"] * t["fetch_scale"] + t["write_kib"] * t["write_scale"]) * 1024)
 
 
 def main():
     args = parse()
+    if args.copy_calibration:
+        copy_calibration(args.copy_calibration)
+        return
     if args.gpus != 1 or int(os.environ.get("WORLD_SIZE", "1")) > 1:
         print("bench.py: this build measures one GPU only (the path shards by sequence / KV "
               "head with no cross-GPU exchange; see DESIGN.md); run with --gpus 1",
@@ -210,7 +239,8 @@ def main():
         },
         "roofline": {
             "bound": "hbm", "achieved": round(achieved, 1), "peak": PEAK_HBM_GBPS, "unit": "GB/s",
-            "frac": round(achieved / PEAK_HBM_GBPS, 4), "traffic": None,
+            "frac": round(achieved / PEAK_HBM_GBPS, 4),
+            "traffic": load_traffic(args.traffic, kernel_us, layer_bytes),
             "kernel": "attention_kernel<128,1,bf16> (fused append)", "kernel_us": round(kernel_us, 3),
             "bytes_per_launch": layer_bytes,
         },
