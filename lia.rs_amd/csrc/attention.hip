@@ -54,10 +54,14 @@ __device__ __forceinline__ uint32_t unit_head(const UnitDesc &u) { return u.nrow
 // the range's first unit and the physical pages of the first four logical pages the range
 // reads, so a workgroup issues its first K/V loads one dependent load after launch.
 constexpr uint32_t kPrePages = 4;
+#ifndef LIA_XCD_MAJOR
+#define LIA_XCD_MAJOR 1
+#endif
+constexpr bool kXcdMajor = LIA_XCD_MAJOR;
 struct WorkDesc {
     uint32_t unit;            // first unit of the range
     uint32_t lo, hi;          // block range [lo, hi)
-    uint32_t flags;           // bit 0: pre[] valid
+    uint32_t flags;           // bit 0: pre[] valid; bits 8-31: range index (record base)
     UnitDesc first;           // units[unit]
     uint4 pre;                // pages of logical pages (32 * (lo - first.block_start)) / P + 0..3
 };
@@ -153,11 +157,13 @@ __global__ __launch_bounds__(256) void plan_kernel(uint32_t n_seqs, const uint32
         if (nu && u + nu <= max_units) {
             uint32_t ncb = nu / hkv;
             const uint32_t cblocks = (p0 + 31) / 32;
-            for (uint32_t cb = 0; cb < ncb; cb++) {
-                uint32_t rows = min(rpc, nr - cb * rpc);
-                uint32_t kend = p0 + cb * rpc + rows;
-                uint32_t blocks = unit_blocks(p0, kend - p0);
-                for (uint32_t h = 0; h < hkv; h++) {
+            // KV head outermost: consecutive units (and the block ranges over them) stream
+            // the same keys
+            for (uint32_t h = 0; h < hkv; h++) {
+                for (uint32_t cb = 0; cb < ncb; cb++) {
+                    uint32_t rows = min(rpc, nr - cb * rpc);
+                    uint32_t kend = p0 + cb * rpc + rows;
+                    uint32_t blocks = unit_blocks(p0, kend - p0);
                     units[u++] = UnitDesc{blk, blocks, cblocks, r0 + cb * rpc, rows | (h << 16),
                                           kend, trow, p0};
                     blk += blocks;
@@ -195,8 +201,14 @@ __global__ __launch_bounds__(256) void plan_kernel(uint32_t n_seqs, const uint32
         merge[u] = m;
     }
     auto range_lo = [&](uint32_t w) { return (uint32_t)((uint64_t)w * B / N); };
+    // Range r of the flat block order runs on workgroup (r % per) * 8 + r / per, so the
+    // workgroups of one XCD (workgroup i runs on XCD i % 8) take contiguous ranges and share
+    // the keys of neighbouring units in their L2.  Records are indexed by range.
+    const bool xcd_major = kXcdMajor && N == n_wg && N % 8 == 0;
+    const uint32_t per = N / 8;
     for (uint32_t w = t; w < N; w += 256) {
-        uint32_t lo = range_lo(w), hi = range_lo(w + 1);
+        const uint32_t r = xcd_major ? (w % 8) * per + w / 8 : w;
+        uint32_t lo = range_lo(r), hi = range_lo(r + 1);
         uint32_t a = 0, e = U; // last unit whose first block <= lo
         while (a + 1 < e) {
             uint32_t mid = (a + e) >> 1;
@@ -206,7 +218,7 @@ __global__ __launch_bounds__(256) void plan_kernel(uint32_t n_seqs, const uint32
         WorkDesc d;
         d.unit = a;
         d.first = units[a];
-        d.flags = 0;
+        d.flags = r << 8;
         d.lo = lo;
         d.hi = hi;
         d.pre = make_uint4(0, 0, 0, 0);
@@ -221,7 +233,7 @@ __global__ __launch_bounds__(256) void plan_kernel(uint32_t n_seqs, const uint32
             uint32_t v[kPrePages];
             for (uint32_t i = 0; i < kPrePages; i++) v[i] = lp + i < lend ? row[lp + i] : 0u;
             d.pre = make_uint4(v[0], v[1], v[2], v[3]);
-            d.flags = 1;
+            d.flags |= 1;
         }
         work[w] = d;
     }
@@ -675,7 +687,7 @@ __device__ __forceinline__ void append_rows(const AttnParams &p, uint32_t wg, ui
     const uint32_t row_bytes = p.hkv * D * C::EB;
     const uint32_t pieces = row_bytes / 16;
     const uint32_t total = p.n_rows * pieces * 2;
-    for (uint32_t i = wg * C::THREADS + threadIdx.x; i < total; i += N * C::THREADS) {
+    for (uint32_t i = wg * blockDim.x + threadIdx.x; i < total; i += N * blockDim.x) {
         const uint32_t plane = i / (p.n_rows * pieces), rem = i % (p.n_rows * pieces);
         const uint32_t r = rem / pieces, k = rem % pieces;
         const uint32_t slot = p.slots[r];
@@ -798,7 +810,7 @@ __global__ __launch_bounds__(D / 32 * 64, kMinWavesPerEU) void attention_kernel(
 
         // Finalise this wave's d slice: normalised output or a split record.
         const bool whole = lo == bs && seg_end == uend;
-        const uint32_t rec = wg + u;
+        const uint32_t rec = (wd.flags >> 8) + u;
 #pragma unroll
         for (int nt = 0; nt < NT; nt++) {
             float lt = st.l[nt];
@@ -833,6 +845,376 @@ __global__ __launch_bounds__(D / 32 * 64, kMinWavesPerEU) void attention_kernel(
     }
 }
 
+// ------------------------------------------------------------------ the prefill kernel
+//
+// Long query chunks (prefill, chunked prefill, prefix-cache hits) share each key across many
+// rows, so the decode kernel's split over head_dim - every wave reading its own slice of K
+// and V, 16-32 columns per workgroup - would re-read the K/V of a prefix once per 4 rows.
+// Here a workgroup covers 128 columns ((row, query head) pairs of one KV head: 16 rows x 8
+// heads at GQA 8) and each of its 4 waves owns 32 of them over the full head_dim.  Every
+// 32-token chunk of K and V is staged once in LDS with direct-to-LDS loads (each wave
+// fetches a quarter of it) and read by all waves: K as the A operand of S^T = K Q^T (one
+// 16-byte read per lane per 16 tokens x 32 dims; chunk positions XOR-swizzled by token so
+// the 16 rows of a read hit distinct banks), V through transpose reads as the A operand of
+// O^T += V^T P^T (swizzled so the 4 rows of a transpose read hit distinct banks).  Three
+// stages with one barrier per chunk: the barrier both publishes chunk i and retires chunk
+// i - 1, whose stage then receives chunk i + 2.  Work units, block ranges, the two key runs
+// (cached keys, this step's keys), the fused append and the split records are the decode
+// kernel's; records hold 128 columns.
+template <int D>
+struct WCfg {
+    static constexpr int WAVES = 4;
+    static constexpr int COLS = 128;            // 32 per wave: two 16-column tiles
+    static constexpr int ROWB = 2 * D;          // bytes of one token's head (16-bit KV)
+    static constexpr int CH = ROWB / 16;        // 16-byte chunks per token
+    static constexpr int RPI = 1024 / ROWB;     // tokens per direct-to-LDS instruction
+    static constexpr int PER = 32 / RPI / WAVES; // instructions per wave per plane and chunk
+    static constexpr int STAGE = 32 * D;        // 16-bit elements of one K or V stage
+    static constexpr int KT = D / 32;           // k steps of S^T = K Q^T
+    static constexpr int DT = D / 16;           // 16-dim tiles of O
+};
+
+// LDS chunk position of chunk c of token t: K rows are swizzled over all positions (the 16
+// rows of an A-operand read), V rows over the 4 rows of a transpose read.
+template <int D>
+__device__ __forceinline__ uint32_t swz_k(uint32_t t) { return t & (WCfg<D>::CH - 1); }
+template <int D>
+__device__ __forceinline__ uint32_t swz_v(uint32_t t) {
+    return D == 128 ? 2 * (t & 3) : 2 * ((t >> 1) & 1);
+}
+
+// This wave's quarter of chunk t of K and V (from the pool or the step's rows) into LDS.
+template <int D>
+__device__ __forceinline__ void wide_load(const AttnParams &p, uint32_t t, const TilePages &tp,
+                                          const uint8_t *kbase, const uint8_t *vbase, uint32_t hk,
+                                          uint32_t wave, uint16_t *kst, uint16_t *vst) {
+    using W = WCfg<D>;
+    const uint32_t lane = lane_id(), P = 1u << p.page_shift;
+    const uint32_t row_bytes = p.hkv * W::ROWB;
+    __builtin_amdgcn_s_waitcnt(0xC07F); // lgkmcnt(0): this wave's reads of the stage are done
+#pragma unroll
+    for (int s = 0; s < W::PER; s++) {
+        const uint32_t q = wave * W::PER + s;          // instruction: tokens q*RPI .. +RPI-1
+        const uint32_t tl = q * W::RPI + lane / W::CH; // token within the chunk
+        const uint32_t pos = lane % W::CH;
+        const uint32_t j = (q * W::RPI) / 16;          // 16-token tile (one page)
+        const uint32_t rowoff = ((t + tl) & (P - 1)) * row_bytes + hk * W::ROWB;
+        const uint32_t base_k = (pos ^ swz_k<D>(tl)) * 16, base_v = (pos ^ swz_v<D>(tl)) * 16;
+        // select, not index: a runtime index into tp would put it in scratch memory
+        const uint32_t page = j ? tp.page[1] : tp.page[0], live = j ? tp.live[1] : tp.live[0];
+        const __amdgpu_buffer_rsrc_t rk = make_rsrc(kbase + (size_t)page * P * row_bytes, live * row_bytes);
+        const __amdgpu_buffer_rsrc_t rv = make_rsrc(vbase + (size_t)page * P * row_bytes, live * row_bytes);
+        __builtin_amdgcn_raw_ptr_buffer_load_lds(
+            rk, (__attribute__((address_space(3))) void *)(kst + q * 512), 16, rowoff + base_k, 0, 0, 0);
+        __builtin_amdgcn_raw_ptr_buffer_load_lds(
+            rv, (__attribute__((address_space(3))) void *)(vst + q * 512), 16, rowoff + base_v, 0, 0, 0);
+    }
+    __builtin_amdgcn_sched_barrier(0);
+}
+
+template <int D>
+constexpr int kWideLoads = 2 * WCfg<D>::PER; // memory operations of one wide_load
+
+template <int D, int KVT>
+struct WState {
+    u32x4 qr[2][WCfg<D>::KT]; // Q^T operands of the wave's two column tiles
+    uint32_t lo, lim[2];
+    float m[2], l[2];
+    f32x4 o[2][WCfg<D>::DT];
+};
+
+// Full-head_dim query operand of one 16-column tile: lane (g, col) holds q[col][32ks + 8g .. +7].
+template <int D, int KVT>
+__device__ __forceinline__ void load_q_full(const AttnParams &p, uint32_t row, uint32_t head,
+                                            bool valid, u32x4 (&qr)[WCfg<D>::KT]) {
+    constexpr bool MB = KVT == LIA_BF16;
+    const uint32_t g = lane_id() >> 4;
+    const uint32_t qb = p.q_f32 ? 4 : 2;
+    const __amdgpu_buffer_rsrc_t r = make_rsrc(p.q, p.n_rows * p.hq * D * qb);
+#pragma unroll
+    for (int ks = 0; ks < WCfg<D>::KT; ks++) {
+        const uint32_t at = (row * p.hq + head) * D + 32 * ks + 8 * g;
+        const uint32_t off = valid ? at * qb : 0x80000000u;
+        float x[8];
+        if (p.q_f32) {
+            const f32x4 a = __builtin_bit_cast(f32x4, buffer_load16(r, off));
+            const f32x4 b = __builtin_bit_cast(f32x4, buffer_load16(r, off + 16));
+            x[0] = a.x; x[1] = a.y; x[2] = a.z; x[3] = a.w;
+            x[4] = b.x; x[5] = b.y; x[6] = b.z; x[7] = b.w;
+        } else {
+            const u32x4 w = buffer_load16(r, off);
+            if constexpr (MB) {
+                qr[ks] = w;
+                continue;
+            }
+#pragma unroll
+            for (int e = 0; e < 4; e++) {
+                x[2 * e] = bf16_to_f32(w[e] & 0xffffu);
+                x[2 * e + 1] = bf16_to_f32(w[e] >> 16);
+            }
+        }
+        qr[ks] = u32x4{pack2<MB>(x[0], x[1]), pack2<MB>(x[2], x[3]), pack2<MB>(x[4], x[5]),
+                       pack2<MB>(x[6], x[7])};
+    }
+}
+
+// One chunk (32 tokens at t) for this wave's 32 columns, from stages kst / vst.
+template <int D, int KVT>
+__device__ __forceinline__ void wide_compute(const AttnParams &p, uint32_t t, WState<D, KVT> &st,
+                                             const uint16_t *kst, const uint16_t *vst) {
+    using W = WCfg<D>;
+    constexpr bool MB = KVT == LIA_BF16;
+    const uint32_t lane = lane_id(), g = lane >> 4, li = lane & 15;
+    // S^T tiles: tokens 16j + (rows), columns 16nt + li
+    f32x4 acc[2][2];
+#pragma unroll
+    for (int j = 0; j < 2; j++) {
+        acc[j][0] = acc[j][1] = f32x4{0.0f, 0.0f, 0.0f, 0.0f};
+        const uint32_t tr = 16 * j + li;
+#pragma unroll
+        for (int ks = 0; ks < W::KT; ks++) {
+            const uint32_t c = 4 * ks + g;
+            const u32x4 a = *(const u32x4 *)(kst + tr * D + (c ^ swz_k<D>(tr)) * 8);
+#pragma unroll
+            for (int nt = 0; nt < 2; nt++) acc[j][nt] = mfma16x16x32<MB>(a, st.qr[nt][ks], acc[j][nt]);
+        }
+    }
+    u32x4 pb[2];
+#pragma unroll
+    for (int nt = 0; nt < 2; nt++) {
+        float x[2][4];
+        float mx = -INFINITY;
+#pragma unroll
+        for (int j = 0; j < 2; j++)
+#pragma unroll
+            for (int i = 0; i < 4; i++) {
+                const uint32_t tok = t + 16 * j + 4 * g + i;
+                const float v = tok - st.lo < st.lim[nt] ? acc[j][nt][i] * p.scale_log2 : -INFINITY;
+                x[j][i] = v;
+                mx = fmaxf(mx, v);
+            }
+        mx = fmaxf(mx, shfl_xor(mx, 16));
+        mx = fmaxf(mx, shfl_xor(mx, 32));
+        const bool first = st.m[nt] == -INFINITY;
+        const bool raise = !first && mx > st.m[nt] + 8.0f;
+        if (__builtin_amdgcn_ballot_w64(raise)) {
+            const float factor = raise ? fast_exp2(st.m[nt] - mx) : 1.0f;
+            st.l[nt] *= factor;
+#pragma unroll
+            for (int n = 0; n < W::DT; n++) st.o[nt][n] *= factor;
+        }
+        if (first || raise) st.m[nt] = mx;
+        const float muse = st.m[nt] == -INFINITY ? 0.0f : st.m[nt];
+        float pr[2][4];
+        float sum = 0.0f;
+#pragma unroll
+        for (int j = 0; j < 2; j++)
+#pragma unroll
+            for (int i = 0; i < 4; i++) {
+                const float e = fast_exp2(x[j][i] - muse);
+                sum += e;
+                pr[j][i] = e;
+            }
+        st.l[nt] += sum;
+        pb[nt] = u32x4{pack2<MB>(pr[0][0], pr[0][1]), pack2<MB>(pr[0][2], pr[0][3]),
+                       pack2<MB>(pr[1][0], pr[1][1]), pack2<MB>(pr[1][2], pr[1][3])};
+    }
+    // O^T += V^T P^T: V^T rows 16n .. 16n+15, k slots = tokens {4g..4g+3, 16+4g..16+4g+3}
+#pragma unroll
+    for (int n = 0; n < W::DT; n++) {
+        const uint32_t r0 = 4 * g + li / 4, c = 2 * n + ((li & 3) >> 1);
+        const uint16_t *a0p = vst + r0 * D + (c ^ swz_v<D>(r0)) * 8 + (li & 1) * 4;
+        const uint16_t *a1p = a0p + 16 * D; // row r0 + 16: same swizzle
+        const s16x4 a0 = __builtin_amdgcn_ds_read_tr16_b64_v4i16((__attribute__((address_space(3))) s16x4 *)(a0p));
+        const s16x4 a1 = __builtin_amdgcn_ds_read_tr16_b64_v4i16((__attribute__((address_space(3))) s16x4 *)(a1p));
+        const u32x2 b0 = __builtin_bit_cast(u32x2, a0), b1 = __builtin_bit_cast(u32x2, a1);
+        const u32x4 vt = u32x4{b0.x, b0.y, b1.x, b1.y};
+#pragma unroll
+        for (int nt = 0; nt < 2; nt++) st.o[nt][n] = mfma16x16x32<MB>(vt, pb[nt], st.o[nt][n]);
+    }
+}
+
+// One step: wait for chunk i (this wave's loads; the next chunk's loads stay in flight),
+// the barrier, the loads of chunk i + 2 into the stage chunk i - 1 used, then chunk i.
+// Restrict stages: the compiler may keep the new loads in flight across the reads.
+template <int D, int KVT>
+__device__ __forceinline__ void wide_step(const AttnParams &p, uint32_t tn, const TilePages &tpn,
+                                          uint16_t *__restrict__ kn, uint16_t *__restrict__ vn,
+                                          uint32_t tc, const uint16_t *__restrict__ kc,
+                                          const uint16_t *__restrict__ vc, const uint8_t *kbase,
+                                          const uint8_t *vbase, uint32_t hk, uint32_t wave,
+                                          bool active, WState<D, KVT> &st) {
+    wait_vmcnt<kWideLoads<D>>();
+    lds_barrier();
+    wide_load<D>(p, tn, tpn, kbase, vbase, hk, wave, kn, vn);
+    if (active) wide_compute<D, KVT>(p, tc, st, kc, vc);
+}
+
+// Keys [s_lo, s_hi) of one source into the running state (windows of at most 64 pages).
+template <int D, int KVT>
+__device__ __forceinline__ void wide_range(const AttnParams &p, const uint8_t *kbase,
+                                           const uint8_t *vbase, const uint32_t *table,
+                                           uint32_t s_lo, uint32_t s_hi, bool use_pre, uint4 pre,
+                                           uint32_t hk, uint32_t wave, bool active,
+                                           WState<D, KVT> &st, uint16_t *k0, uint16_t *k1,
+                                           uint16_t *k2, uint16_t *v0, uint16_t *v1, uint16_t *v2) {
+    const uint32_t shift = p.page_shift;
+    const uint32_t page_limit = (s_hi + (1u << shift) - 1) >> shift;
+    for (uint32_t wbeg = s_lo & ~31u; wbeg < s_hi;) {
+        const uint32_t wend = min(s_hi, ((wbeg >> shift) + 64) << shift);
+        PageWindow win;
+        window_load<false>(p, win, table, wbeg >> shift, page_limit, hk);
+        TilePages tp0, tp1;
+        if (use_pre) {
+            tp0 = tile_pages_pre(pre, wbeg >> shift, wbeg, shift, wend);
+            tp1 = tile_pages_pre(pre, wbeg >> shift, wbeg + 32, shift, wend);
+            use_pre = false;
+        } else {
+            tp0 = tile_pages<false>(win, wbeg, shift, wend);
+            tp1 = tile_pages<false>(win, wbeg + 32, shift, wend);
+        }
+        // every wave finished the previous window's chunks before their stages are refilled
+        lds_barrier();
+        wide_load<D>(p, wbeg, tp0, kbase, vbase, hk, wave, k0, v0);
+        wide_load<D>(p, wbeg + 32, tp1, kbase, vbase, hk, wave, k1, v1);
+        for (uint32_t t = wbeg;; t += 96) {
+            // loads past wend carry no traffic
+            wide_step<D, KVT>(p, t + 64, tile_pages<false>(win, t + 64, shift, wend), k2, v2, t, k0,
+                              v0, kbase, vbase, hk, wave, active, st);
+            if (t + 32 >= wend) break;
+            wide_step<D, KVT>(p, t + 96, tile_pages<false>(win, t + 96, shift, wend), k0, v0, t + 32,
+                              k1, v1, kbase, vbase, hk, wave, active, st);
+            if (t + 64 >= wend) break;
+            wide_step<D, KVT>(p, t + 128, tile_pages<false>(win, t + 128, shift, wend), k1, v1, t + 64,
+                              k2, v2, kbase, vbase, hk, wave, active, st);
+            if (t + 96 >= wend) break;
+        }
+        wait_vmcnt<0>(); // the trailing (empty) loads target stages about to be reused
+        wbeg = wend;
+    }
+}
+
+template <int D, int KVT>
+__global__ __launch_bounds__(256, 2) void wide_kernel(AttnParams p) {
+    using W = WCfg<D>;
+    constexpr uint32_t COLS = W::COLS;
+    __shared__ __attribute__((aligned(16))) uint16_t k0[W::STAGE], k1[W::STAGE], k2[W::STAGE];
+    __shared__ __attribute__((aligned(16))) uint16_t v0[W::STAGE], v1[W::STAGE], v2[W::STAGE];
+    const uint32_t wg = blockIdx.x;
+    const WorkDesc wd = p.work[wg];
+    const uint32_t tid = threadIdx.x, lane = tid & 63;
+    const uint32_t wave = (uint32_t)__builtin_amdgcn_readfirstlane((int)(tid >> 6));
+    const uint32_t g = lane >> 4, li = lane & 15;
+    uint32_t u = wd.unit, lo = wd.lo;
+    const uint32_t hi = wd.hi;
+    const bool fused = p.newk != nullptr;
+    const uint32_t row_bytes = p.hkv * W::ROWB;
+    bool first = true;
+    // the plan guarantees a unit covers every block of a non-empty range
+    while (lo < hi) {
+        UnitDesc ud;
+        if (first) ud = wd.first;
+        else ud = p.units[u];
+        const bool use_pre = first && (wd.flags & 1);
+        first = false;
+        const uint32_t bs = ud.block_start, uend = bs + ud.nblocks;
+        if (uend <= lo) { u++; continue; }
+        const uint32_t seg_end = min(hi, uend);
+        const uint32_t hk = unit_head(ud), nrows = unit_rows(ud);
+        const uint32_t *table = p.pages + (size_t)ud.table_row * p.stride;
+        const uint32_t kend = ud.kend, kcache = ud.kcache, cb = ud.cblocks;
+        const uint32_t pos0 = kend - nrows;
+        const uint32_t ncols = nrows * p.group;
+        const bool active = 32 * wave < ncols; // waves without valid columns only load
+
+        WState<D, KVT> st;
+        uint32_t climit[2];
+#pragma unroll
+        for (int nt = 0; nt < 2; nt++) {
+            const uint32_t col = 32 * wave + 16 * nt + li;
+            const bool valid = col < ncols;
+            const uint32_t ri = valid ? col / p.group : 0;
+            climit[nt] = valid ? pos0 + ri + 1 : 0;
+            load_q_full<D, KVT>(p, ud.rowbeg + ri, hk * p.group + col % p.group, valid, st.qr[nt]);
+            st.m[nt] = -INFINITY;
+            st.l[nt] = 0.0f;
+#pragma unroll
+            for (int n = 0; n < W::DT; n++) st.o[nt][n] = f32x4{0.0f, 0.0f, 0.0f, 0.0f};
+        }
+        const uint32_t a = lo - bs, e = seg_end - bs;
+        auto key_of = [&](uint32_t i) { return i < cb ? 32 * i : min(kcache + 32 * (i - cb), kend); };
+        auto set_limits = [&](uint32_t r_lo, uint32_t r_hi, uint32_t origin) {
+            st.lo = r_lo;
+#pragma unroll
+            for (int nt = 0; nt < 2; nt++) {
+                const int w = (int)min(climit[nt] - origin, r_hi) - (int)r_lo;
+                st.lim[nt] = climit[nt] && w > 0 ? (uint32_t)w : 0u;
+            }
+        };
+        const uint8_t *kpool = (const uint8_t *)p.kc, *vpool = (const uint8_t *)p.vc;
+        if (!fused) {
+            const uint32_t r_lo = key_of(a), r_hi = min(key_of(e), kend);
+            set_limits(r_lo, r_hi, 0);
+            wide_range<D, KVT>(p, kpool, vpool, table, r_lo, r_hi, use_pre, wd.pre, hk, wave, active,
+                               st, k0, k1, k2, v0, v1, v2);
+        } else {
+            if (a < cb) {
+                const uint32_t r_lo = 32 * a, r_hi = min(32 * min(e, cb), kcache);
+                set_limits(r_lo, r_hi, 0);
+                wide_range<D, KVT>(p, kpool, vpool, table, r_lo, r_hi, use_pre, wd.pre, hk, wave,
+                                   active, st, k0, k1, k2, v0, v1, v2);
+            }
+            if (e > cb) {
+                const uint32_t r0 = ud.rowbeg - (pos0 - kcache);
+                const uint32_t r_lo = 32 * (max(a, cb) - cb), r_hi = min(32 * (e - cb), kend - kcache);
+                set_limits(r_lo, r_hi, kcache);
+                wide_range<D, KVT>(p, (const uint8_t *)p.newk + (size_t)r0 * row_bytes,
+                                   (const uint8_t *)p.newv + (size_t)r0 * row_bytes, nullptr, r_lo,
+                                   r_hi, false, wd.pre, hk, wave, active, st, k0, k1, k2, v0, v1, v2);
+            }
+        }
+
+        const bool whole = lo == bs && seg_end == uend;
+        const uint32_t rec = (wd.flags >> 8) + u;
+#pragma unroll
+        for (int nt = 0; nt < 2; nt++) {
+            float lt = st.l[nt];
+            lt += shfl_xor(lt, 16);
+            lt += shfl_xor(lt, 32);
+            const uint32_t col = 32 * wave + 16 * nt + li;
+            if (col >= ncols) continue;
+            const uint32_t row = ud.rowbeg + col / p.group;
+            const uint32_t head = hk * p.group + col % p.group;
+            if (whole) {
+                const float inv = lt > 0.0f ? 1.0f / lt : 0.0f;
+                const size_t base = ((size_t)row * p.hq + head) * D + 4 * g;
+#pragma unroll
+                for (int n = 0; n < W::DT; n++) {
+                    const f32x4 v = st.o[nt][n] * inv;
+                    if (p.out_f32) {
+                        *(f32x4 *)((float *)p.out + base + 16 * n) = v;
+                    } else {
+                        *(u32x2 *)((uint16_t *)p.out + base + 16 * n) =
+                            u32x2{pack2<true>(v.x, v.y), pack2<true>(v.z, v.w)};
+                    }
+                }
+            } else {
+                const size_t rb = (size_t)rec * COLS + col;
+                float *po = p.part_o + rb * D + 4 * g;
+#pragma unroll
+                for (int n = 0; n < W::DT; n++) *(f32x4 *)(po + 16 * n) = st.o[nt][n];
+                if (g == 0) {
+                    p.part_ml[rb * 2] = st.m[nt];
+                    p.part_ml[rb * 2 + 1] = lt;
+                }
+            }
+        }
+        lo = seg_end;
+        u++;
+    }
+    if (fused) append_rows<D, KVT>(p, wg, gridDim.x);
+}
+
 // Merge the partial records of every unit that was split across workgroups.  Weights
 // follow the reference merge: a record with zero mass contributes nothing, the others
 // are scaled by 2^(m_r - M) (m in the log2 domain here), out = sum w o / sum w l
@@ -843,6 +1225,7 @@ __global__ __launch_bounds__(D / 32 * 64, kMinWavesPerEU) void attention_kernel(
 // the record groups are summed through LDS at the end.
 constexpr uint32_t kCombineThreads = 256;
 constexpr uint32_t kCombinePasses = 8;
+constexpr uint32_t kWideNTDev = 8; // column tiles of a prefill-kernel unit (128 columns)
 
 __device__ __forceinline__ float wave_max(float v) {
 #pragma unroll
@@ -932,6 +1315,76 @@ __global__ __launch_bounds__(kCombineThreads) void combine_kernel(AttnParams p) 
     }
 }
 
+// Merge for the prefill kernel's 128-column units, which are split over few workgroups
+// (2-3 records each): one wave per column, four columns per workgroup.  Lanes hold a
+// record's row as float4 quads (64 / (D/4) records per pass); the record groups are summed
+// with lane shuffles.  Same merge rule as combine_kernel.
+template <int D>
+__global__ __launch_bounds__(256) void combine_wide_kernel(AttnParams p) {
+    constexpr uint32_t Q = D / 4, RPP = 64 / Q, COLS = 16 * kWideNTDev;
+    const uint32_t u = blockIdx.x, lane = threadIdx.x & 63;
+    const uint32_t col = blockIdx.y * 4 + (uint32_t)__builtin_amdgcn_readfirstlane((int)(threadIdx.x >> 6));
+    const MergeDesc md = p.merge[u];
+    if (md.n == 0 || col >= (md.nrows_hk & 0xffffu) * p.group) return;
+    const uint32_t n = md.n, rec0 = md.rec0, q = lane % Q, rg = lane / Q;
+    const float4 *po = (const float4 *)p.part_o;
+    float M = -INFINITY, den = 0.0f;
+    float4 num = make_float4(0.0f, 0.0f, 0.0f, 0.0f);
+    for (uint32_t base = 0; base < n; base += RPP * kCombinePasses) {
+        float4 o[kCombinePasses];
+        float m[kCombinePasses], l[kCombinePasses];
+#pragma unroll
+        for (uint32_t k = 0; k < kCombinePasses; k++) {
+            const uint32_t r = base + k * RPP + rg;
+            const size_t rb = (size_t)(rec0 + min(r, n - 1)) * COLS + col;
+            o[k] = po[rb * Q + q];
+            const float2 ml = ((const float2 *)p.part_ml)[rb];
+            m[k] = ml.x;
+            l[k] = r < n ? ml.y : 0.0f;
+        }
+        float bm = -INFINITY;
+#pragma unroll
+        for (uint32_t k = 0; k < kCombinePasses; k++)
+            if (l[k] > 0.0f) bm = fmaxf(bm, m[k]);
+        bm = wave_max(bm);
+        const float nm = fmaxf(M, bm);
+        if (nm != M) {
+            const float f = M == -INFINITY ? 0.0f : fast_exp2(M - nm);
+            num.x *= f; num.y *= f; num.z *= f; num.w *= f;
+            den *= f;
+            M = nm;
+        }
+#pragma unroll
+        for (uint32_t k = 0; k < kCombinePasses; k++) {
+            const float w = l[k] > 0.0f ? fast_exp2(m[k] - M) : 0.0f;
+            num.x = fmaf(w, o[k].x, num.x);
+            num.y = fmaf(w, o[k].y, num.y);
+            num.z = fmaf(w, o[k].z, num.z);
+            num.w = fmaf(w, o[k].w, num.w);
+            den = fmaf(w, l[k], den);
+        }
+    }
+#pragma unroll
+    for (uint32_t off = Q; off < 64; off <<= 1) {
+        num.x += shfl_xor(num.x, off);
+        num.y += shfl_xor(num.y, off);
+        num.z += shfl_xor(num.z, off);
+        num.w += shfl_xor(num.w, off);
+        den += shfl_xor(den, off);
+    }
+    if (rg != 0) return;
+    const float inv = den > 0.0f ? 1.0f / den : 0.0f;
+    const uint32_t row = md.rowbeg + col / p.group, head = (md.nrows_hk >> 16) * p.group + col % p.group;
+    const size_t at = ((size_t)row * p.hq + head) * D + 4 * q;
+    if (p.out_f32) {
+        *(float4 *)((float *)p.out + at) = make_float4(num.x * inv, num.y * inv, num.z * inv, num.w * inv);
+    } else {
+        *(u32x2 *)((uint16_t *)p.out + at) =
+            u32x2{(uint32_t)f32_to_bf16(num.x * inv) | ((uint32_t)f32_to_bf16(num.y * inv) << 16),
+                  (uint32_t)f32_to_bf16(num.z * inv) | ((uint32_t)f32_to_bf16(num.w * inv) << 16)};
+    }
+}
+
 // ------------------------------------------------------------------ host side
 
 struct Layout {
@@ -939,9 +1392,13 @@ struct Layout {
     uint32_t max_units, max_records;
 };
 
-static inline uint32_t nt_for(uint32_t n_rows, uint32_t n_seqs, uint32_t group) {
-    // Decode-only batches (one row per sequence) use one 16-column tile; batches with
-    // multi-row sequences (MTP verify, prefill chunks) use two.
+// Columns per unit / 16.  Decode-only batches (one row per sequence) use one 16-column tile
+// and batches with multi-row sequences (MTP verify, short chunks) two, in the decode kernel;
+// batches averaging 16 or more rows per sequence (prefill chunks) use the prefill kernel's
+// 128 columns (16-bit pools; FP8 pools stay on the decode kernel).
+constexpr uint32_t kWideNT = kWideNTDev;
+static inline uint32_t nt_for(uint32_t n_rows, uint32_t n_seqs, uint32_t group, int kv_dtype) {
+    if (n_rows >= 16 * n_seqs && kv_dtype != LIA_FP8_E4M3 && group <= 32) return kWideNT;
     return (n_rows > n_seqs || group > 16) ? 2 : 1;
 }
 
@@ -959,9 +1416,9 @@ static Layout layout_for(const lia_attention_config *c, uint32_t n_wg) {
     off = (off + 255) & ~(size_t)255;
     L.merge = off; off += (size_t)L.max_units * sizeof(MergeDesc);
     off = (off + 255) & ~(size_t)255;
-    L.part_ml = off; off += (size_t)L.max_records * 32 * 2 * sizeof(float);
+    L.part_ml = off; off += (size_t)L.max_records * 16 * kWideNT * 2 * sizeof(float);
     off = (off + 255) & ~(size_t)255;
-    L.part_o = off; off += (size_t)L.max_records * 32 * c->head_dim * sizeof(float);
+    L.part_o = off; off += (size_t)L.max_records * 16 * kWideNT * c->head_dim * sizeof(float);
     L.total = off;
     return L;
 }
@@ -1026,8 +1483,23 @@ static uint32_t resident_workgroups() {
     return cached;
 }
 
+template <int D, int KVT>
+static uint32_t resident_wide() {
+    static uint32_t cached = 0;
+    if (!cached) {
+        int per_cu = 0;
+        if (hipOccupancyMaxActiveBlocksPerMultiprocessor(
+                &per_cu, reinterpret_cast<const void *>(&wide_kernel<D, KVT>), 256, 0) != hipSuccess ||
+            per_cu < 1)
+            per_cu = 1;
+        cached = (uint32_t)per_cu;
+    }
+    return cached;
+}
+
 template <int D, int NT>
 static uint32_t resident_kv(int kv) {
+    if constexpr (NT == kWideNT) return kv == LIA_BF16 ? resident_wide<D, LIA_BF16>() : resident_wide<D, LIA_F16>();
     if (kv == LIA_BF16) return resident_workgroups<D, NT, LIA_BF16>();
     if (kv == LIA_F16) return resident_workgroups<D, NT, LIA_F16>();
     return resident_workgroups<D, NT, LIA_FP8_E4M3>();
@@ -1037,8 +1509,10 @@ static uint32_t resident_kv(int kv) {
 static uint32_t workgroups_for(uint32_t d, uint32_t nt, int kv) {
     uint32_t cus = lia_device_cus();
     if (!cus) cus = 256;
-    uint32_t per = d == 128 ? (nt == 1 ? resident_kv<128, 1>(kv) : resident_kv<128, 2>(kv))
-                            : (nt == 1 ? resident_kv<64, 1>(kv) : resident_kv<64, 2>(kv));
+    uint32_t per = d == 128 ? (nt == 1 ? resident_kv<128, 1>(kv)
+                               : nt == 2 ? resident_kv<128, 2>(kv) : resident_kv<128, kWideNT>(kv))
+                            : (nt == 1 ? resident_kv<64, 1>(kv)
+                               : nt == 2 ? resident_kv<64, 2>(kv) : resident_kv<64, kWideNT>(kv));
     if (per > kMaxPerCU) per = kMaxPerCU;
     uint32_t n = cus * per * kOversub2 / 2;
     uint32_t cap = max_workgroups();
@@ -1069,6 +1543,12 @@ static int validate(const lia_attention_config *c) {
 template <int D, int NT, int KVT>
 static void launch_partial(const AttnParams &p, uint32_t n_wg, hipStream_t s) {
     hipLaunchKernelGGL((attention_kernel<D, NT, KVT>), dim3(n_wg), dim3(Cfg<D, KVT>::THREADS), 0, s, p);
+}
+
+template <int D>
+static void launch_wide(int kv, const AttnParams &p, uint32_t n_wg, hipStream_t s) {
+    if (kv == LIA_BF16) hipLaunchKernelGGL((wide_kernel<D, LIA_BF16>), dim3(n_wg), dim3(256), 0, s, p);
+    else hipLaunchKernelGGL((wide_kernel<D, LIA_F16>), dim3(n_wg), dim3(256), 0, s, p);
 }
 
 template <int D, int NT>
@@ -1119,7 +1599,7 @@ static int run_stages(int stages, const lia_attention_config *c, uint32_t n_seqs
     if (workspace_bytes < L.total) return LIA_E_WORKSPACE;
     if ((uintptr_t)workspace & 255) return LIA_E_ALIGN;
     const uint32_t group = c->num_q_heads / c->num_kv_heads;
-    const uint32_t NT = nt_for(n_rows, n_seqs, group);
+    const uint32_t NT = nt_for(n_rows, n_seqs, group, c->kv_dtype);
     const uint32_t n_wg = workgroups_for(c->head_dim, NT, c->kv_dtype);
     const uint32_t rpc = (16 * NT) / group;
     uint8_t *ws = (uint8_t *)workspace;
@@ -1156,21 +1636,30 @@ static int run_stages(int stages, const lia_attention_config *c, uint32_t n_seqs
     if (stages & kPartial) {
         if (c->head_dim == 128) {
             if (NT == 1) launch_partial_kv<128, 1>(c->kv_dtype, p, n_wg, s);
-            else launch_partial_kv<128, 2>(c->kv_dtype, p, n_wg, s);
+            else if (NT == 2) launch_partial_kv<128, 2>(c->kv_dtype, p, n_wg, s);
+            else launch_wide<128>(c->kv_dtype, p, n_wg, s);
         } else {
             if (NT == 1) launch_partial_kv<64, 1>(c->kv_dtype, p, n_wg, s);
-            else launch_partial_kv<64, 2>(c->kv_dtype, p, n_wg, s);
+            else if (NT == 2) launch_partial_kv<64, 2>(c->kv_dtype, p, n_wg, s);
+            else launch_wide<64>(c->kv_dtype, p, n_wg, s);
         }
     }
     if (stages & kMerge) {
-        dim3 grid(L.max_units, 16 * NT);
+        // units this NT can produce: rows in blocks of rpc per sequence and KV head
+        const uint32_t units_nt = (c->max_rows / (rpc ? rpc : 1) + n_seqs + 1) * c->num_kv_heads;
+        dim3 grid(units_nt < L.max_units ? units_nt : L.max_units, 16 * NT);
+#define LIA_COMBINE(DD, NN) hipLaunchKernelGGL((combine_kernel<DD, NN>), grid, dim3(kCombineThreads), 0, s, p)
+        const dim3 wgrid(grid.x, 16 * kWideNT / 4);
         if (c->head_dim == 128) {
-            if (NT == 1) hipLaunchKernelGGL((combine_kernel<128, 1>), grid, dim3(kCombineThreads), 0, s, p);
-            else hipLaunchKernelGGL((combine_kernel<128, 2>), grid, dim3(kCombineThreads), 0, s, p);
+            if (NT == 1) LIA_COMBINE(128, 1);
+            else if (NT == 2) LIA_COMBINE(128, 2);
+            else hipLaunchKernelGGL((combine_wide_kernel<128>), wgrid, dim3(256), 0, s, p);
         } else {
-            if (NT == 1) hipLaunchKernelGGL((combine_kernel<64, 1>), grid, dim3(kCombineThreads), 0, s, p);
-            else hipLaunchKernelGGL((combine_kernel<64, 2>), grid, dim3(kCombineThreads), 0, s, p);
+            if (NT == 1) LIA_COMBINE(64, 1);
+            else if (NT == 2) LIA_COMBINE(64, 2);
+            else hipLaunchKernelGGL((combine_wide_kernel<64>), wgrid, dim3(256), 0, s, p);
         }
+#undef LIA_COMBINE
     }
     return hipGetLastError() == hipSuccess ? LIA_OK : LIA_E_HIP;
 }

@@ -118,3 +118,18 @@ def test_repeat_calls_are_identical(lia, wl):
     a = case.run(lia, dev)
     c = case.run(lia, dev)
     assert np.array_equal(a, c)
+
+
+def test_config3_mixed_prefill_full_size(lia, wl):
+    """BASELINE config 3 at full size: chunks (512, 0), (1024, 4096), (2048, 8192) and five
+    decode rows in one batch (the prefill kernel's 128-column units)."""
+    _check(G.Case(wl.config3(seed=0), seed=0), lia, "cfg3")
+
+
+@pytest.mark.parametrize("kv,d,page", [(F16, 128, 32), (BF16, 64, 16)])
+def test_prefill_kernel_geometries(lia, wl, kv, d, page):
+    """Prefill units of 128 columns over other page sizes, head_dim 64 and f16 pools, with
+    chunks that are not multiples of the unit's rows and prefixes not page-aligned."""
+    g = wl.Geometry(hq=16, hkv=2, d=d, page_size=page, kv_dtype=kv, q_dtype=F32, out_dtype=F32)
+    b = wl.custom([300, 1000 + 77, 40, 513], [300, 77, 40, 33], geom=g, seed=9)
+    _check(G.Case(b, seed=9), lia, f"prefill kv={kv} d={d} page={page}")
