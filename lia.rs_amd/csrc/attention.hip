@@ -851,9 +851,10 @@ __global__ __launch_bounds__(D / 32 * 64, kMinWavesPerEU) void attention_kernel(
 // rows, so the decode kernel's split over head_dim - every wave reading its own slice of K
 // and V, 16-32 columns per workgroup - would re-read the K/V of a prefix once per 4 rows.
 // Here a workgroup covers 128 columns ((row, query head) pairs of one KV head: 16 rows x 8
-// heads at GQA 8) and each of its 4 waves owns 32 of them over the full head_dim.  Every
-// 32-token chunk of K and V is staged once in LDS with direct-to-LDS loads (each wave
-// fetches a quarter of it) and read by all waves: K as the A operand of S^T = K Q^T (one
+// heads at GQA 8) and each of its 8 waves owns one 16-column tile over the full head_dim
+// (measured: 8 x 16 beats 4 x 32 - more waves per SIMD hide the LDS -> MFMA -> softmax
+// chain - and 16 x 16).  Every 32-token chunk of K and V is staged once in LDS with
+// direct-to-LDS loads (spread over the waves) and read by all of them: K as the A operand of S^T = K Q^T (one
 // 16-byte read per lane per 16 tokens x 32 dims; chunk positions XOR-swizzled by token so
 // the 16 rows of a read hit distinct banks), V through transpose reads as the A operand of
 // O^T += V^T P^T (swizzled so the 4 rows of a transpose read hit distinct banks).  Three
@@ -861,14 +862,23 @@ __global__ __launch_bounds__(D / 32 * 64, kMinWavesPerEU) void attention_kernel(
 // i - 1, whose stage then receives chunk i + 2.  Work units, block ranges, the two key runs
 // (cached keys, this step's keys), the fused append and the split records are the decode
 // kernel's; records hold 128 columns.
+#ifndef LIA_WIDE_WAVES
+#define LIA_WIDE_WAVES 8
+#endif
+#ifndef LIA_WIDE_NTW
+#define LIA_WIDE_NTW 1
+#endif
 template <int D>
 struct WCfg {
-    static constexpr int WAVES = 4;
-    static constexpr int COLS = 128;            // 32 per wave: two 16-column tiles
+    static constexpr int WAVES = LIA_WIDE_WAVES;
+    static constexpr int NTW = LIA_WIDE_NTW;    // 16-column tiles per wave
+    static constexpr int THREADS = 64 * WAVES;
+    static constexpr int COLS = 16 * NTW * WAVES;
     static constexpr int ROWB = 2 * D;          // bytes of one token's head (16-bit KV)
     static constexpr int CH = ROWB / 16;        // 16-byte chunks per token
     static constexpr int RPI = 1024 / ROWB;     // tokens per direct-to-LDS instruction
-    static constexpr int PER = 32 / RPI / WAVES; // instructions per wave per plane and chunk
+    static constexpr int NI = 32 / RPI;         // instructions per plane and chunk
+    static constexpr int PER = (NI + WAVES - 1) / WAVES; // at most, per wave
     static constexpr int STAGE = 32 * D;        // 16-bit elements of one K or V stage
     static constexpr int KT = D / 32;           // k steps of S^T = K Q^T
     static constexpr int DT = D / 16;           // 16-dim tiles of O
@@ -894,7 +904,8 @@ __device__ __forceinline__ void wide_load(const AttnParams &p, uint32_t t, const
     __builtin_amdgcn_s_waitcnt(0xC07F); // lgkmcnt(0): this wave's reads of the stage are done
 #pragma unroll
     for (int s = 0; s < W::PER; s++) {
-        const uint32_t q = wave * W::PER + s;          // instruction: tokens q*RPI .. +RPI-1
+        const uint32_t q = wave + s * W::WAVES;        // instruction: tokens q*RPI .. +RPI-1
+        if (W::NI % W::WAVES && q >= W::NI) break;     // waves past the last instruction
         const uint32_t tl = q * W::RPI + lane / W::CH; // token within the chunk
         const uint32_t pos = lane % W::CH;
         const uint32_t j = (q * W::RPI) / 16;          // 16-token tile (one page)
@@ -917,10 +928,10 @@ constexpr int kWideLoads = 2 * WCfg<D>::PER; // memory operations of one wide_lo
 
 template <int D, int KVT>
 struct WState {
-    u32x4 qr[2][WCfg<D>::KT]; // Q^T operands of the wave's two column tiles
-    uint32_t lo, lim[2];
-    float m[2], l[2];
-    f32x4 o[2][WCfg<D>::DT];
+    u32x4 qr[WCfg<D>::NTW][WCfg<D>::KT]; // Q^T operands of the wave's column tiles
+    uint32_t lo, lim[WCfg<D>::NTW];
+    float m[WCfg<D>::NTW], l[WCfg<D>::NTW];
+    f32x4 o[WCfg<D>::NTW][WCfg<D>::DT];
 };
 
 // Full-head_dim query operand of one 16-column tile: lane (g, col) holds q[col][32ks + 8g .. +7].
@@ -966,22 +977,24 @@ __device__ __forceinline__ void wide_compute(const AttnParams &p, uint32_t t, WS
     constexpr bool MB = KVT == LIA_BF16;
     const uint32_t lane = lane_id(), g = lane >> 4, li = lane & 15;
     // S^T tiles: tokens 16j + (rows), columns 16nt + li
-    f32x4 acc[2][2];
+    constexpr int NTW = W::NTW;
+    f32x4 acc[2][NTW];
 #pragma unroll
     for (int j = 0; j < 2; j++) {
-        acc[j][0] = acc[j][1] = f32x4{0.0f, 0.0f, 0.0f, 0.0f};
+#pragma unroll
+        for (int nt = 0; nt < NTW; nt++) acc[j][nt] = f32x4{0.0f, 0.0f, 0.0f, 0.0f};
         const uint32_t tr = 16 * j + li;
 #pragma unroll
         for (int ks = 0; ks < W::KT; ks++) {
             const uint32_t c = 4 * ks + g;
             const u32x4 a = *(const u32x4 *)(kst + tr * D + (c ^ swz_k<D>(tr)) * 8);
 #pragma unroll
-            for (int nt = 0; nt < 2; nt++) acc[j][nt] = mfma16x16x32<MB>(a, st.qr[nt][ks], acc[j][nt]);
+            for (int nt = 0; nt < NTW; nt++) acc[j][nt] = mfma16x16x32<MB>(a, st.qr[nt][ks], acc[j][nt]);
         }
     }
-    u32x4 pb[2];
+    u32x4 pb[NTW];
 #pragma unroll
-    for (int nt = 0; nt < 2; nt++) {
+    for (int nt = 0; nt < NTW; nt++) {
         float x[2][4];
         float mx = -INFINITY;
 #pragma unroll
@@ -1030,13 +1043,15 @@ __device__ __forceinline__ void wide_compute(const AttnParams &p, uint32_t t, WS
         const u32x2 b0 = __builtin_bit_cast(u32x2, a0), b1 = __builtin_bit_cast(u32x2, a1);
         const u32x4 vt = u32x4{b0.x, b0.y, b1.x, b1.y};
 #pragma unroll
-        for (int nt = 0; nt < 2; nt++) st.o[nt][n] = mfma16x16x32<MB>(vt, pb[nt], st.o[nt][n]);
+        for (int nt = 0; nt < NTW; nt++) st.o[nt][n] = mfma16x16x32<MB>(vt, pb[nt], st.o[nt][n]);
     }
 }
 
 // One step: wait for chunk i (this wave's loads; the next chunk's loads stay in flight),
 // the barrier, the loads of chunk i + 2 into the stage chunk i - 1 used, then chunk i.
 // Restrict stages: the compiler may keep the new loads in flight across the reads.
+constexpr int kWideStages = 3;
+
 template <int D, int KVT>
 __device__ __forceinline__ void wide_step(const AttnParams &p, uint32_t tn, const TilePages &tpn,
                                           uint16_t *__restrict__ kn, uint16_t *__restrict__ vn,
@@ -1044,7 +1059,7 @@ __device__ __forceinline__ void wide_step(const AttnParams &p, uint32_t tn, cons
                                           const uint16_t *__restrict__ vc, const uint8_t *kbase,
                                           const uint8_t *vbase, uint32_t hk, uint32_t wave,
                                           bool active, WState<D, KVT> &st) {
-    wait_vmcnt<kWideLoads<D>>();
+    wait_vmcnt<(kWideStages - 2) * kWideLoads<D>>(); // the later chunks' loads stay in flight
     lds_barrier();
     wide_load<D>(p, tn, tpn, kbase, vbase, hk, wave, kn, vn);
     if (active) wide_compute<D, KVT>(p, tc, st, kc, vc);
@@ -1095,7 +1110,7 @@ __device__ __forceinline__ void wide_range(const AttnParams &p, const uint8_t *k
 }
 
 template <int D, int KVT>
-__global__ __launch_bounds__(256, 2) void wide_kernel(AttnParams p) {
+__global__ __launch_bounds__(64 * LIA_WIDE_WAVES, LIA_WIDE_NTW == 2 ? 2 : 4) void wide_kernel(AttnParams p) {
     using W = WCfg<D>;
     constexpr uint32_t COLS = W::COLS;
     __shared__ __attribute__((aligned(16))) uint16_t k0[W::STAGE], k1[W::STAGE], k2[W::STAGE];
@@ -1125,13 +1140,14 @@ __global__ __launch_bounds__(256, 2) void wide_kernel(AttnParams p) {
         const uint32_t kend = ud.kend, kcache = ud.kcache, cb = ud.cblocks;
         const uint32_t pos0 = kend - nrows;
         const uint32_t ncols = nrows * p.group;
-        const bool active = 32 * wave < ncols; // waves without valid columns only load
+        constexpr int NTW = W::NTW;
+        const bool active = 16 * NTW * wave < ncols; // waves without valid columns only load
 
         WState<D, KVT> st;
-        uint32_t climit[2];
+        uint32_t climit[NTW];
 #pragma unroll
-        for (int nt = 0; nt < 2; nt++) {
-            const uint32_t col = 32 * wave + 16 * nt + li;
+        for (int nt = 0; nt < NTW; nt++) {
+            const uint32_t col = 16 * NTW * wave + 16 * nt + li;
             const bool valid = col < ncols;
             const uint32_t ri = valid ? col / p.group : 0;
             climit[nt] = valid ? pos0 + ri + 1 : 0;
@@ -1146,7 +1162,7 @@ __global__ __launch_bounds__(256, 2) void wide_kernel(AttnParams p) {
         auto set_limits = [&](uint32_t r_lo, uint32_t r_hi, uint32_t origin) {
             st.lo = r_lo;
 #pragma unroll
-            for (int nt = 0; nt < 2; nt++) {
+            for (int nt = 0; nt < NTW; nt++) {
                 const int w = (int)min(climit[nt] - origin, r_hi) - (int)r_lo;
                 st.lim[nt] = climit[nt] && w > 0 ? (uint32_t)w : 0u;
             }
@@ -1177,11 +1193,11 @@ __global__ __launch_bounds__(256, 2) void wide_kernel(AttnParams p) {
         const bool whole = lo == bs && seg_end == uend;
         const uint32_t rec = (wd.flags >> 8) + u;
 #pragma unroll
-        for (int nt = 0; nt < 2; nt++) {
+        for (int nt = 0; nt < NTW; nt++) {
             float lt = st.l[nt];
             lt += shfl_xor(lt, 16);
             lt += shfl_xor(lt, 32);
-            const uint32_t col = 32 * wave + 16 * nt + li;
+            const uint32_t col = 16 * NTW * wave + 16 * nt + li;
             if (col >= ncols) continue;
             const uint32_t row = ud.rowbeg + col / p.group;
             const uint32_t head = hk * p.group + col % p.group;
@@ -1225,7 +1241,13 @@ __global__ __launch_bounds__(256, 2) void wide_kernel(AttnParams p) {
 // the record groups are summed through LDS at the end.
 constexpr uint32_t kCombineThreads = 256;
 constexpr uint32_t kCombinePasses = 8;
-constexpr uint32_t kWideNTDev = 8; // column tiles of a prefill-kernel unit (128 columns)
+#ifndef LIA_WIDE_WAVES
+#define LIA_WIDE_WAVES 8
+#endif
+#ifndef LIA_WIDE_NTW
+#define LIA_WIDE_NTW 1
+#endif
+constexpr uint32_t kWideNTDev = LIA_WIDE_NTW * LIA_WIDE_WAVES; // column tiles of a prefill unit
 
 __device__ __forceinline__ float wave_max(float v) {
 #pragma unroll
@@ -1489,7 +1511,7 @@ static uint32_t resident_wide() {
     if (!cached) {
         int per_cu = 0;
         if (hipOccupancyMaxActiveBlocksPerMultiprocessor(
-                &per_cu, reinterpret_cast<const void *>(&wide_kernel<D, KVT>), 256, 0) != hipSuccess ||
+                &per_cu, reinterpret_cast<const void *>(&wide_kernel<D, KVT>), WCfg<D>::THREADS, 0) != hipSuccess ||
             per_cu < 1)
             per_cu = 1;
         cached = (uint32_t)per_cu;
@@ -1499,10 +1521,13 @@ static uint32_t resident_wide() {
 
 template <int D, int NT>
 static uint32_t resident_kv(int kv) {
-    if constexpr (NT == kWideNT) return kv == LIA_BF16 ? resident_wide<D, LIA_BF16>() : resident_wide<D, LIA_F16>();
-    if (kv == LIA_BF16) return resident_workgroups<D, NT, LIA_BF16>();
-    if (kv == LIA_F16) return resident_workgroups<D, NT, LIA_F16>();
-    return resident_workgroups<D, NT, LIA_FP8_E4M3>();
+    if constexpr (NT == kWideNT) {
+        return kv == LIA_BF16 ? resident_wide<D, LIA_BF16>() : resident_wide<D, LIA_F16>();
+    } else {
+        if (kv == LIA_BF16) return resident_workgroups<D, NT, LIA_BF16>();
+        if (kv == LIA_F16) return resident_workgroups<D, NT, LIA_F16>();
+        return resident_workgroups<D, NT, LIA_FP8_E4M3>();
+    }
 }
 
 // Workgroups of one launch: every CU filled once with resident workgroups.
@@ -1547,8 +1572,9 @@ static void launch_partial(const AttnParams &p, uint32_t n_wg, hipStream_t s) {
 
 template <int D>
 static void launch_wide(int kv, const AttnParams &p, uint32_t n_wg, hipStream_t s) {
-    if (kv == LIA_BF16) hipLaunchKernelGGL((wide_kernel<D, LIA_BF16>), dim3(n_wg), dim3(256), 0, s, p);
-    else hipLaunchKernelGGL((wide_kernel<D, LIA_F16>), dim3(n_wg), dim3(256), 0, s, p);
+    const dim3 block(WCfg<D>::THREADS);
+    if (kv == LIA_BF16) hipLaunchKernelGGL((wide_kernel<D, LIA_BF16>), dim3(n_wg), block, 0, s, p);
+    else hipLaunchKernelGGL((wide_kernel<D, LIA_F16>), dim3(n_wg), block, 0, s, p);
 }
 
 template <int D, int NT>
