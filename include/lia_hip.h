@@ -44,6 +44,8 @@ enum lia_status {
     LIA_E_MISSING_PAGE = -10,   /* "missing physical KV page"          paging.rs:160-162 */
     LIA_E_DUPLICATE_SLOT = -11, /* "duplicate physical KV write"       paging.rs:163-166 */
     LIA_E_NONCONSECUTIVE = -12, /* "packed positions must be consecutive" paging.rs:167-172 */
+    LIA_E_TRANSFER_WINDOW = -13, /* "invalid KV transfer window"     paging_transfer.rs:38-41 */
+    LIA_E_TRANSFER_DUPLICATE = -14, /* "duplicate KV transfer destination" paging_transfer.rs:50 */
     LIA_E_CONFIG = -19,         /* configure_paging limits             paging.rs:39-50 */
     LIA_E_ARG = -20,            /* invalid extent / geometry   gpu/llama_attention.rs:36-61 */
     LIA_E_ALIGN = -21,          /* unaligned buffers           gpu/llama_attention.rs:62-68 */
@@ -194,6 +196,43 @@ int lia_kv_quantize_pages(const lia_kv_layout *layout, uint32_t n_pages, const u
  */
 int lia_gather_rows(uint32_t count, uint32_t width, const uint32_t *indices, const void *src,
                     void *dst, lia_stream_t stream);
+
+/*
+ * KV page transfer in the reference's page wire format.  A page payload is one physical page
+ * of every layer and plane, layer-major: [layer][K, V][page_size][num_kv_heads][head_dim] pool
+ * elements (MINICPM5_PAGE_BYTES = 42 x 2 x 32 x 256 x 2, src/inference/paging_transfer.rs:4),
+ * followed for FP8 pools by [layer][K, V][num_kv_heads] f32 page scales.
+ *   lia_kv_page_bytes:     bytes of one payload.
+ *   lia_kv_transfer_bytes: bytes of the staging buffers (a header + up to 16 payloads); the
+ *                          caller allocates one in pinned host memory and one on the device.
+ *   lia_kv_write_pages:    write_kv_pages (paging_transfer.rs:37-58 with the pinned upload of
+ *                          paging_upload.rs:23-104): copies the payloads into the host staging
+ *                          buffer, one host-to-device copy, one scatter kernel.
+ *   lia_kv_read_pages:     read_kv_page for up to 16 pages (transfer_kv_pages_raw,
+ *                          paging_transfer.rs:75-177): one gather kernel, one device-to-host
+ *                          copy, then payload i is copied out to payloads[i].
+ * 1 to 16 distinct pages, each below pool_pages (the reference's checks, in its order).  Both
+ * are ordered after earlier work on `stream` and synchronise it before returning, as the
+ * reference does; staging_host (pinned) and staging_device are scratch the caller owns, used
+ * by one call at a time.
+ */
+#define LIA_MAX_LAYERS 128
+typedef struct lia_kv_planes {
+    uint32_t n_layers;
+    void *k[LIA_MAX_LAYERS];         /* device base of each layer's K plane */
+    void *v[LIA_MAX_LAYERS];
+    float *k_scales[LIA_MAX_LAYERS]; /* FP8 pools only */
+    float *v_scales[LIA_MAX_LAYERS];
+} lia_kv_planes;
+
+size_t lia_kv_page_bytes(const lia_kv_layout *layout, uint32_t n_layers);
+size_t lia_kv_transfer_bytes(const lia_kv_layout *layout, uint32_t n_layers);
+int lia_kv_write_pages(const lia_kv_layout *layout, const lia_kv_planes *planes, uint32_t n_pages,
+                       const uint32_t *page_ids, const void *const *payloads, void *staging_host,
+                       void *staging_device, lia_stream_t stream);
+int lia_kv_read_pages(const lia_kv_layout *layout, const lia_kv_planes *planes, uint32_t n_pages,
+                      const uint32_t *page_ids, void *const *payloads, void *staging_host,
+                      void *staging_device, lia_stream_t stream);
 
 /* Geometry and capacity of one paged-attention engine. */
 typedef struct lia_attention_config {

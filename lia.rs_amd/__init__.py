@@ -27,6 +27,7 @@ ERRORS = {
     -9: "missing sequence table", -10: "missing physical KV page",
     -11: "duplicate physical KV write",
     -12: "packed positions must be consecutive within each request",
+    -13: "invalid KV transfer window", -14: "duplicate KV transfer destination",
     -19: "invalid paging configuration", -20: "invalid argument", -21: "unaligned buffer",
     -22: "workspace exhausted", -23: "unsupported geometry", -30: "HIP runtime error",
 }
@@ -62,6 +63,16 @@ class PackInfo(C.Structure):
 class KVLayout(C.Structure):
     _fields_ = [("num_kv_heads", C.c_uint32), ("head_dim", C.c_uint32),
                 ("page_size", C.c_uint32), ("pool_pages", C.c_uint32), ("dtype", C.c_int32)]
+
+
+MAX_LAYERS = 128
+
+
+class KVPlanes(C.Structure):
+    """Per-layer plane addresses of one KV pool (lia_kv_planes)."""
+    _fields_ = [("n_layers", C.c_uint32), ("k", C.c_void_p * MAX_LAYERS),
+                ("v", C.c_void_p * MAX_LAYERS), ("k_scales", C.c_void_p * MAX_LAYERS),
+                ("v_scales", C.c_void_p * MAX_LAYERS)]
 
 
 class AttentionConfig(C.Structure):
@@ -119,6 +130,12 @@ EXPORTS = {
                                         C.c_void_p, C.c_void_p]),
     "lia_attention_merge": (C.c_int, [C.POINTER(AttentionConfig), C.c_uint32, C.c_uint32,
                                       C.c_void_p, C.c_size_t, C.c_void_p, C.c_void_p]),
+    "lia_kv_page_bytes": (C.c_size_t, [C.POINTER(KVLayout), C.c_uint32]),
+    "lia_kv_transfer_bytes": (C.c_size_t, [C.POINTER(KVLayout), C.c_uint32]),
+    "lia_kv_write_pages": (C.c_int, [C.POINTER(KVLayout), C.POINTER(KVPlanes), C.c_uint32,
+                                     C.c_void_p, C.c_void_p, C.c_void_p, C.c_void_p, C.c_void_p]),
+    "lia_kv_read_pages": (C.c_int, [C.POINTER(KVLayout), C.POINTER(KVPlanes), C.c_uint32,
+                                    C.c_void_p, C.c_void_p, C.c_void_p, C.c_void_p, C.c_void_p]),
     "lia_device_cus": (C.c_uint32, []),
     "lia_init": (C.c_int, [C.c_int]),
 }
@@ -267,6 +284,72 @@ def gather_rows(indices, src, dst, stream=None):
     st = lib().lia_gather_rows(indices.numel(), width, _dptr(indices), _dptr(src), _dptr(dst),
                                _stream(stream))
     _check(st, "gather_rows")
+
+
+class KVTransfer:
+    """Stream-ordered page transfers of one KV pool in the reference's page wire format
+    (Engine::read_kv_page / write_kv_page / write_kv_pages, src/inference/paging_transfer.rs:
+    26-58): a payload is one physical page of every layer and plane, layer-major, plus the
+    page's f32 scales for FP8 pools.  Owns a pinned host and a device staging buffer."""
+
+    def __init__(self, layout, k, v, k_scales=None, v_scales=None):
+        import torch
+        if not 1 <= len(k) <= MAX_LAYERS or len(v) != len(k):
+            raise LiaError(-20, "KVTransfer: one K and one V plane per layer")
+        self.layout = layout
+        self.planes = KVPlanes()
+        self.planes.n_layers = len(k)
+        for i in range(len(k)):
+            self.planes.k[i], self.planes.v[i] = k[i].data_ptr(), v[i].data_ptr()
+            if k_scales is not None:
+                self.planes.k_scales[i] = k_scales[i].data_ptr()
+                self.planes.v_scales[i] = v_scales[i].data_ptr()
+        self._keep = (k, v, k_scales, v_scales)
+        self.page_bytes = lib().lia_kv_page_bytes(C.byref(layout), len(k))
+        total = lib().lia_kv_transfer_bytes(C.byref(layout), len(k))
+        if self.page_bytes == 0 or total == 0:
+            raise LiaError(-20, "KVTransfer: invalid pool geometry")
+        self.host = torch.empty(total, dtype=torch.uint8, pin_memory=True)
+        self.device = torch.empty(total, dtype=torch.uint8, device=k[0].device)
+
+    def _ids(self, pages):
+        return (C.c_uint32 * max(len(pages), 1))(*pages)
+
+    def read_kv_pages(self, pages, stream=None, out=None):
+        """Payloads (bytearray) of up to 16 distinct physical pages; `out` may supply
+        writable buffers of page_bytes each to fill instead of new ones."""
+        n = len(pages)
+        bufs = list(out) if out is not None else [bytearray(self.page_bytes) for _ in range(n)]
+        if len(bufs) != n:
+            raise LiaError(-20, "read_kv_pages: one output buffer per page")
+        views = [(C.c_char * self.page_bytes).from_buffer(b) for b in bufs]
+        ptrs = (C.c_void_p * max(n, 1))(*[C.addressof(x) for x in views])
+        st = lib().lia_kv_read_pages(C.byref(self.layout), C.byref(self.planes), n,
+                                     self._ids(pages), ptrs, _dptr(self.host),
+                                     _dptr(self.device), _stream(stream))
+        del views
+        _check(st, "read_kv_pages")
+        return bufs
+
+    def read_kv_page(self, page, stream=None):
+        return self.read_kv_pages([page], stream)[0]
+
+    def write_kv_pages(self, pages, stream=None):
+        """pages: [(physical page, payload bytes)], 1 to 16 distinct destinations."""
+        for _, payload in pages:
+            if len(payload) != self.page_bytes:
+                raise LiaError(-20, "write_kv_pages: invalid saved KV page extent")
+        n = len(pages)
+        held = [p if isinstance(p, bytes) else bytes(p) for _, p in pages]
+        ptrs = (C.c_void_p * max(n, 1))(*[C.cast(C.c_char_p(b), C.c_void_p).value
+                                          for b in held])
+        st = lib().lia_kv_write_pages(C.byref(self.layout), C.byref(self.planes), n,
+                                      self._ids([p for p, _ in pages]), ptrs, _dptr(self.host),
+                                      _dptr(self.device), _stream(stream))
+        _check(st, "write_kv_pages")
+
+    def write_kv_page(self, page, payload, stream=None):
+        self.write_kv_pages([(page, payload)], stream)
 
 
 def workspace_bytes(config):
@@ -424,3 +507,26 @@ class Engine:
                         w["sequences"], w["pages"], q, self.k[layer], self.v[layer], out,
                         w["workspace"], self.k_scales[layer], self.v_scales[layer])
         return out
+
+    def _transfer(self):
+        if self.paging is None:
+            raise LiaError(-19, "KV pages require configured paging")
+        if getattr(self, "_kv_transfer", None) is None:
+            layout = KVLayout(self.hkv, self.d, self.page_size, self.pool_pages, self.kv_dtype)
+            fp8 = self.kv_dtype == FP8
+            self._kv_transfer = KVTransfer(layout, self.k, self.v,
+                                           self.k_scales if fp8 else None,
+                                           self.v_scales if fp8 else None)
+        return self._kv_transfer
+
+    def read_kv_page(self, page):
+        """Engine::read_kv_page (src/inference/paging_transfer.rs:26-31)."""
+        return self._transfer().read_kv_page(page)
+
+    def write_kv_page(self, page, payload):
+        """Engine::write_kv_page (src/inference/paging_transfer.rs:33-35)."""
+        self._transfer().write_kv_page(page, payload)
+
+    def write_kv_pages(self, pages):
+        """Engine::write_kv_pages (src/inference/paging_transfer.rs:37-58)."""
+        self._transfer().write_kv_pages(pages)

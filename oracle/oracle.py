@@ -267,3 +267,43 @@ def gather(indices, x, width):
     out = np.zeros(indices.size * width, np.float32)
     lib().lo_gather(indices.size, width, ptr(indices), ptr(x), ptr(out))
     return out
+
+
+def kv_page_payload(k_planes, v_planes, page, page_size, k_scales=None, v_scales=None, hkv=0):
+    """Wire payload of one physical page (transfer_kv_pages_raw, src/inference/
+    paging_transfer.rs:80-99): for layer l and plane p (K=0, V=1) the bytes
+    [page * page_size, (page + 1) * page_size) token rows of that plane land at
+    (2 * l + p) * plane_bytes.  FP8 pools append the page's [layer][plane][hkv] f32 scales
+    (no counterpart in the reference, which has no FP8 pool).  Planes are numpy arrays of
+    [pool_tokens][hkv][d] storage elements."""
+    parts = []
+    for k, v in zip(k_planes, v_planes):
+        for plane in (k, v):
+            parts.append(np.ascontiguousarray(plane[page * page_size:(page + 1) * page_size])
+                         .view(np.uint8).reshape(-1))
+    if k_scales is not None:
+        for ks, vs in zip(k_scales, v_scales):
+            for s in (ks, vs):
+                parts.append(np.ascontiguousarray(s[page * hkv:(page + 1) * hkv], np.float32)
+                             .view(np.uint8))
+    return np.concatenate(parts).tobytes()
+
+
+def kv_page_store(k_planes, v_planes, page, page_size, payload, k_scales=None, v_scales=None,
+                  hkv=0):
+    """Inverse of kv_page_payload: writes one payload into the planes in place (the upload
+    direction of the same copies, paging_transfer.rs:94-97)."""
+    raw = np.frombuffer(payload, np.uint8)
+    at = 0
+    for k, v in zip(k_planes, v_planes):
+        for plane in (k, v):
+            rows = plane[page * page_size:(page + 1) * page_size]
+            n = rows.nbytes
+            rows[...] = raw[at:at + n].view(plane.dtype).reshape(rows.shape)
+            at += n
+    if k_scales is not None:
+        for ks, vs in zip(k_scales, v_scales):
+            for s in (ks, vs):
+                s[page * hkv:(page + 1) * hkv] = raw[at:at + 4 * hkv].view(np.float32)
+                at += 4 * hkv
+    assert at == raw.size, "payload extent"
