@@ -46,11 +46,16 @@ enum lia_status {
     LIA_E_NONCONSECUTIVE = -12, /* "packed positions must be consecutive" paging.rs:167-172 */
     LIA_E_TRANSFER_WINDOW = -13, /* "invalid KV transfer window"     paging_transfer.rs:38-41 */
     LIA_E_TRANSFER_DUPLICATE = -14, /* "duplicate KV transfer destination" paging_transfer.rs:50 */
+    LIA_E_PREFIX_EXTENT = -15,  /* "invalid computed prefix extent"    page_cache.rs:209-212 */
+    LIA_E_IMMUTABLE_PAGE = -16, /* "attempted to overwrite immutable KV page" page_cache.rs:225-228 */
+    LIA_E_PAGE_UNDERFLOW = -17, /* "KV page reference underflow"       page_cache.rs:246 */
+    LIA_E_ACTIVE_EVICT = -18,   /* "cannot evict an active KV page"    page_cache.rs:277 */
     LIA_E_CONFIG = -19,         /* configure_paging limits             paging.rs:39-50 */
     LIA_E_ARG = -20,            /* invalid extent / geometry   gpu/llama_attention.rs:36-61 */
     LIA_E_ALIGN = -21,          /* unaligned buffers           gpu/llama_attention.rs:62-68 */
     LIA_E_WORKSPACE = -22,      /* workspace exhausted         gpu/llama_attention.rs:53-61 */
     LIA_E_UNSUPPORTED = -23,    /* geometry this build has no kernel for */
+    LIA_E_STORE = -24,          /* a page-store or page-I/O callback failed (positive return) */
     LIA_E_HIP = -30             /* a HIP runtime call failed */
 };
 
@@ -327,6 +332,85 @@ uint32_t lia_device_cus(void);
 
 /* Optional: select the device and cache its properties.  Returns LIA_OK. */
 int lia_init(int device);
+
+/*
+ * Host page manager (src/inference/page_cache.rs:48-304): reference-counted physical pages of
+ * page_size tokens, content-addressed by the prefix key chain of src/prefix_cache.rs:61-70
+ * (SHA-256 of "lia-kv-prefix-v1" | parent key | token count u64 LE | tokens u32 LE; the first
+ * parent is the caller's 32-byte namespace), with least-recently-used eviction of idle
+ * immutable pages.  Not thread-safe: one thread drives a cache, as the reference's single
+ * inference thread does.
+ *
+ * The page store (RAM/SSD tiers) and the KV pool are reached through callbacks, each
+ * returning 0 on success or a negative status (a positive return reads as LIA_E_STORE):
+ *   load:        look up a prefix page: 1 and *payload (page_bytes, valid until the next
+ *                write_pages call returns) on a hit, 0 on a miss.  NULL: every lookup misses.
+ *   put:         keep an evicted page's payload under its key.  NULL: evicted pages are dropped.
+ *   read_page:   Engine::read_kv_page - needed when put is set.
+ *   write_pages: Engine::write_kv_pages for up to 16 restored pages.
+ */
+typedef struct lia_page_io {
+    void *ctx;
+    size_t page_bytes;
+    int (*load)(void *ctx, const uint8_t *key, const void **payload);
+    int (*put)(void *ctx, const uint8_t *key, const void *payload);
+    int (*read_page)(void *ctx, uint32_t page, void *payload);
+    int (*write_pages)(void *ctx, uint32_t n, const uint32_t *pages, const void *const *payloads);
+} lia_page_io;
+
+typedef struct lia_page_cache lia_page_cache; /* PageCache */
+typedef struct lia_sequence lia_sequence;     /* page_cache::Sequence: pages + sealed keys */
+
+/* Key::prefix (prefix_cache.rs:61-70). */
+int lia_prefix_key(const uint8_t parent[32], const uint32_t *tokens, size_t n_tokens, uint8_t out[32]);
+/* PageCache::new (page_cache.rs:29-44); an empty pool is LIA_E_CONFIG. */
+int lia_page_cache_create(const uint8_t ns[32], uint32_t n_pages, uint32_t page_size,
+                          const lia_page_io *io, lia_page_cache **out);
+void lia_page_cache_destroy(lia_page_cache *cache);
+/* PageCache::attach (page_cache.rs:48-157): *cached = tokens already resident or restored. */
+int lia_page_cache_attach(lia_page_cache *cache, const uint32_t *tokens, size_t n_tokens,
+                          lia_sequence **sequence, size_t *cached);
+/* PageCache::can_fit (page_cache.rs:163-180): 1 or 0. */
+int lia_page_cache_can_fit(const lia_page_cache *cache, const uint32_t *tokens, size_t n_tokens);
+/* PageCache::available_pages (page_cache.rs:159-161). */
+size_t lia_page_cache_available(const lia_page_cache *cache);
+/* PageCache::ensure_position (page_cache.rs:183-206): 1, 0 when the pool is occupied, or < 0. */
+int lia_page_cache_ensure_position(lia_page_cache *cache, lia_sequence *sequence, size_t position);
+/* PageCache::seal (page_cache.rs:208-237). */
+int lia_page_cache_seal(lia_page_cache *cache, lia_sequence *sequence, const uint32_t *tokens,
+                        size_t n_tokens, size_t computed);
+/* PageCache::release (page_cache.rs:239-244); frees the handle. */
+int lia_page_cache_release(lia_page_cache *cache, lia_sequence *sequence);
+/* PageCache::evict_idle (page_cache.rs:255-262). */
+int lia_page_cache_evict_idle(lia_page_cache *cache);
+void lia_page_cache_stats(const lia_page_cache *cache, uint64_t *gpu_hits, uint64_t *evictions);
+/* The sequence's block-table row (Sequence::pages); valid until the next call on it. */
+uint32_t lia_sequence_pages(const lia_sequence *sequence, const uint32_t **pages);
+
+/* One active slot of the paged runtime (src/server/paged/request.rs). */
+typedef struct lia_request {
+    const uint32_t *tokens;
+    size_t n_tokens;
+    size_t computed;          /* tokens already in the KV pool */
+    lia_sequence *sequence;
+    int32_t active;           /* slot holds a request */
+    int32_t closed;           /* its output stream is closed: marked done, no rows */
+    int32_t done;             /* out */
+    int32_t reserved;
+} lia_request;
+
+typedef struct lia_update {
+    uint32_t slot;
+    uint64_t computed;
+    uint32_t output;          /* 1 when the step's last row of this slot produces logits */
+} lia_update;
+
+/* Runtime::step row construction (src/server/paged/schedule.rs:5-60): rows for
+ * lia_pack_rows, output row indices and per-slot updates; LIA_E_ROWS beyond max_rows. */
+int lia_schedule_rows(lia_page_cache *cache, uint32_t n_slots, lia_request *requests,
+                      uint32_t prefill_batch, lia_paged_row *rows, uint32_t max_rows,
+                      uint32_t *n_rows, uint32_t *outputs, uint32_t *n_outputs,
+                      lia_update *updates, uint32_t *n_updates);
 
 #ifdef __cplusplus
 }

@@ -28,6 +28,9 @@ ERRORS = {
     -11: "duplicate physical KV write",
     -12: "packed positions must be consecutive within each request",
     -13: "invalid KV transfer window", -14: "duplicate KV transfer destination",
+    -15: "invalid computed prefix extent", -16: "attempted to overwrite immutable KV page",
+    -17: "KV page reference underflow", -18: "cannot evict an active KV page",
+    -24: "page store callback failed",
     -19: "invalid paging configuration", -20: "invalid argument", -21: "unaligned buffer",
     -22: "workspace exhausted", -23: "unsupported geometry", -30: "HIP runtime error",
 }
@@ -73,6 +76,29 @@ class KVPlanes(C.Structure):
     _fields_ = [("n_layers", C.c_uint32), ("k", C.c_void_p * MAX_LAYERS),
                 ("v", C.c_void_p * MAX_LAYERS), ("k_scales", C.c_void_p * MAX_LAYERS),
                 ("v_scales", C.c_void_p * MAX_LAYERS)]
+
+
+LOAD_FN = C.CFUNCTYPE(C.c_int, C.c_void_p, C.POINTER(C.c_uint8), C.POINTER(C.c_void_p))
+PUT_FN = C.CFUNCTYPE(C.c_int, C.c_void_p, C.POINTER(C.c_uint8), C.c_void_p)
+READ_FN = C.CFUNCTYPE(C.c_int, C.c_void_p, C.c_uint32, C.c_void_p)
+WRITE_FN = C.CFUNCTYPE(C.c_int, C.c_void_p, C.c_uint32, C.POINTER(C.c_uint32),
+                       C.POINTER(C.c_void_p))
+
+
+class PageIO(C.Structure):
+    _fields_ = [("ctx", C.c_void_p), ("page_bytes", C.c_size_t), ("load", LOAD_FN),
+                ("put", PUT_FN), ("read_page", READ_FN), ("write_pages", WRITE_FN)]
+
+
+class Request(C.Structure):
+    """One active slot of the paged runtime (lia_request)."""
+    _fields_ = [("tokens", C.c_void_p), ("n_tokens", C.c_size_t), ("computed", C.c_size_t),
+                ("sequence", C.c_void_p), ("active", C.c_int32), ("closed", C.c_int32),
+                ("done", C.c_int32), ("reserved", C.c_int32)]
+
+
+class Update(C.Structure):
+    _fields_ = [("slot", C.c_uint32), ("computed", C.c_uint64), ("output", C.c_uint32)]
 
 
 class AttentionConfig(C.Structure):
@@ -136,6 +162,25 @@ EXPORTS = {
                                      C.c_void_p, C.c_void_p, C.c_void_p, C.c_void_p, C.c_void_p]),
     "lia_kv_read_pages": (C.c_int, [C.POINTER(KVLayout), C.POINTER(KVPlanes), C.c_uint32,
                                     C.c_void_p, C.c_void_p, C.c_void_p, C.c_void_p, C.c_void_p]),
+    "lia_prefix_key": (C.c_int, [C.c_char_p, C.c_void_p, C.c_size_t, C.c_void_p]),
+    "lia_page_cache_create": (C.c_int, [C.c_char_p, C.c_uint32, C.c_uint32, C.POINTER(PageIO),
+                                        C.POINTER(C.c_void_p)]),
+    "lia_page_cache_destroy": (None, [C.c_void_p]),
+    "lia_page_cache_attach": (C.c_int, [C.c_void_p, C.c_void_p, C.c_size_t,
+                                        C.POINTER(C.c_void_p), C.POINTER(C.c_size_t)]),
+    "lia_page_cache_can_fit": (C.c_int, [C.c_void_p, C.c_void_p, C.c_size_t]),
+    "lia_page_cache_available": (C.c_size_t, [C.c_void_p]),
+    "lia_page_cache_ensure_position": (C.c_int, [C.c_void_p, C.c_void_p, C.c_size_t]),
+    "lia_page_cache_seal": (C.c_int, [C.c_void_p, C.c_void_p, C.c_void_p, C.c_size_t,
+                                      C.c_size_t]),
+    "lia_page_cache_release": (C.c_int, [C.c_void_p, C.c_void_p]),
+    "lia_page_cache_evict_idle": (C.c_int, [C.c_void_p]),
+    "lia_page_cache_stats": (None, [C.c_void_p, C.POINTER(C.c_uint64), C.POINTER(C.c_uint64)]),
+    "lia_sequence_pages": (C.c_uint32, [C.c_void_p, C.POINTER(C.POINTER(C.c_uint32))]),
+    "lia_schedule_rows": (C.c_int, [C.c_void_p, C.c_uint32, C.POINTER(Request), C.c_uint32,
+                                    C.POINTER(PagedRow), C.c_uint32, C.POINTER(C.c_uint32),
+                                    C.POINTER(C.c_uint32), C.POINTER(C.c_uint32),
+                                    C.POINTER(Update), C.POINTER(C.c_uint32)]),
     "lia_device_cus": (C.c_uint32, []),
     "lia_init": (C.c_int, [C.c_int]),
 }
@@ -350,6 +395,187 @@ class KVTransfer:
 
     def write_kv_page(self, page, payload, stream=None):
         self.write_kv_pages([(page, payload)], stream)
+
+
+def prefix_key(parent, tokens):
+    """Key::prefix (src/prefix_cache.rs:61-70) through lia_prefix_key."""
+    t = np.ascontiguousarray(tokens, dtype=np.uint32)
+    out = C.create_string_buffer(32)
+    _check(lib().lia_prefix_key(bytes(parent), t.ctypes.data, t.size, out), "prefix_key")
+    return out.raw
+
+
+class Sequence:
+    """A sequence's pages in the cache (page_cache::Sequence); `pages` is its block-table row."""
+
+    def __init__(self, handle):
+        self.handle = handle
+
+    @property
+    def pages(self):
+        p = C.POINTER(C.c_uint32)()
+        n = lib().lia_sequence_pages(self.handle, C.byref(p))
+        return [p[i] for i in range(n)]
+
+
+class PageCache:
+    """Host page manager (PageCache, src/inference/page_cache.rs:18-304) over liblia_hip.
+    `store` is a dict-like key -> payload (the RAM/SSD tiers; None drops evicted pages);
+    the KV pool is either a KVTransfer (device planes) or, for host-only use, a dict
+    page -> payload of `page_bytes` bytes."""
+
+    def __init__(self, namespace, pages, page_size=32, store=None, transfer=None, pool=None,
+                 page_bytes=None):
+        self.store, self.transfer, self.pool = store, transfer, pool
+        self.page_bytes = transfer.page_bytes if transfer is not None else (page_bytes or 0)
+        self._held = []
+        io = PageIO()
+        io.ctx = None
+        io.page_bytes = self.page_bytes
+        # dispatch through the instance so a subclass or a test can wrap a callback
+        self._callbacks = (LOAD_FN(lambda *a: self._load(*a)), PUT_FN(lambda *a: self._put(*a)),
+                           READ_FN(lambda *a: self._read(*a)),
+                           WRITE_FN(lambda *a: self._write(*a)))
+        if store is not None:
+            io.load, io.put = self._callbacks[0], self._callbacks[1]
+        io.read_page, io.write_pages = self._callbacks[2], self._callbacks[3]
+        self._io = io
+        h = C.c_void_p()
+        _check(lib().lia_page_cache_create(bytes(namespace), pages, page_size, C.byref(io),
+                                           C.byref(h)), "PageCache")
+        self.handle = h
+
+    def __del__(self):
+        if getattr(self, "handle", None):
+            lib().lia_page_cache_destroy(self.handle)
+            self.handle = None
+
+    # callbacks: 0 ok, a negative lia status, or 1 (-> LIA_E_STORE) on a Python error
+    @staticmethod
+    def _status(e):
+        return e.status if isinstance(e, LiaError) else 1
+
+    def _load(self, ctx, key, payload):
+        try:
+            data = self.store.get(C.string_at(key, 32))
+            if data is None:
+                return 0
+            buf = C.create_string_buffer(bytes(data), len(data))
+            self._held.append(buf)
+            payload[0] = C.addressof(buf)
+            return 1
+        except Exception as e:  # noqa: BLE001 - a positive return means "hit" here
+            return e.status if isinstance(e, LiaError) else -24
+
+    def _put(self, ctx, key, payload):
+        try:
+            self.store[C.string_at(key, 32)] = C.string_at(payload, self.page_bytes)
+            return 0
+        except Exception as e:  # noqa: BLE001
+            return self._status(e)
+
+    def _read(self, ctx, page, dst):
+        try:
+            data = (self.transfer.read_kv_page(page) if self.transfer is not None
+                    else self.pool[page])
+            C.memmove(dst, bytes(data), self.page_bytes)
+            return 0
+        except Exception as e:  # noqa: BLE001
+            return self._status(e)
+
+    def _write(self, ctx, n, pages, payloads):
+        try:
+            items = [(pages[i], C.string_at(payloads[i], self.page_bytes)) for i in range(n)]
+            if self.transfer is not None:
+                self.transfer.write_kv_pages(items)
+            else:
+                for p, d in items:
+                    self.pool[p] = d
+            self._held.clear()
+            return 0
+        except Exception as e:  # noqa: BLE001
+            return self._status(e)
+
+    @staticmethod
+    def _tokens(tokens):
+        return np.ascontiguousarray(tokens, dtype=np.uint32)
+
+    def attach(self, tokens):
+        t = self._tokens(tokens)
+        h, cached = C.c_void_p(), C.c_size_t()
+        st = lib().lia_page_cache_attach(self.handle, t.ctypes.data, t.size, C.byref(h),
+                                         C.byref(cached))
+        self._held.clear()
+        _check(st, "attach")
+        return Sequence(h), cached.value
+
+    def can_fit(self, tokens):
+        t = self._tokens(tokens)
+        return lib().lia_page_cache_can_fit(self.handle, t.ctypes.data, t.size) == 1
+
+    def available_pages(self):
+        return lib().lia_page_cache_available(self.handle)
+
+    def ensure_position(self, sequence, position):
+        st = lib().lia_page_cache_ensure_position(self.handle, sequence.handle, position)
+        if st < 0:
+            _check(st, "ensure_position")
+        return st == 1
+
+    def seal(self, sequence, tokens, computed):
+        t = self._tokens(tokens)
+        _check(lib().lia_page_cache_seal(self.handle, sequence.handle, t.ctypes.data, t.size,
+                                         computed), "seal")
+
+    def release(self, sequence):
+        st = lib().lia_page_cache_release(self.handle, sequence.handle)
+        sequence.handle = None
+        _check(st, "release")
+
+    def evict_idle(self):
+        _check(lib().lia_page_cache_evict_idle(self.handle), "evict_idle")
+
+    @property
+    def gpu_hits(self):
+        a, b = C.c_uint64(), C.c_uint64()
+        lib().lia_page_cache_stats(self.handle, C.byref(a), C.byref(b))
+        return a.value
+
+    @property
+    def evictions(self):
+        a, b = C.c_uint64(), C.c_uint64()
+        lib().lia_page_cache_stats(self.handle, C.byref(a), C.byref(b))
+        return b.value
+
+    def schedule_rows(self, requests, prefill_batch):
+        """Runtime::step row construction (src/server/paged/schedule.rs:5-60).  requests: one
+        dict per slot (tokens, computed, sequence, closed) or None.  Returns (rows as
+        [(token, position, slot)], output row indices, updates [(slot, computed, output)])."""
+        n = len(requests)
+        arr = (Request * max(n, 1))()
+        keep = []
+        for i, r in enumerate(requests):
+            if r is None:
+                continue
+            t = self._tokens(r["tokens"])
+            keep.append(t)
+            arr[i] = Request(t.ctypes.data, t.size, r["computed"], r["sequence"].handle, 1,
+                             int(bool(r.get("closed"))), 0, 0)
+        active = sum(r is not None for r in requests)
+        cap = max(prefill_batch, active, 1)
+        rows = (PagedRow * cap)()
+        outs = (C.c_uint32 * cap)()
+        ups = (Update * max(n, 1))()
+        nr, no, nu = C.c_uint32(), C.c_uint32(), C.c_uint32()
+        _check(lib().lia_schedule_rows(self.handle, n, arr, prefill_batch, rows, cap,
+                                       C.byref(nr), outs, C.byref(no), ups, C.byref(nu)),
+               "schedule_rows")
+        for i, r in enumerate(requests):
+            if r is not None and arr[i].done:
+                r["done"] = True
+        return ([(rows[i].token, rows[i].position, rows[i].sequence) for i in range(nr.value)],
+                [outs[i] for i in range(no.value)],
+                [(ups[i].slot, ups[i].computed, bool(ups[i].output)) for i in range(nu.value)])
 
 
 def workspace_bytes(config):

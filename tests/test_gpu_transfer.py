@@ -1,4 +1,4 @@
-"""GPU tests of KV page transfer through the C ABI: bit-exact against the oracle's wire
+"""GPU tests of KV page transfer (and of the host page manager over it) through the C ABI: bit-exact against the oracle's wire
 layout (oracle.kv_page_payload / kv_page_store) and the reference's own transfer tests
 (src/inference/paging_upload.rs:110-150, tests/minicpm5.rs:98-110)."""
 import numpy as np
@@ -99,3 +99,43 @@ def test_full_window_read_write_matches_oracle(lia, O, kv):
         if fp8:
             assert np.array_equal(ks[layer].cpu().numpy(), nks[layer])
             assert np.array_equal(vs[layer].cpu().numpy(), nvs[layer])
+
+
+def test_page_cache_evicts_and_restores_through_device_pool(lia, O):
+    """The host page manager with its page I/O on the device pool (page_cache.rs:275-287
+    eviction reads a page, attach restores through write_kv_pages): evicted payloads are the
+    pool's bytes, and a restored prefix is bit-identical after the pool was cleared."""
+    print("[case] page cache over the device pool", flush=True)
+    layers, pool_pages = 3, 8
+    L = lia.KVLayout(2, 128, 32, pool_pages, lia.F16)
+    k = [torch.randint(-32768, 32768, (pool_pages * 32, 2, 128), dtype=torch.int16,
+                       device="cuda") for _ in range(layers)]
+    v = [torch.randint(-32768, 32768, (pool_pages * 32, 2, 128), dtype=torch.int16,
+                       device="cuda") for _ in range(layers)]
+    t = lia.KVTransfer(L, k, v)
+    store = {}
+    ns = bytes(range(32))
+    cache = lia.PageCache(ns, pool_pages, 32, store=store, transfer=t)
+    prompt = list(range(1000, 1097))                 # 3 full pages + 1 token
+    seq, cached = cache.attach(prompt)
+    assert cached == 0
+    for pos in range(len(prompt)):
+        assert cache.ensure_position(seq, pos)
+    pages = seq.pages
+    want = t.read_kv_pages(pages[:3])
+    assert want[0] == O.kv_page_payload([x.cpu().numpy() for x in k],
+                                        [x.cpu().numpy() for x in v], pages[0], 32)
+    cache.seal(seq, prompt, len(prompt))
+    cache.release(seq)
+    cache.evict_idle()
+    key, keys = ns, []
+    for b in range(3):
+        key = lia.prefix_key(key, prompt[32 * b:32 * (b + 1)])
+        keys.append(key)
+    assert [store[x] for x in keys] == [bytes(w) for w in want]
+    for x in k + v:
+        x.zero_()
+    seq, cached = cache.attach(prompt)
+    assert cached == 96 and cache.gpu_hits == 0
+    assert t.read_kv_pages(seq.pages) == [bytes(w) for w in want]
+    cache.release(seq)
