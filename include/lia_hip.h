@@ -56,6 +56,11 @@ enum lia_status {
     LIA_E_WORKSPACE = -22,      /* workspace exhausted         gpu/llama_attention.rs:53-61 */
     LIA_E_UNSUPPORTED = -23,    /* geometry this build has no kernel for */
     LIA_E_STORE = -24,          /* a page-store or page-I/O callback failed (positive return) */
+    LIA_E_SAMPLER_SETTINGS = -25, /* temperature / top_k / top_p checks  sampling.rs:33-47 */
+    LIA_E_SAMPLING_LOGITS = -26,  /* "invalid sampling logits", "invalid sampler logits or normalizer" sampling.rs:88-93, gpu/nucleus.rs:106-109 */
+    LIA_E_EMPTY_DISTRIBUTION = -27, /* "empty sampling distribution", "empty greedy vocabulary" sampling.rs:102, paged_sampling.rs:69 */
+    LIA_E_DUPLICATE_CANDIDATE = -28, /* "duplicate sampling candidate"   sampling.rs:104-107 */
+    LIA_E_NUCLEUS = -29,          /* normalizer / nucleus mass / candidate order / candidate id nucleus.rs:56-74,119, gpu/nucleus.rs:127-130 */
     LIA_E_HIP = -30             /* a HIP runtime call failed */
 };
 
@@ -411,6 +416,48 @@ int lia_schedule_rows(lia_page_cache *cache, uint32_t n_slots, lia_request *requ
                       uint32_t prefill_batch, lia_paged_row *rows, uint32_t max_rows,
                       uint32_t *n_rows, uint32_t *outputs, uint32_t *n_outputs,
                       lia_update *updates, uint32_t *n_updates);
+
+/*
+ * Sparse sampling of the paged step's output rows (Engine::forward_paged_sampled,
+ * src/inference/paged_sampling.rs:7-76).
+ *   lia_sampler_*: Sampling (src/sampling.rs:19-190): temperature, top_k 0..20, top_p (0,1],
+ *     MT19937 stream from the seed, or position-keyed Gumbel draws (with_position_gumbel).
+ *   lia_nucleus_candidates: llama_nucleus_candidates (src/gpu/kernels/llama_nucleus.rs:18-117):
+ *     per row and 1024-entry part, 21 (id << 32 | f32 bits) words by descending total order
+ *     (ties: larger id) and (max, f64 mass) normalizers.  Device pointers, async on stream.
+ *   lia_sample_host: the host tail on host copies of those records (logits: the full rows,
+ *     read only for a nucleus fallback).
+ *   lia_sample_paged: the whole tail: temperatures up, kernel, records down, per-row
+ *     sampling, full-row reads for fallbacks; synchronises the stream (as the reference).
+ *     workspace (device) and host buffers of lia_nucleus_workspace_bytes / _host_bytes.
+ * samplers[i] == NULL selects greedy for output row i; positions[i] is the row's position
+ * (Sampling::set_position).  *fallbacks counts full-row reads (nucleus_fallbacks).
+ */
+typedef struct lia_sampler lia_sampler;
+int lia_sampler_create(double temperature, uint32_t top_k, double top_p, uint64_t seed,
+                       int32_t position_keyed, lia_sampler **out);
+void lia_sampler_destroy(lia_sampler *sampler);
+void lia_sampler_set_position(lia_sampler *sampler, uint64_t position);
+/* Sampling::distribution over (ids, logits): n_out entries sorted as the reference sorts. */
+int lia_sampler_distribution(const lia_sampler *sampler, uint32_t n, const uint32_t *ids,
+                             const float *logits, uint32_t *out_ids, double *out_probs,
+                             uint32_t *n_out);
+/* Sampling::draw. */
+int lia_sampler_draw(lia_sampler *sampler, uint32_t n, const uint32_t *ids, const double *probs,
+                     uint32_t *token);
+size_t lia_nucleus_workspace_bytes(uint32_t vocab, uint32_t rows);
+size_t lia_nucleus_host_bytes(uint32_t vocab, uint32_t rows);
+int lia_nucleus_candidates(uint32_t vocab, uint32_t rows, const double *temperatures,
+                           const float *logits, uint64_t *candidates, double *normalizers,
+                           lia_stream_t stream);
+int lia_sample_host(uint32_t vocab, uint32_t n, lia_sampler *const *samplers,
+                    const uint32_t *positions, const uint64_t *candidates,
+                    const double *normalizers, const float *logits, uint32_t *tokens,
+                    uint64_t *fallbacks);
+int lia_sample_paged(uint32_t vocab, uint32_t n, lia_sampler *const *samplers,
+                     const uint32_t *positions, const float *logits, void *workspace,
+                     size_t workspace_bytes, void *host, size_t host_bytes, uint32_t *tokens,
+                     uint64_t *fallbacks, lia_stream_t stream);
 
 #ifdef __cplusplus
 }

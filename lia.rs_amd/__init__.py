@@ -31,6 +31,9 @@ ERRORS = {
     -15: "invalid computed prefix extent", -16: "attempted to overwrite immutable KV page",
     -17: "KV page reference underflow", -18: "cannot evict an active KV page",
     -24: "page store callback failed",
+    -25: "invalid sampling settings", -26: "invalid sampling logits",
+    -27: "empty sampling distribution", -28: "duplicate sampling candidate",
+    -29: "invalid nucleus normalizer, mass or candidates",
     -19: "invalid paging configuration", -20: "invalid argument", -21: "unaligned buffer",
     -22: "workspace exhausted", -23: "unsupported geometry", -30: "HIP runtime error",
 }
@@ -181,6 +184,23 @@ EXPORTS = {
                                     C.POINTER(PagedRow), C.c_uint32, C.POINTER(C.c_uint32),
                                     C.POINTER(C.c_uint32), C.POINTER(C.c_uint32),
                                     C.POINTER(Update), C.POINTER(C.c_uint32)]),
+    "lia_sampler_create": (C.c_int, [C.c_double, C.c_uint32, C.c_double, C.c_uint64, C.c_int32,
+                                     C.POINTER(C.c_void_p)]),
+    "lia_sampler_destroy": (None, [C.c_void_p]),
+    "lia_sampler_set_position": (None, [C.c_void_p, C.c_uint64]),
+    "lia_sampler_distribution": (C.c_int, [C.c_void_p, C.c_uint32, C.c_void_p, C.c_void_p,
+                                           C.c_void_p, C.c_void_p, C.POINTER(C.c_uint32)]),
+    "lia_sampler_draw": (C.c_int, [C.c_void_p, C.c_uint32, C.c_void_p, C.c_void_p,
+                                   C.POINTER(C.c_uint32)]),
+    "lia_nucleus_workspace_bytes": (C.c_size_t, [C.c_uint32, C.c_uint32]),
+    "lia_nucleus_host_bytes": (C.c_size_t, [C.c_uint32, C.c_uint32]),
+    "lia_nucleus_candidates": (C.c_int, [C.c_uint32, C.c_uint32, C.c_void_p, C.c_void_p,
+                                         C.c_void_p, C.c_void_p, C.c_void_p]),
+    "lia_sample_host": (C.c_int, [C.c_uint32, C.c_uint32, C.c_void_p, C.c_void_p, C.c_void_p,
+                                  C.c_void_p, C.c_void_p, C.c_void_p, C.POINTER(C.c_uint64)]),
+    "lia_sample_paged": (C.c_int, [C.c_uint32, C.c_uint32, C.c_void_p, C.c_void_p, C.c_void_p,
+                                   C.c_void_p, C.c_size_t, C.c_void_p, C.c_size_t, C.c_void_p,
+                                   C.POINTER(C.c_uint64), C.c_void_p]),
     "lia_device_cus": (C.c_uint32, []),
     "lia_init": (C.c_int, [C.c_int]),
 }
@@ -444,10 +464,11 @@ class PageCache:
         _check(lib().lia_page_cache_create(bytes(namespace), pages, page_size, C.byref(io),
                                            C.byref(h)), "PageCache")
         self.handle = h
+        self._destroy = lib().lia_page_cache_destroy
 
     def __del__(self):
         if getattr(self, "handle", None):
-            lib().lia_page_cache_destroy(self.handle)
+            self._destroy(self.handle)
             self.handle = None
 
     # callbacks: 0 ok, a negative lia status, or 1 (-> LIA_E_STORE) on a Python error
@@ -576,6 +597,108 @@ class PageCache:
         return ([(rows[i].token, rows[i].position, rows[i].sequence) for i in range(nr.value)],
                 [outs[i] for i in range(no.value)],
                 [(ups[i].slot, ups[i].computed, bool(ups[i].output)) for i in range(nu.value)])
+
+
+class Sampler:
+    """Sampling (src/sampling.rs:19-190) held by the library: temperature, top_k (0 = none,
+    else 1..20), top_p, the seed's MT19937 stream, or position-keyed Gumbel draws."""
+
+    def __init__(self, temperature, top_k, top_p, seed, position_keyed=False):
+        h = C.c_void_p()
+        _check(lib().lia_sampler_create(temperature, top_k, top_p, seed, int(position_keyed),
+                                        C.byref(h)), "Sampler")
+        self.handle = h
+        self._destroy = lib().lia_sampler_destroy   # still reachable at interpreter exit
+        self.temperature, self.top_k, self.top_p = temperature, top_k, top_p
+
+    def __del__(self):
+        if getattr(self, "handle", None):
+            self._destroy(self.handle)
+            self.handle = None
+
+    def set_position(self, position):
+        lib().lia_sampler_set_position(self.handle, position)
+
+    def distribution(self, candidates):
+        """[(id, logit)] -> [(id, probability)] (Sampling::distribution)."""
+        ids = np.array([c[0] for c in candidates], np.uint32)
+        vals = np.array([c[1] for c in candidates], np.float32)
+        n = len(ids)
+        oi = np.zeros(max(n, 1), np.uint32)
+        op = np.zeros(max(n, 1), np.float64)
+        k = C.c_uint32()
+        _check(lib().lia_sampler_distribution(self.handle, n, ids.ctypes.data, vals.ctypes.data,
+                                              oi.ctypes.data, op.ctypes.data, C.byref(k)),
+               "distribution")
+        return [(int(oi[i]), float(op[i])) for i in range(k.value)]
+
+    def draw(self, entries):
+        ids = np.array([e[0] for e in entries], np.uint32)
+        ps = np.array([e[1] for e in entries], np.float64)
+        t = C.c_uint32()
+        _check(lib().lia_sampler_draw(self.handle, len(ids), ids.ctypes.data, ps.ctypes.data,
+                                      C.byref(t)), "draw")
+        return t.value
+
+
+def _sampler_array(samplers):
+    arr = (C.c_void_p * max(len(samplers), 1))()
+    for i, s in enumerate(samplers):
+        arr[i] = s.handle.value if s is not None else None
+    return arr
+
+
+def sample_host(vocab, samplers, positions, candidates, normalizers, logits=None):
+    """Host tail of forward_paged_sampled on host candidate records (lia_sample_host)."""
+    n = len(samplers)
+    pos = np.ascontiguousarray(positions, np.uint32)
+    cand = np.ascontiguousarray(candidates, np.uint64)
+    norm = np.ascontiguousarray(normalizers, np.float64)
+    lg = None if logits is None else np.ascontiguousarray(logits, np.float32)
+    tokens = np.zeros(max(n, 1), np.uint32)
+    fb = C.c_uint64()
+    _check(lib().lia_sample_host(vocab, n, _sampler_array(samplers), pos.ctypes.data,
+                                 cand.ctypes.data, norm.ctypes.data,
+                                 None if lg is None else lg.ctypes.data, tokens.ctypes.data,
+                                 C.byref(fb)), "sample_host")
+    return [int(t) for t in tokens[:n]], fb.value
+
+
+def nucleus_candidates(temperatures, logits, candidates, normalizers, stream=None):
+    """llama_nucleus_candidates on device tensors (lia_nucleus_candidates)."""
+    rows, vocab = logits.shape
+    _check(lib().lia_nucleus_candidates(vocab, rows, _dptr(temperatures), _dptr(logits),
+                                        _dptr(candidates), _dptr(normalizers), _stream(stream)),
+           "nucleus_candidates")
+
+
+class PagedSampler:
+    """Sparse sampling of a step's output rows (Engine::forward_paged_sampled's tail,
+    src/inference/paged_sampling.rs:7-76) with its device workspace and host buffer."""
+
+    def __init__(self, vocab, max_rows, device="cuda"):
+        import torch
+        self.vocab, self.max_rows = vocab, max_rows
+        self.ws_bytes = lib().lia_nucleus_workspace_bytes(vocab, max_rows)
+        self.host_bytes = lib().lia_nucleus_host_bytes(vocab, max_rows)
+        self.workspace = torch.empty(self.ws_bytes, dtype=torch.uint8, device=device)
+        self.host = torch.empty(self.host_bytes, dtype=torch.uint8, pin_memory=True)
+        self.fallbacks = 0
+
+    def sample(self, logits, samplers, positions, stream=None):
+        """logits: device f32 [rows][vocab]; samplers: Sampler or None (greedy) per row."""
+        n = len(samplers)
+        if logits.shape[0] != n or n > self.max_rows or logits.shape[1] != self.vocab:
+            raise LiaError(-20, "sample: logits do not match the sampler rows")
+        pos = np.ascontiguousarray(positions, np.uint32)
+        tokens = np.zeros(max(n, 1), np.uint32)
+        fb = C.c_uint64()
+        _check(lib().lia_sample_paged(self.vocab, n, _sampler_array(samplers), pos.ctypes.data,
+                                      _dptr(logits), _dptr(self.workspace), self.ws_bytes,
+                                      _dptr(self.host), self.host_bytes, tokens.ctypes.data,
+                                      C.byref(fb), _stream(stream)), "sample_paged")
+        self.fallbacks += fb.value
+        return [int(t) for t in tokens[:n]]
 
 
 def workspace_bytes(config):
