@@ -1672,8 +1672,14 @@ static int run_stages(int stages, const lia_attention_config *c, uint32_t n_seqs
     }
     if (stages & kMerge) {
         // units this NT can produce: rows in blocks of rpc per sequence and KV head
-        const uint32_t units_nt = (c->max_rows / (rpc ? rpc : 1) + n_seqs + 1) * c->num_kv_heads;
-        dim3 grid(units_nt < L.max_units ? units_nt : L.max_units, 16 * NT);
+        uint32_t units_nt = (c->max_rows / (rpc ? rpc : 1) + n_seqs + 1) * c->num_kv_heads;
+        uint32_t cols = 16 * NT;
+        if (n_rows == n_seqs) {
+            // one row per sequence: exactly one unit per (sequence, KV head), `group` columns
+            units_nt = n_seqs * c->num_kv_heads;
+            cols = group < cols ? group : cols;
+        }
+        dim3 grid(units_nt < L.max_units ? units_nt : L.max_units, cols);
 #define LIA_COMBINE(DD, NN) hipLaunchKernelGGL((combine_kernel<DD, NN>), grid, dim3(kCombineThreads), 0, s, p)
         const dim3 wgrid(grid.x, 16 * kWideNT / 4);
         if (c->head_dim == 128) {
