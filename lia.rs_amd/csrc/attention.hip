@@ -549,8 +549,7 @@ __device__ __forceinline__ void compute_chunk(const AttnParams &p, const Chunk<D
                 x[j][i] = v;
                 mx = fmaxf(mx, v);
             }
-        mx = fmaxf(mx, shfl_xor(mx, 16));
-        mx = fmaxf(mx, shfl_xor(mx, 32));
+        mx = rows_max(mx);
         const bool first = st.m[nt] == -INFINITY;
         const bool raise = !first && mx > st.m[nt] + 8.0f;
         if (__builtin_amdgcn_ballot_w64(raise)) { // wave-uniform: rare after the first chunk
@@ -814,8 +813,7 @@ __global__ __launch_bounds__(D / 32 * 64, kMinWavesPerEU) void attention_kernel(
 #pragma unroll
         for (int nt = 0; nt < NT; nt++) {
             float lt = st.l[nt];
-            lt += shfl_xor(lt, 16);
-            lt += shfl_xor(lt, 32);
+            lt = rows_sum(lt);
             const uint32_t col = nt * 16 + li;
             if (col >= ncols) continue;
             const uint32_t row = ud.rowbeg + col / p.group;
@@ -1006,8 +1004,7 @@ __device__ __forceinline__ void wide_compute(const AttnParams &p, uint32_t t, WS
                 x[j][i] = v;
                 mx = fmaxf(mx, v);
             }
-        mx = fmaxf(mx, shfl_xor(mx, 16));
-        mx = fmaxf(mx, shfl_xor(mx, 32));
+        mx = rows_max(mx);
         const bool first = st.m[nt] == -INFINITY;
         const bool raise = !first && mx > st.m[nt] + 8.0f;
         if (__builtin_amdgcn_ballot_w64(raise)) {
@@ -1195,8 +1192,7 @@ __global__ __launch_bounds__(64 * LIA_WIDE_WAVES, LIA_WIDE_NTW == 2 ? 2 : 4) voi
 #pragma unroll
         for (int nt = 0; nt < NTW; nt++) {
             float lt = st.l[nt];
-            lt += shfl_xor(lt, 16);
-            lt += shfl_xor(lt, 32);
+            lt = rows_sum(lt);
             const uint32_t col = 16 * NTW * wave + 16 * nt + li;
             if (col >= ncols) continue;
             const uint32_t row = ud.rowbeg + col / p.group;

@@ -102,6 +102,24 @@ __device__ __forceinline__ float shfl_xor(float v, int mask) { return __shfl_xor
 
 __device__ __forceinline__ uint32_t lane_id() { return __lane_id(); }
 
+// Max / sum over the lanes l, l^16, l^32, l^48 (the same position in the wave's four 16-lane
+// rows) with the row-swap instructions: VALU moves, no LDS round trip as a shuffle takes.
+// permlane16_swap(x, x) leaves x of the even row of each row pair in the first result and of
+// the odd row in the second (in every lane of the pair); permlane32_swap does the same for the
+// wave halves.  Both rows of a pair combine the two values in the same order.
+__device__ __forceinline__ float rows_max(float x) {
+    const auto a = __builtin_amdgcn_permlane16_swap(__float_as_uint(x), __float_as_uint(x), false, false);
+    const float y = fmaxf(__uint_as_float(a[0]), __uint_as_float(a[1]));
+    const auto b = __builtin_amdgcn_permlane32_swap(__float_as_uint(y), __float_as_uint(y), false, false);
+    return fmaxf(__uint_as_float(b[0]), __uint_as_float(b[1]));
+}
+__device__ __forceinline__ float rows_sum(float x) {
+    const auto a = __builtin_amdgcn_permlane16_swap(__float_as_uint(x), __float_as_uint(x), false, false);
+    const float y = __uint_as_float(a[0]) + __uint_as_float(a[1]);
+    const auto b = __builtin_amdgcn_permlane32_swap(__float_as_uint(y), __float_as_uint(y), false, false);
+    return __uint_as_float(b[0]) + __uint_as_float(b[1]);
+}
+
 template <typename T>
 __device__ __forceinline__ T uniform(T v) {
     return __builtin_bit_cast(T, __builtin_amdgcn_readfirstlane(__builtin_bit_cast(int, v)));
