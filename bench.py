@@ -27,6 +27,7 @@ ROOT = os.path.dirname(os.path.abspath(__file__))
 sys.path.insert(0, ROOT)
 
 PEAK_HBM_GBPS = 8000.0
+PEAK_BF16_TFLOPS = 2500.0   # dense MFMA, MI355X
 METRIC = "decode-attn tokens/s + achieved HBM GB/s (% peak), ragged batch 8, 1 GPU"
 
 
@@ -47,6 +48,9 @@ def parse():
     ap.add_argument("--traffic", default=os.path.join(ROOT, "profiles",
                                                     "attention_decode_cfg2_traffic.json"),
                     help="HBM traffic per launch measured by rocprofv3 --pmc (JSON summary)")
+    ap.add_argument("--config", type=int, default=2, choices=(2, 3, 4, 5),
+                    help="3, 4 or 5: time one layer of that BASELINE configuration's attention "
+                         "(a parity workload, not the headline line) and print its own JSON line")
     ap.add_argument("--copy-calibration", type=int, default=0, metavar="MIB",
                     help="only run device copies of MIB MiB (the counter calibration kernel)")
     return ap.parse_args()
@@ -73,10 +77,91 @@ def load_traffic(path, kernel_us, layer_bytes):
     return round((t["fetch_kib"] * t["fetch_scale"] + t["write_kib"] * t["write_scale"]) * 1024)
 
 
+def side_config(args):
+    """One layer of BASELINE config 3 (mixed prefill + decode, MFMA-bound), 4 (MTP verify) or
+    5 (FP8 decode) on resident synthetic data: the plan once, then split attention + combine
+    replayed from a graph.  Prints a JSON line with the layer time and its roofline."""
+    import torch
+    from __graft_entry__ import package
+    lia = package()
+    import lia_rs_amd.workloads as wl
+    b = getattr(wl, "config%d" % args.config)(seed=args.seed)
+    g = b.geom
+    P = g.page_size
+    tokens = b.pool_pages * P
+    dev = "cuda"
+    gen = torch.Generator(device=dev)
+    gen.manual_seed(args.seed)
+    fp8 = g.kv_dtype == lia.FP8
+    if fp8:
+        kp = torch.randint(0, 120, (tokens, g.hkv, g.d), generator=gen, dtype=torch.uint8, device=dev)
+        vp = torch.randint(0, 120, (tokens, g.hkv, g.d), generator=gen, dtype=torch.uint8, device=dev)
+        ks = torch.full((b.pool_pages * g.hkv,), 0.01, device=dev)
+        vs = ks.clone()
+    else:
+        kp = torch.randn((tokens, g.hkv, g.d), generator=gen, device=dev).to(torch.bfloat16)
+        vp = torch.randn((tokens, g.hkv, g.d), generator=gen, device=dev).to(torch.bfloat16)
+        ks = vs = None
+    q = torch.randn((b.n_rows, g.hq, g.d), generator=gen, device=dev).to(torch.bfloat16)
+    out = torch.empty((b.n_rows, g.hq, g.d), dtype=torch.bfloat16, device=dev)
+    i32 = lambda a: torch.from_numpy(np.asarray(a, np.uint32).view(np.int32)).to(dev)
+    cu, pos, seq, flat = i32(b.cu_seqlens()), i32(b.positions()), i32(b.sequences()), i32(b.flat_table())
+    cfg = lia.AttentionConfig(g.hq, g.hkv, g.d, P, b.pool_pages, b.stride, g.q_dtype, g.kv_dtype,
+                              g.out_dtype, g.scale, b.n_seqs, b.n_rows, int(b.ctx.max()))
+    ws = torch.zeros(lia.workspace_bytes(cfg), dtype=torch.uint8, device=dev)
+    lia.attention_plan(cfg, b.n_seqs, b.n_rows, cu, pos, seq, ws, pages=flat)
+    reps = max(args.kernel_reps, 1)
+
+    def layer():
+        lia.attention_partial(cfg, b.n_seqs, flat, q, kp, vp, out, ws, k_scales=ks, v_scales=vs)
+        lia.attention_merge(cfg, b.n_seqs, b.n_rows, out, ws)
+
+    layer()
+    torch.cuda.synchronize()
+    graph, stream = torch.cuda.CUDAGraph(), torch.cuda.Stream()
+    with torch.cuda.stream(stream):
+        with torch.cuda.graph(graph, stream=stream):
+            for _ in range(reps):
+                layer()
+    for _ in range(max(args.warmup, 1)):
+        graph.replay()
+    torch.cuda.synchronize()
+    e0, e1 = torch.cuda.Event(enable_timing=True), torch.cuda.Event(enable_timing=True)
+    cur = torch.cuda.current_stream()
+    e0.record(cur)
+    for _ in range(args.steps):
+        graph.replay()
+    e1.record(cur)
+    torch.cuda.synchronize()
+    us = e0.elapsed_time(e1) * 1e3 / (args.steps * reps)
+    nbytes, flops = b.algorithmic_bytes(), b.flops()
+    gbps, tflops = nbytes / (us * 1e-6) / 1e9, flops / (us * 1e-6) / 1e12
+    mfma = args.config == 3
+    names = {3: "mixed chunked-prefill + decode attention", 4: "MTP-verify attention",
+             5: "FP8-KV decode attention"}
+    print(json.dumps({
+        "metric": f"{names[args.config]} us per layer (split attention + combine)",
+        "value": round(us, 3), "unit": "us", "higher_is_better": False, "n_gpus": 1,
+        "steps": args.steps, "warmup": args.warmup, "dtype": "fp8-e4m3 KV, bf16 Q" if fp8 else "bf16",
+        "data": "synthetic (seeded, resident in HBM)",
+        "config": {"workload": f"BASELINE config {args.config}", "rows": b.n_rows,
+                   "sequences": b.n_seqs, "sum_ctx": int(b.ctx.sum())},
+        "roofline": {"bound": "mfma" if mfma else "hbm",
+                     "achieved": round(tflops if mfma else gbps, 1),
+                     "peak": PEAK_BF16_TFLOPS if mfma else PEAK_HBM_GBPS,
+                     "unit": "TFLOP/s" if mfma else "GB/s",
+                     "frac": round((tflops / PEAK_BF16_TFLOPS) if mfma else (gbps / PEAK_HBM_GBPS), 4),
+                     "bytes_per_layer": nbytes, "flops_per_layer": flops},
+    }), flush=True)
+
+
 def main():
     args = parse()
     if args.copy_calibration:
         copy_calibration(args.copy_calibration)
+        return
+    if args.config != 2:
+        side_config(args)
         return
     if args.gpus != 1 or int(os.environ.get("WORLD_SIZE", "1")) > 1:
         print("bench.py: this build measures one GPU only (the path shards by sequence / KV "
