@@ -51,6 +51,9 @@ def parse():
     ap.add_argument("--config", type=int, default=2, choices=(2, 3, 4, 5),
                     help="3, 4 or 5: time one layer of that BASELINE configuration's attention "
                          "(a parity workload, not the headline line) and print its own JSON line")
+    ap.add_argument("--stream-probe", action="store_true",
+                    help="only run the streaming-rate probe on the config-2 pool shape: the read "
+                         "ceiling of the kernel's page pattern and of other load mappings")
     ap.add_argument("--copy-calibration", type=int, default=0, metavar="MIB",
                     help="only run device copies of MIB MiB (the counter calibration kernel)")
     return ap.parse_args()
@@ -155,8 +158,33 @@ def side_config(args):
     }), flush=True)
 
 
+def stream_probe(args):
+    """The probe program built beside the library (csrc/stream_probe.hip), run on the
+    config-2 pool shape: pages of 16 tokens, 2 KV heads, head_dim 128, the seed's contexts,
+    8 pool copies rotated so no launch reads cache-resident data.  Prints its JSON lines."""
+    import subprocess
+    from __graft_entry__ import package
+    package()
+    import lia_rs_amd.workloads as wl
+    b = wl.config2(seed=args.seed, layers=1)
+    g = b.geom
+    exe = os.path.join(ROOT, "lia.rs_amd", "stream_probe")
+    if not os.path.exists(exe):
+        raise SystemExit("stream_probe is not built (run __graft_entry__.build())")
+    cmd = [exe, str(g.page_size), str(g.hkv), str(g.d), "8", *[str(int(c)) for c in b.ctx]]
+    log("running " + " ".join(cmd))
+    r = subprocess.run(cmd, stdout=subprocess.PIPE, timeout=300)
+    sys.stdout.write(r.stdout.decode())
+    sys.stdout.flush()
+    if r.returncode:
+        raise SystemExit(f"stream_probe exited with {r.returncode}")
+
+
 def main():
     args = parse()
+    if args.stream_probe:
+        stream_probe(args)
+        return
     if args.copy_calibration:
         copy_calibration(args.copy_calibration)
         return
