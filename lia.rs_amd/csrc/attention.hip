@@ -255,10 +255,16 @@ struct Cfg {
     static constexpr bool FP8 = KVT == LIA_FP8_E4M3;
     static constexpr bool MBF16 = KVT == LIA_BF16;  // MFMA operand type (f16 for f16 and FP8)
     static constexpr int EB = FP8 ? 1 : 2;          // bytes per stored KV element
-    static constexpr int WAVES = D / 32;            // one wave per 32-dim slice
+    // Each wave owns a head_dim slice of SW dims, 64 bytes of a token either way: 32 dims
+    // of a 16-bit pool, 64 dims of an FP8 pool.  A lane loads 16 contiguous bytes of a token
+    // per 16-token tile (its A-operand k slots for KS k-steps), so every load instruction
+    // reads 16 tokens x 64 bytes.
+    static constexpr int SW = FP8 ? 64 : 32;
+    static constexpr int WAVES = D / SW;            // one wave per slice
+    static constexpr int KS = SW / 32;              // k-steps of S^T = K Q^T per tile
+    static constexpr int DTW = SW / 16;             // 16-dim tiles of O per wave
     static constexpr int THREADS = WAVES * 64;
-    static constexpr int SLICE = 32 * EB;           // bytes of one token's slice (one head)
-    static constexpr int STAGE = 32 * 32;           // staged V per wave: [32 tokens][32] 16-bit
+    static constexpr int STAGE = 32 * SW;           // staged V per wave: [32 tokens][SW] 16-bit
 };
 
 // Staged V rows hold 32 16-bit values (4 chunks of 16 bytes); chunk c of row r sits in
@@ -266,10 +272,18 @@ struct Cfg {
 // chunks {2n, 2n+1}) on distinct banks.
 __device__ __forceinline__ uint32_t swz(uint32_t row) { return 2 * ((row >> 1) & 1); }
 
+// Swizzle of a staged V row of SW 16-bit values: 32-value rows as above; 64-value rows
+// (128 bytes) flip the chunk pair by row bit 2, so rows r and r + 4 of a transpose read (the
+// same banks otherwise) land on distinct banks.
+template <int SW>
+__device__ __forceinline__ uint32_t vswz(uint32_t row) {
+    return SW == 32 ? swz(row) : 2 * ((row >> 2) & 1);
+}
+
 template <int D, int KVT>
 struct Chunk {
-    uint32_t k[2][Cfg<D, KVT>::FP8 ? 2 : 4]; // A operand words of the two 16-token tiles
-    u32x4 v;                                   // FP8 only: the wave's V slice, staged later
+    uint32_t k[2][4]; // per 16-token tile: this lane's 16 bytes of K (A-operand k slots)
+    u32x4 v[2];       // FP8 only: this lane's 16 bytes of V per tile, staged later
     float ks[2], vs[2];
 };
 
@@ -377,7 +391,7 @@ __device__ __forceinline__ void load_chunk(const AttnParams &p, Chunk<D, KVT> &c
     const uint32_t lane = lane_id(), g = lane >> 4, li = lane & 15;
     const uint32_t P = 1u << p.page_shift;
     const uint32_t row_bytes = p.hkv * D * C::EB; // bytes per slot (all KV heads)
-    const uint32_t slice_off = (hk * D + 32 * wave) * C::EB;
+    const uint32_t slice_off = (hk * D + C::SW * wave) * C::EB;
     __amdgpu_buffer_rsrc_t r[2];
 #pragma unroll
     for (int j = 0; j < 2; j++) {
@@ -387,34 +401,27 @@ __device__ __forceinline__ void load_chunk(const AttnParams &p, Chunk<D, KVT> &c
             c.vs[j] = tp.vs[j];
         }
     }
-    // K: lane (g, li) of tile j reads token 16j+li, dims 32w + 8g .. +7 (the four groups
-    // of a token cover its 32-dim slice contiguously).
+    // K: lane (g, li) of tile j reads token 16j+li, bytes 16g .. 16g+15 of the wave's slice
+    // (the four groups of a token cover its 64-byte slice contiguously): dims 32w + 8g .. +7
+    // of a 16-bit pool, dims 64w + 16g .. +15 of an FP8 pool (k slots 8g..8g+7 of k-step s
+    // hold dims 64w + 16g + 8s .. +7, and Q is loaded to match).
 #pragma unroll
     for (int j = 0; j < 2; j++) {
-        const uint32_t off = (((t + 16 * j) & (P - 1)) + li) * row_bytes + slice_off + 8 * g * C::EB;
-        if constexpr (C::FP8) {
-            auto x = __builtin_amdgcn_raw_buffer_load_b64(r[j], (int)off, 0, 0);
-            c.k[j][0] = x[0];
-            c.k[j][1] = x[1];
-        } else {
-            u32x4 x = buffer_load16(r[j], off);
-            c.k[j][0] = x.x; c.k[j][1] = x.y; c.k[j][2] = x.z; c.k[j][3] = x.w;
-        }
+        const uint32_t off = (((t + 16 * j) & (P - 1)) + li) * row_bytes + slice_off + 16 * g;
+        u32x4 x = buffer_load16(r[j], off);
+        c.k[j][0] = x.x; c.k[j][1] = x.y; c.k[j][2] = x.z; c.k[j][3] = x.w;
     }
     if constexpr (C::FP8) {
-        // V slice (32 bytes per token) into registers: lane l reads token l/2, bytes
-        // 16*(l%2) .. +16, through a descriptor over the V plane bounded like K's.
-        const uint32_t tok = lane >> 1;
-        __amdgpu_buffer_rsrc_t vr[2];
+        // V slice into registers: lane l of tile j reads token 16j + l/4, bytes 16(l%4) ..
+        // +15 of the slice (16 dims), through a descriptor over the V plane bounded like K's.
 #pragma unroll
-        for (int jj = 0; jj < 2; jj++)
-            vr[jj] = make_rsrc(vbase + (size_t)tp.page[jj] * P * row_bytes, tp.live[jj] * row_bytes);
-        const uint32_t off = (((t + 16 * (tok >> 4)) & (P - 1)) + (tok & 15)) * row_bytes + slice_off +
-                             16 * (lane & 1);
-        // lanes 0-31 read tile 0, lanes 32-63 tile 1: two loads, each with half the lanes live
-        const u32x4 a = buffer_load16(vr[0], tok < 16 ? off : 0xFFFFFFF0u);
-        const u32x4 b = buffer_load16(vr[1], tok >= 16 ? off : 0xFFFFFFF0u);
-        c.v = tok < 16 ? a : b;
+        for (int j = 0; j < 2; j++) {
+            const __amdgpu_buffer_rsrc_t vr =
+                make_rsrc(vbase + (size_t)tp.page[j] * P * row_bytes, tp.live[j] * row_bytes);
+            const uint32_t off = (((t + 16 * j) & (P - 1)) + (lane >> 2)) * row_bytes + slice_off +
+                                 16 * (lane & 3);
+            c.v[j] = buffer_load16(vr, off);
+        }
     } else {
         // V slice goes straight to this wave's LDS stage: instruction s fills rows
         // 16s .. 16s+15, lane l writes slot l%4 of row 16s + l/4 with the swizzled chunk.
@@ -434,15 +441,15 @@ __device__ __forceinline__ void load_chunk(const AttnParams &p, Chunk<D, KVT> &c
     __builtin_amdgcn_sched_barrier(0);
 }
 
-// Query operand of one 16-column tile for this wave's d slice: lane (g, col) holds
-// q[col][32w + 8g .. +7] - the dims the K loads put in the same k slots.  Padding columns
-// load from an out-of-range offset (zeros) so the loads are unconditional.
+// Query operand of one 16-column tile for this wave's d slice, k-step s: lane (g, col) holds
+// q[col][SW*w + (SW/4)*g + 8s .. +7] - the dims the K loads put in the same k slots.
+// Padding columns load from an out-of-range offset (zeros) so the loads are unconditional.
 template <int D, int KVT>
 __device__ __forceinline__ u32x4 load_q(const AttnParams &p, uint32_t row, uint32_t head,
-                                        bool valid, uint32_t wave) {
+                                        bool valid, uint32_t wave, uint32_t s) {
     using C = Cfg<D, KVT>;
     const uint32_t g = lane_id() >> 4;
-    const uint32_t at = (row * p.hq + head) * D + 32 * wave + 8 * g;
+    const uint32_t at = (row * p.hq + head) * D + C::SW * wave + (C::SW / 4) * g + 8 * s;
     const uint32_t qb = p.q_f32 ? 4 : 2;
     const __amdgpu_buffer_rsrc_t r = make_rsrc(p.q, p.n_rows * p.hq * D * qb);
     const uint32_t off = valid ? at * qb : 0x80000000u;
@@ -469,11 +476,11 @@ __device__ __forceinline__ u32x4 load_q(const AttnParams &p, uint32_t row, uint3
 
 template <int D, int NT, int KVT>
 struct State {
-    u32x4 qr[NT];
+    u32x4 qr[NT][Cfg<D, KVT>::KS];
     uint32_t lo;       // first key of the current range (wave-uniform)
     uint32_t lim[NT];  // per column: live keys of the range, counted from lo
     float m[NT], l[NT];
-    f32x4 o[NT][2];
+    f32x4 o[NT][Cfg<D, KVT>::DTW];
 };
 
 // One chunk: partial scores for this wave's d slice, cross-wave sum through LDS, online
@@ -485,14 +492,18 @@ __device__ __forceinline__ void compute_chunk(const AttnParams &p, const Chunk<D
     using C = Cfg<D, KVT>;
     const uint32_t lane = lane_id(), g = lane >> 4, li = lane & 15;
     if constexpr (C::FP8) {
-        // convert the wave's FP8 V slice (16 values per lane) to f16 and stage it swizzled
-        const uint32_t row = lane >> 1;
-        u32x2 a = e4m3x4_to_f16x4_scaled(c.v.x), b = e4m3x4_to_f16x4_scaled(c.v.y);
-        u32x2 e = e4m3x4_to_f16x4_scaled(c.v.z), f = e4m3x4_to_f16x4_scaled(c.v.w);
-        uint16_t *dst = stage + row * 32;
-        const uint32_t c0 = 2 * (lane & 1);
-        *(u32x4 *)(dst + ((c0 ^ swz(row)) * 8)) = u32x4{a.x, a.y, b.x, b.y};
-        *(u32x4 *)(dst + (((c0 + 1) ^ swz(row)) * 8)) = u32x4{e.x, e.y, f.x, f.y};
+        // convert the wave's FP8 V slice (16 values per lane and tile) to f16 and stage it:
+        // lane l of tile j holds dims 16(l%4) .. +15 of token 16j + l/4 = 8-value chunks
+        // 2(l%4) and 2(l%4) + 1 of that row
+#pragma unroll
+        for (int j = 0; j < 2; j++) {
+            const uint32_t row = 16 * j + (lane >> 2), c0 = 2 * (lane & 3);
+            const u32x2 a = e4m3x4_to_f16x4_scaled(c.v[j].x), b = e4m3x4_to_f16x4_scaled(c.v[j].y);
+            const u32x2 e = e4m3x4_to_f16x4_scaled(c.v[j].z), f = e4m3x4_to_f16x4_scaled(c.v[j].w);
+            uint16_t *dst = stage + row * C::SW;
+            *(u32x4 *)(dst + ((c0 ^ vswz<C::SW>(row)) * 8)) = u32x4{a.x, a.y, b.x, b.y};
+            *(u32x4 *)(dst + (((c0 + 1) ^ vswz<C::SW>(row)) * 8)) = u32x4{e.x, e.y, f.x, f.y};
+        }
     } else {
         wait_vmcnt<VW>(); // this chunk's V is in LDS (VW = memory ops issued after its loads)
     }
@@ -510,14 +521,20 @@ __device__ __forceinline__ void compute_chunk(const AttnParams &p, const Chunk<D
     for (int nt = 0; nt < NT; nt++) {
 #pragma unroll
         for (int j = 0; j < 2; j++) {
-            u32x4 a;
-            if constexpr (C::FP8) {
-                u32x2 x0 = e4m3x4_to_f16x4_scaled(c.k[j][0]), x1 = e4m3x4_to_f16x4_scaled(c.k[j][1]);
-                a = u32x4{x0.x, x0.y, x1.x, x1.y};
-            } else {
-                a = u32x4{c.k[j][0], c.k[j][1], c.k[j][2], c.k[j][3]};
+            f32x4 sp = f32x4{0.0f, 0.0f, 0.0f, 0.0f};
+#pragma unroll
+            for (int ks = 0; ks < C::KS; ks++) {
+                u32x4 a;
+                if constexpr (C::FP8) {
+                    // k-step ks: bytes 8ks .. 8ks+7 of the lane's 16
+                    u32x2 x0 = e4m3x4_to_f16x4_scaled(c.k[j][2 * ks]);
+                    u32x2 x1 = e4m3x4_to_f16x4_scaled(c.k[j][2 * ks + 1]);
+                    a = u32x4{x0.x, x0.y, x1.x, x1.y};
+                } else {
+                    a = u32x4{c.k[j][0], c.k[j][1], c.k[j][2], c.k[j][3]};
+                }
+                sp = mfma16x16x32<C::MBF16>(a, st.qr[nt][ks], sp);
             }
-            f32x4 sp = mfma16x16x32<C::MBF16>(a, st.qr[nt], f32x4{0.0f, 0.0f, 0.0f, 0.0f});
             sx[((wave * NT + nt) * 2 + j) * 64 + lane] = sp;
         }
     }
@@ -555,8 +572,8 @@ __device__ __forceinline__ void compute_chunk(const AttnParams &p, const Chunk<D
         if (__builtin_amdgcn_ballot_w64(raise)) { // wave-uniform: rare after the first chunk
             const float factor = raise ? fast_exp2(st.m[nt] - mx) : 1.0f;
             st.l[nt] *= factor;
-            st.o[nt][0] *= factor;
-            st.o[nt][1] *= factor;
+#pragma unroll
+            for (int n = 0; n < C::DTW; n++) st.o[nt][n] *= factor;
         }
         if (first || raise) st.m[nt] = mx;
         const float muse = st.m[nt] == -INFINITY ? 0.0f : st.m[nt];
@@ -574,12 +591,12 @@ __device__ __forceinline__ void compute_chunk(const AttnParams &p, const Chunk<D
         const u32x4 pb = u32x4{pack2<C::MBF16>(pr[0][0], pr[0][1]), pack2<C::MBF16>(pr[0][2], pr[0][3]),
                                pack2<C::MBF16>(pr[1][0], pr[1][1]), pack2<C::MBF16>(pr[1][2], pr[1][3])};
 #pragma unroll
-        for (int n = 0; n < 2; n++) {
+        for (int n = 0; n < C::DTW; n++) {
             // V^T operand: d rows 16n .. 16n+15 of the slice, k slots = tokens
             // {4g..4g+3, 16+4g..16+4g+3} (transpose reads of the staged rows).
             const uint32_t row0 = 4 * g + li / 4, ch = 2 * n + ((li & 3) >> 1);
-            const uint16_t *r0 = stage + row0 * 32 + ((ch ^ swz(row0)) * 8) + (li & 1) * 4;
-            const uint16_t *r1 = r0 + 16 * 32; // row0 + 16 has the same swizzle
+            const uint16_t *r0 = stage + row0 * C::SW + ((ch ^ vswz<C::SW>(row0)) * 8) + (li & 1) * 4;
+            const uint16_t *r1 = r0 + 16 * C::SW; // row0 + 16 has the same swizzle
             s16x4 a0 = __builtin_amdgcn_ds_read_tr16_b64_v4i16(
                 (__attribute__((address_space(3))) s16x4 *)(r0));
             s16x4 a1 = __builtin_amdgcn_ds_read_tr16_b64_v4i16(
@@ -698,14 +715,15 @@ __device__ __forceinline__ void append_rows(const AttnParams &p, uint32_t wg, ui
     }
 }
 
-// One column's split record: unnormalised O for this wave's d slice, reference max and mass.
-template <int D>
-__device__ __forceinline__ void store_record(const AttnParams &p, size_t rb, const f32x4 (&o)[2],
+// One column's split record: unnormalised O for this wave's d slice (SW dims), reference
+// max and mass.
+template <int D, int SW>
+__device__ __forceinline__ void store_record(const AttnParams &p, size_t rb, const f32x4 (&o)[SW / 16],
                                              float m, float l, uint32_t wave) {
     const uint32_t g = lane_id() >> 4;
-    float *po = p.part_o + rb * D + 32 * wave + 4 * g;
+    float *po = p.part_o + rb * D + SW * wave + 4 * g;
 #pragma unroll
-    for (int n = 0; n < 2; n++) *(f32x4 *)(po + 16 * n) = o[n];
+    for (int n = 0; n < SW / 16; n++) *(f32x4 *)(po + 16 * n) = o[n];
     if (wave == 0 && g == 0) {
         p.part_ml[rb * 2] = m;
         p.part_ml[rb * 2 + 1] = l;
@@ -764,10 +782,13 @@ __global__ __launch_bounds__(D / 32 * 64, kMinWavesPerEU) void attention_kernel(
             const bool valid = col < ncols;
             const uint32_t ri = valid ? col / p.group : 0;
             climit[nt] = valid ? pos0 + ri + 1 : 0;
-            st.qr[nt] = load_q<D, KVT>(p, ud.rowbeg + ri, hk * p.group + col % p.group, valid, wave);
+#pragma unroll
+            for (int ks = 0; ks < C::KS; ks++)
+                st.qr[nt][ks] = load_q<D, KVT>(p, ud.rowbeg + ri, hk * p.group + col % p.group, valid, wave, ks);
             st.m[nt] = -INFINITY;
             st.l[nt] = 0.0f;
-            st.o[nt][0] = st.o[nt][1] = f32x4{0.0f, 0.0f, 0.0f, 0.0f};
+#pragma unroll
+            for (int n = 0; n < C::DTW; n++) st.o[nt][n] = f32x4{0.0f, 0.0f, 0.0f, 0.0f};
         }
         // Block i of the unit covers keys [32i, 32i+32) of the cached run for i < cb and
         // [kcache + 32(i-cb), ...) of the new run otherwise.
@@ -820,9 +841,9 @@ __global__ __launch_bounds__(D / 32 * 64, kMinWavesPerEU) void attention_kernel(
             const uint32_t head = hk * p.group + col % p.group;
             if (whole) {
                 const float inv = lt > 0.0f ? 1.0f / lt : 0.0f;
-                const size_t base = ((size_t)row * p.hq + head) * D + 32 * wave + 4 * g;
+                const size_t base = ((size_t)row * p.hq + head) * D + C::SW * wave + 4 * g;
 #pragma unroll
-                for (int n = 0; n < 2; n++) {
+                for (int n = 0; n < C::DTW; n++) {
                     const f32x4 v = st.o[nt][n] * inv;
                     if (p.out_f32) {
                         *(f32x4 *)((float *)p.out + base + 16 * n) = v;
@@ -832,7 +853,7 @@ __global__ __launch_bounds__(D / 32 * 64, kMinWavesPerEU) void attention_kernel(
                     }
                 }
             } else {
-                store_record<D>(p, (size_t)rec * COLS + col, st.o[nt], st.m[nt], lt, wave);
+                store_record<D, C::SW>(p, (size_t)rec * COLS + col, st.o[nt], st.m[nt], lt, wave);
             }
         }
         lo = seg_end;
@@ -1435,9 +1456,12 @@ static Layout layout_for(const lia_attention_config *c, uint32_t n_wg) {
     off = (off + 255) & ~(size_t)255;
     L.merge = off; off += (size_t)L.max_units * sizeof(MergeDesc);
     off = (off + 255) & ~(size_t)255;
-    L.part_ml = off; off += (size_t)L.max_records * 16 * kWideNT * 2 * sizeof(float);
+    // record columns: 16 per tile, up to two tiles on the decode kernel (FP8 pools) or the
+    // prefill kernel's kWideNT
+    const size_t rec_cols = 16 * (c->kv_dtype == LIA_FP8_E4M3 ? 2 : kWideNT);
+    L.part_ml = off; off += (size_t)L.max_records * rec_cols * 2 * sizeof(float);
     off = (off + 255) & ~(size_t)255;
-    L.part_o = off; off += (size_t)L.max_records * 16 * kWideNT * c->head_dim * sizeof(float);
+    L.part_o = off; off += (size_t)L.max_records * rec_cols * c->head_dim * sizeof(float);
     L.total = off;
     return L;
 }
@@ -1478,12 +1502,24 @@ extern "C" uint32_t lia_device_cus(void) {
 #endif
 constexpr uint32_t kMaxPerCU = LIA_MAX_WG_PER_CU;
 constexpr uint32_t kOversub2 = LIA_WG_OVERSUB2;
+// Decode kernel: at most this many waves per CU (three 4-wave workgroups measured best on
+// 16-bit pools; FP8 pools run 2-wave workgroups, so six of them).
+constexpr uint32_t kMaxWavesPerCU = 12;
 
-// Upper bound on attention workgroups per launch: sizes the plan and the record area.
-static uint32_t max_workgroups() {
+static uint32_t decode_waves(uint32_t d, int kv) { return kv == LIA_FP8_E4M3 ? d / 64 : d / 32; }
+
+// Resident workgroups per CU allowed for a launch of NT column tiles.
+static uint32_t max_per_cu(uint32_t d, uint32_t nt, int kv) {
+    return nt == kWideNT ? kMaxPerCU : kMaxWavesPerCU / decode_waves(d, kv);
+}
+
+// Upper bound on attention workgroups per launch of a configuration: sizes the plan and
+// the record area.
+static uint32_t max_workgroups(const lia_attention_config *c) {
     uint32_t cus = lia_device_cus();
     if (!cus) cus = 256;
-    return cus * kMaxPerCU * kOversub2 / 2;
+    const uint32_t per = max(kMaxPerCU, kMaxWavesPerCU / decode_waves(c->head_dim, c->kv_dtype));
+    return cus * per * kOversub2 / 2;
 }
 
 template <int D, int NT, int KVT>
@@ -1528,22 +1564,24 @@ static uint32_t resident_kv(int kv) {
 }
 
 // Workgroups of one launch: every CU filled once with resident workgroups.
-static uint32_t workgroups_for(uint32_t d, uint32_t nt, int kv) {
+static uint32_t workgroups_for(const lia_attention_config *c, uint32_t nt) {
+    const uint32_t d = c->head_dim;
+    const int kv = c->kv_dtype;
     uint32_t cus = lia_device_cus();
     if (!cus) cus = 256;
     uint32_t per = d == 128 ? (nt == 1 ? resident_kv<128, 1>(kv)
                                : nt == 2 ? resident_kv<128, 2>(kv) : resident_kv<128, kWideNT>(kv))
                             : (nt == 1 ? resident_kv<64, 1>(kv)
                                : nt == 2 ? resident_kv<64, 2>(kv) : resident_kv<64, kWideNT>(kv));
-    if (per > kMaxPerCU) per = kMaxPerCU;
+    if (per > max_per_cu(d, nt, kv)) per = max_per_cu(d, nt, kv);
     uint32_t n = cus * per * kOversub2 / 2;
-    uint32_t cap = max_workgroups();
+    uint32_t cap = max_workgroups(c);
     return n < cap ? n : cap;
 }
 
 extern "C" size_t lia_attention_workspace_bytes(const lia_attention_config *c) {
     if (!c || !c->num_kv_heads) return 0;
-    return layout_for(c, max_workgroups()).total;
+    return layout_for(c, max_workgroups(c)).total;
 }
 
 static int validate(const lia_attention_config *c) {
@@ -1618,12 +1656,12 @@ static int run_stages(int stages, const lia_attention_config *c, uint32_t n_seqs
     if ((uint64_t)c->max_rows * c->num_q_heads * c->head_dim * 4 >= (1ull << 31) ||
         (uint64_t)c->pool_pages * c->num_kv_heads * 4 >= (1ull << 31))
         return LIA_E_UNSUPPORTED;
-    Layout L = layout_for(c, max_workgroups());
+    Layout L = layout_for(c, max_workgroups(c));
     if (workspace_bytes < L.total) return LIA_E_WORKSPACE;
     if ((uintptr_t)workspace & 255) return LIA_E_ALIGN;
     const uint32_t group = c->num_q_heads / c->num_kv_heads;
     const uint32_t NT = nt_for(n_rows, n_seqs, group, c->kv_dtype);
-    const uint32_t n_wg = workgroups_for(c->head_dim, NT, c->kv_dtype);
+    const uint32_t n_wg = workgroups_for(c, NT);
     const uint32_t rpc = (16 * NT) / group;
     uint8_t *ws = (uint8_t *)workspace;
     AttnParams p;
