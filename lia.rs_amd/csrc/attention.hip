@@ -250,6 +250,10 @@ __global__ __launch_bounds__(256) void plan_kernel(uint32_t n_seqs, const uint32
 // therefore split evenly whatever the segment lengths, and no end-of-segment merge is
 // needed: each wave writes its own slice of the output or of the split record.
 
+#ifndef LIA_SW16
+#define LIA_SW16 32
+#endif
+
 template <int D, int KVT>
 struct Cfg {
     static constexpr bool FP8 = KVT == LIA_FP8_E4M3;
@@ -259,12 +263,17 @@ struct Cfg {
     // of a 16-bit pool, 64 dims of an FP8 pool.  A lane loads 16 contiguous bytes of a token
     // per 16-token tile (its A-operand k slots for KS k-steps), so every load instruction
     // reads 16 tokens x 64 bytes.
-    static constexpr int SW = FP8 ? 64 : 32;
+    static constexpr int SW = FP8 ? 64 : LIA_SW16;
     static constexpr int WAVES = D / SW;            // one wave per slice
     static constexpr int KS = SW / 32;              // k-steps of S^T = K Q^T per tile
     static constexpr int DTW = SW / 16;             // 16-dim tiles of O per wave
     static constexpr int THREADS = WAVES * 64;
     static constexpr int STAGE = 32 * SW;           // staged V per wave: [32 tokens][SW] 16-bit
+    static constexpr int KL = FP8 ? 1 : KS;         // K loads per tile (16 bytes each)
+    static constexpr int KW = 4 * KL;               // K words per tile and lane
+    static constexpr int CPR = SW / 8;              // 16-byte chunks of a staged V row
+    static constexpr int VRPI = 64 / CPR;           // staged V rows per direct-to-LDS load
+    static constexpr int NV = FP8 ? 2 : 32 / VRPI;  // V loads per chunk
 };
 
 // Staged V rows hold 32 16-bit values (4 chunks of 16 bytes); chunk c of row r sits in
@@ -282,7 +291,7 @@ __device__ __forceinline__ uint32_t vswz(uint32_t row) {
 
 template <int D, int KVT>
 struct Chunk {
-    uint32_t k[2][4]; // per 16-token tile: this lane's 16 bytes of K (A-operand k slots)
+    uint32_t k[2][Cfg<D, KVT>::KW]; // per 16-token tile: this lane's K bytes (A-operand k slots)
     u32x4 v[2];       // FP8 only: this lane's 16 bytes of V per tile, staged later
     float ks[2], vs[2];
 };
@@ -376,7 +385,7 @@ __device__ __forceinline__ void wait_vmcnt() {
 
 // Vector-memory operations one load_chunk issues (the pipeline waits on this count).
 template <int D, int KVT>
-constexpr int kLoadsPerChunk = 4; // two K loads + two V loads
+constexpr int kLoadsPerChunk = 2 * Cfg<D, KVT>::KL + Cfg<D, KVT>::NV; // K loads + V loads
 
 // Loads chunk t (32 tokens, t a multiple of 32) of this wave's d slice from the planes at
 // kbase / vbase (the pool, or the step's new rows).  Buffer loads are bounded to each
@@ -405,11 +414,16 @@ __device__ __forceinline__ void load_chunk(const AttnParams &p, Chunk<D, KVT> &c
     // (the four groups of a token cover its 64-byte slice contiguously): dims 32w + 8g .. +7
     // of a 16-bit pool, dims 64w + 16g .. +15 of an FP8 pool (k slots 8g..8g+7 of k-step s
     // hold dims 64w + 16g + 8s .. +7, and Q is loaded to match).
+    // A 16-bit slice of 64 dims takes two loads per tile, bytes 64q + 16g (dims 32q + 8g ..
+    // +7 = k-step q), so each load instruction still reads 64 contiguous bytes of a token.
 #pragma unroll
     for (int j = 0; j < 2; j++) {
-        const uint32_t off = (((t + 16 * j) & (P - 1)) + li) * row_bytes + slice_off + 16 * g;
-        u32x4 x = buffer_load16(r[j], off);
-        c.k[j][0] = x.x; c.k[j][1] = x.y; c.k[j][2] = x.z; c.k[j][3] = x.w;
+#pragma unroll
+        for (int q = 0; q < C::KL; q++) {
+            const uint32_t off = (((t + 16 * j) & (P - 1)) + li) * row_bytes + slice_off + 64 * q + 16 * g;
+            u32x4 x = buffer_load16(r[j], off);
+            c.k[j][4 * q] = x.x; c.k[j][4 * q + 1] = x.y; c.k[j][4 * q + 2] = x.z; c.k[j][4 * q + 3] = x.w;
+        }
     }
     if constexpr (C::FP8) {
         // V slice into registers: lane l of tile j reads token 16j + l/4, bytes 16(l%4) ..
@@ -423,17 +437,17 @@ __device__ __forceinline__ void load_chunk(const AttnParams &p, Chunk<D, KVT> &c
             c.v[j] = buffer_load16(vr, off);
         }
     } else {
-        // V slice goes straight to this wave's LDS stage: instruction s fills rows
-        // 16s .. 16s+15, lane l writes slot l%4 of row 16s + l/4 with the swizzled chunk.
+        // V slice goes straight to this wave's LDS stage: load s fills rows VRPI*s ..
+        // +VRPI-1, lane l writes slot l%CPR of row VRPI*s + l/CPR with the swizzled chunk.
         __builtin_amdgcn_s_waitcnt(0xC07F); // lgkmcnt(0): earlier reads of this stage are done
 #pragma unroll
-        for (int s = 0; s < 2; s++) {
-            const uint32_t t0 = t + 16 * s;
+        for (int s = 0; s < C::NV; s++) {
+            const uint32_t j = (C::VRPI * s) / 16; // the load's 16-token tile
             const __amdgpu_buffer_rsrc_t vr =
-                make_rsrc(vbase + (size_t)tp.page[s] * P * row_bytes, tp.live[s] * row_bytes);
-            const uint32_t row = 16 * s + (lane >> 2);
-            const uint32_t chunk = (lane & 3) ^ swz(row);
-            const uint32_t off = ((t0 & (P - 1)) + (row & 15)) * row_bytes + slice_off + 16 * chunk;
+                make_rsrc(vbase + (size_t)tp.page[j] * P * row_bytes, tp.live[j] * row_bytes);
+            const uint32_t row = C::VRPI * s + lane / C::CPR;
+            const uint32_t chunk = (lane % C::CPR) ^ vswz<C::SW>(row);
+            const uint32_t off = (((t + 16 * j) & (P - 1)) + (row & 15)) * row_bytes + slice_off + 16 * chunk;
             __builtin_amdgcn_raw_ptr_buffer_load_lds(
                 vr, (__attribute__((address_space(3))) void *)(stage + s * 512), 16, off, 0, 0, 0);
         }
@@ -449,7 +463,9 @@ __device__ __forceinline__ u32x4 load_q(const AttnParams &p, uint32_t row, uint3
                                         bool valid, uint32_t wave, uint32_t s) {
     using C = Cfg<D, KVT>;
     const uint32_t g = lane_id() >> 4;
-    const uint32_t at = (row * p.hq + head) * D + C::SW * wave + (C::SW / 4) * g + 8 * s;
+    // FP8: a lane's 16 bytes hold dims 16g .. 16g+15 (k-steps 0, 1); 16-bit: load s holds
+    // dims 32s + 8g .. +7
+    const uint32_t at = (row * p.hq + head) * D + C::SW * wave + (C::FP8 ? 16 * g + 8 * s : 32 * s + 8 * g);
     const uint32_t qb = p.q_f32 ? 4 : 2;
     const __amdgpu_buffer_rsrc_t r = make_rsrc(p.q, p.n_rows * p.hq * D * qb);
     const uint32_t off = valid ? at * qb : 0x80000000u;
@@ -531,7 +547,7 @@ __device__ __forceinline__ void compute_chunk(const AttnParams &p, const Chunk<D
                     u32x2 x1 = e4m3x4_to_f16x4_scaled(c.k[j][2 * ks + 1]);
                     a = u32x4{x0.x, x0.y, x1.x, x1.y};
                 } else {
-                    a = u32x4{c.k[j][0], c.k[j][1], c.k[j][2], c.k[j][3]};
+                    a = u32x4{c.k[j][4 * ks], c.k[j][4 * ks + 1], c.k[j][4 * ks + 2], c.k[j][4 * ks + 3]};
                 }
                 sp = mfma16x16x32<C::MBF16>(a, st.qr[nt][ks], sp);
             }
@@ -1506,7 +1522,7 @@ constexpr uint32_t kOversub2 = LIA_WG_OVERSUB2;
 // 16-bit pools; FP8 pools run 2-wave workgroups, so six of them).
 constexpr uint32_t kMaxWavesPerCU = 12;
 
-static uint32_t decode_waves(uint32_t d, int kv) { return kv == LIA_FP8_E4M3 ? d / 64 : d / 32; }
+static uint32_t decode_waves(uint32_t d, int kv) { return kv == LIA_FP8_E4M3 ? d / 64 : d / LIA_SW16; }
 
 // Resident workgroups per CU allowed for a launch of NT column tiles.
 static uint32_t max_per_cu(uint32_t d, uint32_t nt, int kv) {

@@ -111,6 +111,16 @@ def test_config4_mtp_full_size(lia, wl):
     _check(G.Case(b, seed=0), lia, "cfg4")
 
 
+def test_config5_fp8_long_contexts(lia, wl):
+    """The FP8 decode workload of BASELINE config 5 on its first 8 sequences (contexts from
+    its log-uniform [1k, 128k] draw; the full 64-sequence pool takes a minute to build on the
+    host): e4m3 pages with per-page scales, long contexts split over many workgroups."""
+    full = wl.config5(seed=0)
+    ctx = [int(c) for c in full.ctx[:8]]
+    b = wl.custom(ctx, [1] * len(ctx), geom=wl.Geometry(kv_dtype=FP8), seed=11)
+    _check(G.Case(b, seed=11), lia, f"cfg5 first 8 (sum ctx {sum(ctx)})")
+
+
 def test_repeat_calls_are_identical(lia, wl):
     b = wl.custom([5000, 17, 900], [1, 1, 3], seed=8)
     case = G.Case(b, seed=8)
