@@ -82,8 +82,11 @@ def load_traffic(path, kernel_us, layer_bytes):
 
 def side_config(args):
     """One layer of BASELINE config 3 (mixed prefill + decode, MFMA-bound), 4 (MTP verify) or
-    5 (FP8 decode) on resident synthetic data: the plan once, then split attention + combine
-    replayed from a graph.  Prints a JSON line with the layer time and its roofline."""
+    5 (FP8 decode) on resident synthetic data, timed as a step of its own: device packing,
+    the plan, the KV append of the step's rows (fused into the attention launch on 16-bit
+    pools, the separate quantising append on FP8 pools), split attention and the combine,
+    replayed from a graph.  Prints a JSON line with the step time and the roofline of the
+    layer's algorithmic work."""
     import torch
     from __graft_entry__ import package
     lia = package()
@@ -96,36 +99,57 @@ def side_config(args):
     gen = torch.Generator(device=dev)
     gen.manual_seed(args.seed)
     fp8 = g.kv_dtype == lia.FP8
+    rows = b.n_rows
     if fp8:
         kp = torch.randint(0, 120, (tokens, g.hkv, g.d), generator=gen, dtype=torch.uint8, device=dev)
         vp = torch.randint(0, 120, (tokens, g.hkv, g.d), generator=gen, dtype=torch.uint8, device=dev)
         ks = torch.full((b.pool_pages * g.hkv,), 0.01, device=dev)
         vs = ks.clone()
+        newk = torch.randn((rows, g.hkv * g.d), generator=gen, device=dev).to(torch.bfloat16)
+        newv = torch.randn((rows, g.hkv * g.d), generator=gen, device=dev).to(torch.bfloat16)
+        layout = lia.KVLayout(g.hkv, g.d, P, b.pool_pages, g.kv_dtype)
     else:
         kp = torch.randn((tokens, g.hkv, g.d), generator=gen, device=dev).to(torch.bfloat16)
         vp = torch.randn((tokens, g.hkv, g.d), generator=gen, device=dev).to(torch.bfloat16)
         ks = vs = None
-    q = torch.randn((b.n_rows, g.hq, g.d), generator=gen, device=dev).to(torch.bfloat16)
-    out = torch.empty((b.n_rows, g.hq, g.d), dtype=torch.bfloat16, device=dev)
+        newk = torch.randn((rows, g.hkv * g.d), generator=gen, device=dev).to(torch.bfloat16)
+        newv = torch.randn((rows, g.hkv * g.d), generator=gen, device=dev).to(torch.bfloat16)
+    q = torch.randn((rows, g.hq, g.d), generator=gen, device=dev).to(torch.bfloat16)
+    out = torch.empty((rows, g.hq, g.d), dtype=torch.bfloat16, device=dev)
     i32 = lambda a: torch.from_numpy(np.asarray(a, np.uint32).view(np.int32)).to(dev)
-    cu, pos, seq, flat = i32(b.cu_seqlens()), i32(b.positions()), i32(b.sequences()), i32(b.flat_table())
+    seq_slots, q_lens, cached = i32(np.arange(b.n_seqs)), i32(b.q_len), i32(b.cached)
+    flat = i32(b.flat_table())
+    cu = torch.zeros(b.n_seqs + 1, dtype=torch.int32, device=dev)
+    positions = torch.zeros(rows, dtype=torch.int32, device=dev)
+    sequences = torch.zeros(rows, dtype=torch.int32, device=dev)
+    slots = torch.zeros(rows, dtype=torch.int32, device=dev)
+    status = torch.zeros(1, dtype=torch.int32, device=dev)
     cfg = lia.AttentionConfig(g.hq, g.hkv, g.d, P, b.pool_pages, b.stride, g.q_dtype, g.kv_dtype,
-                              g.out_dtype, g.scale, b.n_seqs, b.n_rows, int(b.ctx.max()))
+                              g.out_dtype, g.scale, b.n_seqs, rows, int(b.ctx.max()))
     ws = torch.zeros(lia.workspace_bytes(cfg), dtype=torch.uint8, device=dev)
-    lia.attention_plan(cfg, b.n_seqs, b.n_rows, cu, pos, seq, ws, pages=flat)
+    context = b.stride * P
     reps = max(args.kernel_reps, 1)
 
-    def layer():
-        lia.attention_partial(cfg, b.n_seqs, flat, q, kp, vp, out, ws, k_scales=ks, v_scales=vs)
-        lia.attention_merge(cfg, b.n_seqs, b.n_rows, out, ws)
+    def step():
+        lia.pack_device(seq_slots, q_lens, cached, flat, b.stride, P, b.pool_pages, context, rows,
+                        cu, positions, sequences, slots, status)
+        lia.attention_plan(cfg, b.n_seqs, rows, cu, positions, sequences, ws, pages=flat)
+        if fp8:
+            lia.kv_append(layout, newk, newv, kp, vp, slot_mapping=slots, k_scales=ks, v_scales=vs)
+            lia.attention_partial(cfg, b.n_seqs, flat, q, kp, vp, out, ws, k_scales=ks, v_scales=vs)
+        else:
+            lia.attention_partial_append(cfg, b.n_seqs, flat, slots, q, newk, newv, kp, vp, out, ws)
+        lia.attention_merge(cfg, b.n_seqs, rows, out, ws)
 
-    layer()
+    step()
     torch.cuda.synchronize()
+    if status.item() != 0:
+        raise RuntimeError(f"device packing failed: status {status.item()}")
     graph, stream = torch.cuda.CUDAGraph(), torch.cuda.Stream()
     with torch.cuda.stream(stream):
         with torch.cuda.graph(graph, stream=stream):
             for _ in range(reps):
-                layer()
+                step()
     for _ in range(max(args.warmup, 1)):
         graph.replay()
     torch.cuda.synchronize()
@@ -137,17 +161,19 @@ def side_config(args):
     e1.record(cur)
     torch.cuda.synchronize()
     us = e0.elapsed_time(e1) * 1e3 / (args.steps * reps)
-    nbytes, flops = b.algorithmic_bytes(), b.flops()
+    # the appended rows: read from the step's rows (bf16) and written to the pool
+    append_bytes = rows * g.hkv * g.d * 2 * (2 + (1 if fp8 else 2))
+    nbytes, flops = b.algorithmic_bytes() + append_bytes, b.flops()
     gbps, tflops = nbytes / (us * 1e-6) / 1e9, flops / (us * 1e-6) / 1e12
     mfma = args.config == 3
-    names = {3: "mixed chunked-prefill + decode attention", 4: "MTP-verify attention",
-             5: "FP8-KV decode attention"}
+    names = {3: "mixed chunked-prefill + decode attention step", 4: "MTP-verify attention step",
+             5: "FP8-KV decode attention step"}
     print(json.dumps({
-        "metric": f"{names[args.config]} us per layer (split attention + combine)",
+        "metric": f"{names[args.config]}, us per layer (pack + plan + append + split attention + combine)",
         "value": round(us, 3), "unit": "us", "higher_is_better": False, "n_gpus": 1,
         "steps": args.steps, "warmup": args.warmup, "dtype": "fp8-e4m3 KV, bf16 Q" if fp8 else "bf16",
         "data": "synthetic (seeded, resident in HBM)",
-        "config": {"workload": f"BASELINE config {args.config}", "rows": b.n_rows,
+        "config": {"workload": f"BASELINE config {args.config}", "rows": rows,
                    "sequences": b.n_seqs, "sum_ctx": int(b.ctx.sum())},
         "roofline": {"bound": "mfma" if mfma else "hbm",
                      "achieved": round(tflops if mfma else gbps, 1),

@@ -114,6 +114,197 @@ __device__ __forceinline__ uint32_t unit_blocks(uint32_t p0, uint32_t new_keys) 
     return (p0 + 31) / 32 + (new_keys + 31) / 32;
 }
 
+// sum_{i=0}^{n-1} floor((a*i + b) / m) (the standard floor-sum reduction, O(log) steps),
+// for the plan's small operands: 32-bit divisions, 64-bit sum.
+__device__ __forceinline__ uint64_t floor_sum(uint32_t n, uint32_t m, uint32_t a, uint32_t b) {
+    uint64_t ans = 0;
+    while (true) {
+        if (a >= m) {
+            ans += (uint64_t)n * (n - 1) / 2 * (a / m);
+            a %= m;
+        }
+        if (b >= m) {
+            ans += (uint64_t)n * (b / m);
+            b %= m;
+        }
+        const uint32_t y = a * n + b;
+        if (y < m) break;
+        n = y / m;
+        b = y % m;
+        const uint32_t tmp = m;
+        m = a;
+        a = tmp;
+    }
+    return ans;
+}
+
+// New-key blocks of column blocks 0 .. m-1 of a sequence in one KV head: sum over c = 1..m
+// of ceil(c * rpc / 32) (column block c-1 ends at row c * rpc, before the last block).
+// Power-of-two rpc (every batch shape the launches choose) in closed form with k = 32/rpc:
+// k*q*(q+1)/2 + r*(q+1), q = m / k, r = m % k.
+__device__ __forceinline__ uint32_t new_blocks_before(uint32_t m, uint32_t rpc) {
+    if (!m) return 0;
+    if ((rpc & (rpc - 1)) == 0) {
+        if (rpc >= 32) return (rpc >> 5) * (m * (m + 1) / 2);
+        const uint32_t lk = 5 - (31 - __builtin_clz(rpc)), k = 1u << lk; // k = 32 / rpc
+        const uint32_t q = m >> lk, r = m & (k - 1);
+        return k * q * (q + 1) / 2 + r * (q + 1);
+    }
+    return (uint32_t)floor_sum(m, 32, rpc, rpc + 31);
+}
+
+constexpr uint32_t kPlanSeqs = 1024; // sequences the plan keeps in LDS
+
+// The plan for up to kPlanSeqs sequences: per-sequence extents in LDS and every unit in
+// closed form (unit (h, cb) of sequence b starts at block b0 + h*nbh + cb*cblocks +
+// new_blocks_before(cb)), so units, merge descriptors and the work list are each written
+// in parallel with no serial per-sequence loop and no reads of the units just written.
+__device__ void plan_lds(uint32_t n_seqs, const uint32_t *cu, const uint32_t *positions,
+                         const uint32_t *sequences, const uint32_t *pages, uint32_t stride,
+                         uint32_t page_shift, uint32_t rpc, uint32_t hkv, uint32_t max_units,
+                         uint32_t n_wg, UnitDesc *units, WorkDesc *work, MergeDesc *merge,
+                         uint32_t *header) {
+    __shared__ uint32_t s_r0[kPlanSeqs], s_nr[kPlanSeqs], s_p0[kPlanSeqs], s_trow[kPlanSeqs];
+    __shared__ uint32_t s_u0[kPlanSeqs + 1], s_b0[kPlanSeqs + 1];
+    __shared__ uint32_t s_units[256], s_blocks[256];
+    __shared__ uint32_t carry_units, carry_blocks;
+    const uint32_t t = threadIdx.x;
+    if (t == 0) { carry_units = 0; carry_blocks = 0; }
+    __syncthreads();
+    for (uint32_t base = 0; base < n_seqs; base += 256) {
+        const uint32_t b = base + t;
+        uint32_t nu = 0, nb = 0, r0 = 0, nr = 0, p0 = 0, trow = 0;
+        if (b < n_seqs) {
+            r0 = cu[b];
+            nr = cu[b + 1] - r0;
+            if (nr > 0) {
+                p0 = positions[r0];
+                trow = sequences[r0];
+                const uint32_t ncb = (nr + rpc - 1) / rpc;
+                nu = ncb * hkv;
+                nb = (ncb * ((p0 + 31) / 32) + new_blocks_before(ncb - 1, rpc) + (nr + 31) / 32) * hkv;
+            }
+            s_r0[b] = r0; s_nr[b] = nr; s_p0[b] = p0; s_trow[b] = trow;
+        }
+        s_units[t] = nu;
+        s_blocks[t] = nb;
+        __syncthreads();
+        for (uint32_t off = 1; off < 256; off <<= 1) { // inclusive Hillis-Steele scan
+            uint32_t a = t >= off ? s_units[t - off] : 0, c = t >= off ? s_blocks[t - off] : 0;
+            __syncthreads();
+            s_units[t] += a;
+            s_blocks[t] += c;
+            __syncthreads();
+        }
+        if (b < n_seqs) {
+            s_u0[b] = carry_units + s_units[t] - nu;
+            s_b0[b] = carry_blocks + s_blocks[t] - nb;
+        }
+        __syncthreads();
+        if (t == 255) { carry_units += s_units[255]; carry_blocks += s_blocks[255]; }
+        __syncthreads();
+    }
+    const bool overflow = carry_units > max_units;
+    const uint32_t U = overflow ? 0 : carry_units, B = overflow ? 0 : carry_blocks;
+    const uint32_t N = min(n_wg, B);
+    if (t == 0) {
+        s_u0[n_seqs] = carry_units;
+        s_b0[n_seqs] = carry_blocks;
+        units[U] = UnitDesc{B, 0, 0, 0, 0, 0, 0, 0};
+        header[0] = U;
+        header[1] = B;
+        header[2] = N;
+        header[3] = overflow;
+    }
+    __syncthreads();
+    // last sequence b with arr[b] <= v (empty sequences share their offset with the next
+    // one, so this is the sequence that owns v)
+    auto seq_of = [&](const uint32_t *arr, uint32_t v) {
+        uint32_t a = 0, e = n_seqs;
+        while (a + 1 < e) {
+            const uint32_t mid = (a + e) >> 1;
+            if (arr[mid] <= v) a = mid; else e = mid;
+        }
+        return a;
+    };
+    auto make_unit = [&](uint32_t b, uint32_t h, uint32_t cb) {
+        const uint32_t nr = s_nr[b], p0 = s_p0[b], cblocks = (p0 + 31) / 32;
+        const uint32_t nbh = (s_b0[b + 1] - s_b0[b]) / hkv;
+        const uint32_t rows = min(rpc, nr - cb * rpc), kend = p0 + cb * rpc + rows;
+        const uint32_t blk = s_b0[b] + h * nbh + cb * cblocks + new_blocks_before(cb, rpc);
+        return UnitDesc{blk, unit_blocks(p0, kend - p0), cblocks, s_r0[b] + cb * rpc, rows | (h << 16),
+                        kend, s_trow[b], p0};
+    };
+    auto unit_by_index = [&](uint32_t u) {
+        const uint32_t b = seq_of(s_u0, u), ncb = (s_nr[b] + rpc - 1) / rpc, i = u - s_u0[b];
+        return make_unit(b, i / ncb, i % ncb);
+    };
+    for (uint32_t u = t; u < U; u += 256) units[u] = unit_by_index(u);
+    const uint32_t P = 1u << page_shift;
+    for (uint32_t w = N + t; w < n_wg; w += 256) { // launched workgroups without work
+        WorkDesc d = {};
+        work[w] = d;
+    }
+    for (uint32_t u = t; u < max_units; u += 256) {
+        MergeDesc m = {0, 0, 0, 0};
+        if (u < U) {
+            const UnitDesc ud = unit_by_index(u);
+            const uint32_t wf = (uint32_t)((((uint64_t)ud.block_start + 1) * N - 1) / B);
+            const uint32_t wl = (uint32_t)((((uint64_t)ud.block_start + ud.nblocks) * N - 1) / B);
+            if (wf != wl) m = MergeDesc{wf + u, wl - wf + 1, ud.rowbeg, ud.nrows_hk};
+        }
+        merge[u] = m;
+    }
+    auto range_lo = [&](uint32_t w) { return (uint32_t)((uint64_t)w * B / N); };
+    const bool xcd_major = kXcdMajor && N == n_wg && N % 8 == 0;
+    const uint32_t per = N / 8;
+    // Work descriptors four at a time, so the page-table reads of all four are in flight
+    // together (unconditional loads: an entry not needed reads cu[0] and is replaced by 0).
+    for (uint32_t w0 = t; w0 < N; w0 += 4 * 256) {
+        WorkDesc d[4];
+        uint32_t v[4][kPrePages];
+#pragma unroll
+        for (int k = 0; k < 4; k++) {
+            const uint32_t w = min(w0 + k * 256, N - 1); // past N: a copy of the last, not stored
+            const uint32_t r = xcd_major ? (w % 8) * per + w / 8 : w;
+            const uint32_t lo = range_lo(r), hi = range_lo(r + 1);
+            // the unit holding block lo: its sequence, KV head, then column block
+            const uint32_t b = seq_of(s_b0, lo);
+            const uint32_t ncb = (s_nr[b] + rpc - 1) / rpc, cblocks = (s_p0[b] + 31) / 32;
+            const uint32_t nbh = (s_b0[b + 1] - s_b0[b]) / hkv, off = lo - s_b0[b];
+            const uint32_t h = off / nbh, rem = off - h * nbh;
+            uint32_t c = 0, e = ncb; // last cb whose first block <= rem
+            while (c + 1 < e) {
+                const uint32_t mid = (c + e) >> 1;
+                if (mid * cblocks + new_blocks_before(mid, rpc) <= rem) c = mid; else e = mid;
+            }
+            d[k].unit = s_u0[b] + h * ncb + c;
+            d[k].first = make_unit(b, h, c);
+            d[k].flags = r << 8;
+            d[k].lo = lo;
+            d[k].hi = hi;
+            // logical pages the range starts with, when it starts in the cached keys
+            const uint32_t rel = lo - d[k].first.block_start;
+            const bool pre = pages && rel < d[k].first.cblocks;
+            const uint32_t lp = (32 * rel) >> page_shift;
+            const uint32_t lend = (d[k].first.kend + P - 1) >> page_shift;
+#pragma unroll
+            for (uint32_t i = 0; i < kPrePages; i++) {
+                const bool use = pre && lp + i < lend;
+                const uint32_t *src = use ? pages + (size_t)d[k].first.table_row * stride + lp + i : cu;
+                v[k][i] = *src;
+                v[k][i] = use ? v[k][i] : 0u;
+            }
+            if (pre) d[k].flags |= 1;
+        }
+#pragma unroll
+        for (int k = 0; k < 4; k++) {
+            d[k].pre = make_uint4(v[k][0], v[k][1], v[k][2], v[k][3]);
+            if (w0 + k * 256 < N) work[w0 + k * 256] = d[k];
+        }
+    }
+}
+
 __global__ __launch_bounds__(256) void plan_kernel(uint32_t n_seqs, const uint32_t *cu,
                                                    const uint32_t *positions,
                                                    const uint32_t *sequences, const uint32_t *pages,
@@ -121,6 +312,11 @@ __global__ __launch_bounds__(256) void plan_kernel(uint32_t n_seqs, const uint32
                                                    uint32_t hkv, uint32_t max_units,
                                                    uint32_t n_wg, UnitDesc *units, WorkDesc *work,
                                                    MergeDesc *merge, uint32_t *header) {
+    if (n_seqs <= kPlanSeqs) {
+        plan_lds(n_seqs, cu, positions, sequences, pages, stride, page_shift, rpc, hkv, max_units, n_wg,
+                 units, work, merge, header);
+        return;
+    }
     __shared__ uint32_t s_units[256], s_blocks[256];
     __shared__ uint32_t carry_units, carry_blocks, overflow;
     const uint32_t t = threadIdx.x;

@@ -15,15 +15,21 @@ __global__ __launch_bounds__(1024) void pack_kernel(uint32_t n_seqs, const uint3
                                                     uint32_t *cu, uint32_t *positions,
                                                     uint32_t *sequences, uint32_t *slot_mapping,
                                                     uint32_t *status) {
-    __shared__ uint32_t scan[1024];
+    __shared__ uint32_t scan[1024], s_slot[1024], s_c0[1024];
+    // error: (row << 4) | code of the failing row with the lowest index, so the status is the
+    // first failure in row order whatever the thread timing (codes are below 16)
     __shared__ uint32_t carry, error;
     const uint32_t t = threadIdx.x;
-    if (t == 0) { carry = 0; error = 0; }
+    if (t == 0) { carry = 0; error = 0xFFFFFFFFu; }
     __syncthreads();
     const uint32_t P = 1u << page_shift;
     for (uint32_t base = 0; base < n_seqs; base += 1024) {
         uint32_t b = base + t;
         uint32_t n = b < n_seqs ? q_lens[b] : 0;
+        if (n_seqs <= 1024) { // kept for the rows below
+            s_slot[t] = b < n_seqs ? seq_slots[b] : 0u;
+            s_c0[t] = b < n_seqs ? cached[b] : 0u;
+        }
         scan[t] = n;
         __syncthreads();
         for (uint32_t off = 1; off < 1024; off <<= 1) {
@@ -46,27 +52,46 @@ __global__ __launch_bounds__(1024) void pack_kernel(uint32_t n_seqs, const uint3
         if (t == 0) *status = (uint32_t)(-LIA_E_ROWS);
         return;
     }
-    // Rows: walk sequences, threads stride over each sequence's rows.
-    for (uint32_t b = 0; b < n_seqs; b++) {
-        uint32_t start = cu[b], n = q_lens[b], slot = seq_slots[b], c0 = cached[b];
-        for (uint32_t i = t; i < n; i += 1024) {
-            uint32_t pos = c0 + i;
-            uint32_t r = start + i;
-            uint32_t s = kNone;
-            if (pos >= context) {
-                atomicCAS(&error, 0u, (uint32_t)(-LIA_E_POSITION));
-            } else {
-                uint32_t page = pages[(size_t)slot * stride + (pos >> page_shift)];
-                if (page >= pool_pages) atomicCAS(&error, 0u, (uint32_t)(-LIA_E_MISSING_PAGE));
-                else s = page * P + (pos & (P - 1));
-            }
-            positions[r] = pos;
-            sequences[r] = slot;
-            slot_mapping[r] = s;
+    auto fill = [&](uint32_t r, uint32_t i, uint32_t slot, uint32_t c0) {
+        const uint32_t pos = c0 + i;
+        uint32_t s = kNone;
+        if (pos >= context) {
+            atomicMin(&error, (r << 4) | (uint32_t)(-LIA_E_POSITION));
+        } else {
+            uint32_t page = pages[(size_t)slot * stride + (pos >> page_shift)];
+            if (page >= pool_pages) atomicMin(&error, (r << 4) | (uint32_t)(-LIA_E_MISSING_PAGE));
+            else s = page * P + (pos & (P - 1));
         }
+        positions[r] = pos;
+        sequences[r] = slot;
+        slot_mapping[r] = s;
+    };
+    auto report = [&] {
+        __syncthreads();
+        if (t == 0) *status = error == 0xFFFFFFFFu ? 0u : (error & 15u);
+    };
+    if (n_seqs <= 1024) {
+        // Rows in parallel: row r belongs to the first sequence whose inclusive prefix sum
+        // (scan, still in LDS) exceeds r.
+        for (uint32_t r = t; r < total; r += 1024) {
+            uint32_t a = 0, e = n_seqs; // smallest b with scan[b] > r
+            while (a < e) {
+                const uint32_t mid = (a + e) >> 1;
+                if (scan[mid] > r) e = mid; else a = mid + 1;
+            }
+            const uint32_t start = a ? scan[a - 1] : 0u;
+            fill(r, r - start, s_slot[a], s_c0[a]);
+        }
+        report();
+        return;
     }
-    __syncthreads();
-    if (t == 0) *status = error;
+    // More sequences than the LDS copies hold: walk sequences, threads stride over each
+    // sequence's rows.
+    for (uint32_t b = 0; b < n_seqs; b++) {
+        const uint32_t start = cu[b], n = q_lens[b], slot = seq_slots[b], c0 = cached[b];
+        for (uint32_t i = t; i < n; i += 1024) fill(start + i, i, slot, c0);
+    }
+    report();
 }
 
 template <typename SRC>

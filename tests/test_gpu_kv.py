@@ -126,6 +126,21 @@ def test_pack_device_reports_missing_page(lia):
     assert status.item() == 10  # -LIA_E_MISSING_PAGE
 
 
+@pytest.mark.parametrize("order,expect", [((0, 1), 10), ((1, 0), 8)])
+def test_pack_device_reports_first_failing_row(lia, order, expect):
+    """Two failing sequences: the status is the error of the earlier row in packed order
+    (sequence A: its second row needs a missing page; sequence B: position 40 >= context)."""
+    pages = G.u32_dev(np.array([3, 0xFFFFFFFF, 4, 5], np.uint32))  # stride 2: rows 0 and 1
+    seqs = {0: (0, 2, 15), 1: (1, 1, 40)}  # (table row, q_len, cached)
+    slot, q_len, cached = zip(*[seqs[i] for i in order])
+    out = [torch.zeros(8, dtype=torch.int32, device="cuda") for _ in range(4)]
+    status = torch.zeros(1, dtype=torch.int32, device="cuda")
+    lia.pack_device(G.u32_dev(slot), G.u32_dev(q_len), G.u32_dev(cached), pages, 2, 16, 8, 32, 8,
+                    out[0], out[1], out[2], out[3], status)
+    torch.cuda.synchronize()
+    assert status.item() == expect  # 10: -LIA_E_MISSING_PAGE, 8: -LIA_E_POSITION
+
+
 def test_kv_quantize_pages_bit_exact(O, lia):
     rng = np.random.default_rng(12)
     H, D, P, pool = 2, 128, 16, 40
