@@ -1445,10 +1445,16 @@ __global__ __launch_bounds__(64 * LIA_WIDE_WAVES, LIA_WIDE_NTW == 2 ? 2 : 4) voi
                     }
                 }
             } else {
+                // split record: O normalised by its own mass, in f16 (|O/l| <= max |V|, relative
+                // error 2^-11; half the record traffic of f32), with the mass and maximum in f32
                 const size_t rb = (size_t)rec * COLS + col;
-                float *po = p.part_o + rb * D + 4 * g;
+                uint16_t *po = (uint16_t *)p.part_o + rb * D + 4 * g;
+                const float inv = lt > 0.0f ? 1.0f / lt : 0.0f;
 #pragma unroll
-                for (int n = 0; n < W::DT; n++) *(f32x4 *)(po + 16 * n) = st.o[nt][n];
+                for (int n = 0; n < W::DT; n++) {
+                    const f32x4 v = st.o[nt][n] * inv;
+                    *(u32x2 *)(po + 16 * n) = u32x2{pack2<false>(v.x, v.y), pack2<false>(v.z, v.w)};
+                }
                 if (g == 0) {
                     p.part_ml[rb * 2] = st.m[nt];
                     p.part_ml[rb * 2 + 1] = lt;
@@ -1571,69 +1577,101 @@ __global__ __launch_bounds__(kCombineThreads) void combine_kernel(AttnParams p) 
 // (2-3 records each): one wave per column, four columns per workgroup.  Lanes hold a
 // record's row as float4 quads (64 / (D/4) records per pass); the record groups are summed
 // with lane shuffles.  Same merge rule as combine_kernel.
+// Columns merged by one wave of combine_wide_kernel, and record passes loaded per batch.
+#ifndef LIA_WCC
+#define LIA_WCC 4
+#endif
+constexpr uint32_t kWideCombineCols = LIA_WCC;
+constexpr uint32_t kWideCombinePasses = 2;
+
 template <int D>
 __global__ __launch_bounds__(256) void combine_wide_kernel(AttnParams p) {
     constexpr uint32_t Q = D / 4, RPP = 64 / Q, COLS = 16 * kWideNTDev;
+    constexpr uint32_t CW = kWideCombineCols, KP = kWideCombinePasses;
     const uint32_t u = blockIdx.x, lane = threadIdx.x & 63;
-    const uint32_t col = blockIdx.y * 4 + (uint32_t)__builtin_amdgcn_readfirstlane((int)(threadIdx.x >> 6));
+    const uint32_t wave = (uint32_t)__builtin_amdgcn_readfirstlane((int)(threadIdx.x >> 6));
+    const uint32_t col0 = (blockIdx.y * 4 + wave) * CW; // this wave's first column
     const MergeDesc md = p.merge[u];
-    if (md.n == 0 || col >= (md.nrows_hk & 0xffffu) * p.group) return;
+    const uint32_t ncols = (md.nrows_hk & 0xffffu) * p.group;
+    if (md.n == 0 || col0 >= ncols) return;
     const uint32_t n = md.n, rec0 = md.rec0, q = lane % Q, rg = lane / Q;
-    const float4 *po = (const float4 *)p.part_o;
-    float M = -INFINITY, den = 0.0f;
-    float4 num = make_float4(0.0f, 0.0f, 0.0f, 0.0f);
-    for (uint32_t base = 0; base < n; base += RPP * kCombinePasses) {
-        float4 o[kCombinePasses];
-        float m[kCombinePasses], l[kCombinePasses];
+    // records hold O / l in f16 (four values per quad), so a record weighs w * l
+    const u32x2 *po = (const u32x2 *)p.part_o;
+    float M[CW], den[CW];
+    float4 num[CW];
 #pragma unroll
-        for (uint32_t k = 0; k < kCombinePasses; k++) {
-            const uint32_t r = base + k * RPP + rg;
-            const size_t rb = (size_t)(rec0 + min(r, n - 1)) * COLS + col;
-            o[k] = po[rb * Q + q];
-            const float2 ml = ((const float2 *)p.part_ml)[rb];
-            m[k] = ml.x;
-            l[k] = r < n ? ml.y : 0.0f;
-        }
-        float bm = -INFINITY;
+    for (uint32_t c = 0; c < CW; c++) {
+        M[c] = -INFINITY;
+        den[c] = 0.0f;
+        num[c] = make_float4(0.0f, 0.0f, 0.0f, 0.0f);
+    }
+    for (uint32_t base = 0; base < n; base += RPP * KP) {
+        // every load of the batch (all CW columns) before any use: unconditional, records
+        // past n clamped to the last and weighted zero, columns past the unit's to its last
+        float4 o[CW][KP];
+        float m[CW][KP], l[CW][KP];
 #pragma unroll
-        for (uint32_t k = 0; k < kCombinePasses; k++)
-            if (l[k] > 0.0f) bm = fmaxf(bm, m[k]);
-        bm = wave_max(bm);
-        const float nm = fmaxf(M, bm);
-        if (nm != M) {
-            const float f = M == -INFINITY ? 0.0f : fast_exp2(M - nm);
-            num.x *= f; num.y *= f; num.z *= f; num.w *= f;
-            den *= f;
-            M = nm;
-        }
+        for (uint32_t c = 0; c < CW; c++)
 #pragma unroll
-        for (uint32_t k = 0; k < kCombinePasses; k++) {
-            const float w = l[k] > 0.0f ? fast_exp2(m[k] - M) : 0.0f;
-            num.x = fmaf(w, o[k].x, num.x);
-            num.y = fmaf(w, o[k].y, num.y);
-            num.z = fmaf(w, o[k].z, num.z);
-            num.w = fmaf(w, o[k].w, num.w);
-            den = fmaf(w, l[k], den);
+            for (uint32_t k = 0; k < KP; k++) {
+                const uint32_t r = base + k * RPP + rg;
+                const size_t rb = (size_t)(rec0 + min(r, n - 1)) * COLS + min(col0 + c, ncols - 1);
+                const u32x2 h = po[rb * Q + q];
+                o[c][k] = make_float4(f16_to_f32(h.x & 0xffffu), f16_to_f32(h.x >> 16),
+                                      f16_to_f32(h.y & 0xffffu), f16_to_f32(h.y >> 16));
+                const float2 ml = ((const float2 *)p.part_ml)[rb];
+                m[c][k] = ml.x;
+                l[c][k] = r < n ? ml.y : 0.0f;
+            }
+#pragma unroll
+        for (uint32_t c = 0; c < CW; c++) {
+            float bm = -INFINITY;
+#pragma unroll
+            for (uint32_t k = 0; k < KP; k++)
+                if (l[c][k] > 0.0f) bm = fmaxf(bm, m[c][k]);
+            bm = wave_max(bm);
+            const float nm = fmaxf(M[c], bm);
+            if (nm != M[c]) {
+                const float f = M[c] == -INFINITY ? 0.0f : fast_exp2(M[c] - nm);
+                num[c].x *= f; num[c].y *= f; num[c].z *= f; num[c].w *= f;
+                den[c] *= f;
+                M[c] = nm;
+            }
+#pragma unroll
+            for (uint32_t k = 0; k < KP; k++) {
+                const float w = l[c][k] > 0.0f ? fast_exp2(m[c][k] - M[c]) * l[c][k] : 0.0f;
+                num[c].x = fmaf(w, o[c][k].x, num[c].x);
+                num[c].y = fmaf(w, o[c][k].y, num[c].y);
+                num[c].z = fmaf(w, o[c][k].z, num[c].z);
+                num[c].w = fmaf(w, o[c][k].w, num[c].w);
+                den[c] += w;
+            }
         }
     }
 #pragma unroll
-    for (uint32_t off = Q; off < 64; off <<= 1) {
-        num.x += shfl_xor(num.x, off);
-        num.y += shfl_xor(num.y, off);
-        num.z += shfl_xor(num.z, off);
-        num.w += shfl_xor(num.w, off);
-        den += shfl_xor(den, off);
-    }
-    if (rg != 0) return;
-    const float inv = den > 0.0f ? 1.0f / den : 0.0f;
-    const uint32_t row = md.rowbeg + col / p.group, head = (md.nrows_hk >> 16) * p.group + col % p.group;
-    const size_t at = ((size_t)row * p.hq + head) * D + 4 * q;
-    if (p.out_f32) {
-        *(float4 *)((float *)p.out + at) = make_float4(num.x * inv, num.y * inv, num.z * inv, num.w * inv);
-    } else {
-        *(u32x2 *)((uint16_t *)p.out + at) =
-            u32x2{(uint32_t)f32_to_bf16(num.x * inv) | ((uint32_t)f32_to_bf16(num.y * inv) << 16),
-                  (uint32_t)f32_to_bf16(num.z * inv) | ((uint32_t)f32_to_bf16(num.w * inv) << 16)};
+    for (uint32_t c = 0; c < CW; c++) {
+        const uint32_t col = col0 + c;
+        float4 x = num[c];
+        float dn = den[c];
+#pragma unroll
+        for (uint32_t off = Q; off < 64; off <<= 1) {
+            x.x += shfl_xor(x.x, off);
+            x.y += shfl_xor(x.y, off);
+            x.z += shfl_xor(x.z, off);
+            x.w += shfl_xor(x.w, off);
+            dn += shfl_xor(dn, off);
+        }
+        if (rg != 0 || col >= ncols) continue;
+        const float inv = dn > 0.0f ? 1.0f / dn : 0.0f;
+        const uint32_t row = md.rowbeg + col / p.group, head = (md.nrows_hk >> 16) * p.group + col % p.group;
+        const size_t at = ((size_t)row * p.hq + head) * D + 4 * q;
+        if (p.out_f32) {
+            *(float4 *)((float *)p.out + at) = make_float4(x.x * inv, x.y * inv, x.z * inv, x.w * inv);
+        } else {
+            *(u32x2 *)((uint16_t *)p.out + at) =
+                u32x2{(uint32_t)f32_to_bf16(x.x * inv) | ((uint32_t)f32_to_bf16(x.y * inv) << 16),
+                      (uint32_t)f32_to_bf16(x.z * inv) | ((uint32_t)f32_to_bf16(x.w * inv) << 16)};
+        }
     }
 }
 
@@ -1928,7 +1966,7 @@ static int run_stages(int stages, const lia_attention_config *c, uint32_t n_seqs
         }
         dim3 grid(units_nt < L.max_units ? units_nt : L.max_units, cols);
 #define LIA_COMBINE(DD, NN) hipLaunchKernelGGL((combine_kernel<DD, NN>), grid, dim3(kCombineThreads), 0, s, p)
-        const dim3 wgrid(grid.x, 16 * kWideNT / 4);
+        const dim3 wgrid(grid.x, 16 * kWideNT / (4 * kWideCombineCols));
         if (c->head_dim == 128) {
             if (NT == 1) LIA_COMBINE(128, 1);
             else if (NT == 2) LIA_COMBINE(128, 2);
