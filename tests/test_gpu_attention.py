@@ -100,6 +100,19 @@ def test_prefill_group_sizes(lia, wl, kv):
         _check(G.Case(b, seed=6), lia, f"groups hq={hq} hkv={hkv} kv={kv}")
 
 
+@pytest.mark.parametrize("hq,hkv", [(6, 2), (10, 2)])
+def test_odd_group_sizes(lia, wl, hq, hkv):
+    """GQA groups of 3 and 5: rows per column block (16 NT / group, 128 / group on the prefill
+    kernel) are not powers of two, so the plan's block offsets take the general floor-sum.
+    Decode rows, MTP-like rows and prefill chunks with prefixes."""
+    g = wl.Geometry(hq=hq, hkv=hkv, d=128)
+    for ctx, q, name in [([17, 300, 2049, 64], [1, 1, 1, 1], "decode"),
+                         ([40, 700, 1500], [3, 2, 4], "mtp"),
+                         ([300, 1077, 40, 513], [300, 77, 40, 33], "prefill")]:
+        b = wl.custom(ctx, q, geom=g, seed=13)
+        _check(G.Case(b, seed=13), lia, f"group {hq // hkv} {name}")
+
+
 def test_config2_full_size_one_layer(lia, wl):
     """North-star shape: batch 8, contexts U[1k, 32k], one layer against the oracle."""
     b = wl.config2(seed=0, layers=1)
