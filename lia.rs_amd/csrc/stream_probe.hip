@@ -6,6 +6,8 @@
 // register, so the time is the memory system's alone.  Four access patterns:
 //   contiguous  both planes read front to back (the pool's bytes, no paging): the practical
 //               read ceiling for a transfer of this size;
+//   contiguous_1gib  one launch reading 1 GiB front to back: the sustained rate, without the
+//               ramp and tail a launch of a few tens of microseconds pays;
 //   slices      the decode kernel's mapping: a 4-wave workgroup per block range of a
 //               (sequence, KV head) unit, wave w loading the 64-byte slice [64w, 64w+64) of
 //               each token's head row (one load = 16 tokens x 64 bytes);
@@ -218,6 +220,22 @@ int main(int argc, char **argv) {
         });
         printf("{\"pattern\": \"contiguous\", \"us\": %.3f, \"GBps\": %.1f, \"bytes\": %.0f, \"workgroups\": %u}\n",
                us, 2.0 * plane / us / 1e3, 2.0 * plane, wgs);
+    }
+    {
+        const size_t big = (size_t)1 << 30; // 512 MiB per plane
+        uint8_t *bk, *bv;
+        CHECK(hipMalloc(&bk, big / 2));
+        CHECK(hipMalloc(&bv, big / 2));
+        CHECK(hipMemset(bk, 0x11, big / 2));
+        CHECK(hipMemset(bv, 0x22, big / 2));
+        const uint32_t n16 = (uint32_t)(big / 2 / 16), wgs = 3 * cus;
+        const double us = timed([&](uint32_t) {
+            contiguous_read<<<wgs, 256>>>((const u32x4 *)bk, (const u32x4 *)bv, n16, sink);
+        });
+        printf("{\"pattern\": \"contiguous_1gib\", \"us\": %.3f, \"GBps\": %.1f, \"bytes\": %.0f, \"workgroups\": %u}\n",
+               us, (double)big / us / 1e3, (double)big, wgs);
+        CHECK(hipFree(bk));
+        CHECK(hipFree(bv));
     }
     // paged patterns: units' chunks laid end to end, cut into equal ranges (3 workgroups per
     // CU, as the decode kernel runs), split where a range crosses units
