@@ -446,8 +446,18 @@ __global__ __launch_bounds__(256) void plan_kernel(uint32_t n_seqs, const uint32
 // therefore split evenly whatever the segment lengths, and no end-of-segment merge is
 // needed: each wave writes its own slice of the output or of the split record.
 
+// Dims per wave of a 16-bit pool (64: a wave reads whole 128-byte lines of a token; 32
+// halves the lines).  Cache policy of the K/V loads per pool type: 2 (non-temporal) on
+// 16-bit pools, where each wave reads whole lines, 0 on FP8 pools, whose 64-byte slices
+// share a line between two waves.
 #ifndef LIA_SW16
-#define LIA_SW16 32
+#define LIA_SW16 64
+#endif
+#ifndef LIA_KV_AUX
+#define LIA_KV_AUX 2
+#endif
+#ifndef LIA_KV_AUX_FP8
+#define LIA_KV_AUX_FP8 0
 #endif
 
 template <int D, int KVT>
@@ -455,11 +465,12 @@ struct Cfg {
     static constexpr bool FP8 = KVT == LIA_FP8_E4M3;
     static constexpr bool MBF16 = KVT == LIA_BF16;  // MFMA operand type (f16 for f16 and FP8)
     static constexpr int EB = FP8 ? 1 : 2;          // bytes per stored KV element
-    // Each wave owns a head_dim slice of SW dims, 64 bytes of a token either way: 32 dims
-    // of a 16-bit pool, 64 dims of an FP8 pool.  A lane loads 16 contiguous bytes of a token
-    // per 16-token tile (its A-operand k slots for KS k-steps), so every load instruction
-    // reads 16 tokens x 64 bytes.
+    // Each wave owns a head_dim slice of SW dims: 64 dims of a 16-bit pool (128 bytes of a
+    // token, two loads per tile), 64 dims of an FP8 pool (64 bytes).  A lane loads 16
+    // contiguous bytes of a token per 16-token tile and load (its A-operand k slots), so
+    // every load instruction reads 16 tokens x 64 bytes.
     static constexpr int SW = FP8 ? 64 : LIA_SW16;
+    static constexpr int AUX = FP8 ? LIA_KV_AUX_FP8 : LIA_KV_AUX; // cache policy of the K/V loads
     static constexpr int WAVES = D / SW;            // one wave per slice
     static constexpr int KS = SW / 32;              // k-steps of S^T = K Q^T per tile
     static constexpr int DTW = SW / 16;             // 16-dim tiles of O per wave
@@ -617,7 +628,7 @@ __device__ __forceinline__ void load_chunk(const AttnParams &p, Chunk<D, KVT> &c
 #pragma unroll
         for (int q = 0; q < C::KL; q++) {
             const uint32_t off = (((t + 16 * j) & (P - 1)) + li) * row_bytes + slice_off + 64 * q + 16 * g;
-            u32x4 x = buffer_load16(r[j], off);
+            u32x4 x = buffer_load16_p<C::AUX>(r[j], off);
             c.k[j][4 * q] = x.x; c.k[j][4 * q + 1] = x.y; c.k[j][4 * q + 2] = x.z; c.k[j][4 * q + 3] = x.w;
         }
     }
@@ -630,7 +641,7 @@ __device__ __forceinline__ void load_chunk(const AttnParams &p, Chunk<D, KVT> &c
                 make_rsrc(vbase + (size_t)tp.page[j] * P * row_bytes, tp.live[j] * row_bytes);
             const uint32_t off = (((t + 16 * j) & (P - 1)) + (lane >> 2)) * row_bytes + slice_off +
                                  16 * (lane & 3);
-            c.v[j] = buffer_load16(vr, off);
+            c.v[j] = buffer_load16_p<C::AUX>(vr, off);
         }
     } else {
         // V slice goes straight to this wave's LDS stage: load s fills rows VRPI*s ..
@@ -644,8 +655,11 @@ __device__ __forceinline__ void load_chunk(const AttnParams &p, Chunk<D, KVT> &c
             const uint32_t row = C::VRPI * s + lane / C::CPR;
             const uint32_t chunk = (lane % C::CPR) ^ vswz<C::SW>(row);
             const uint32_t off = (((t + 16 * j) & (P - 1)) + (row & 15)) * row_bytes + slice_off + 16 * chunk;
-            __builtin_amdgcn_raw_ptr_buffer_load_lds(
-                vr, (__attribute__((address_space(3))) void *)(stage + s * 512), 16, off, 0, 0, 0);
+            auto *dst = (__attribute__((address_space(3))) void *)(stage + s * 512);
+            if constexpr (C::AUX == 2)
+                __builtin_amdgcn_raw_ptr_buffer_load_lds(vr, dst, 16, off, 0, 0, 2);
+            else
+                __builtin_amdgcn_raw_ptr_buffer_load_lds(vr, dst, 16, off, 0, 0, 0);
         }
     }
     __builtin_amdgcn_sched_barrier(0);
@@ -1752,15 +1766,24 @@ extern "C" uint32_t lia_device_cus(void) {
 #endif
 constexpr uint32_t kMaxPerCU = LIA_MAX_WG_PER_CU;
 constexpr uint32_t kOversub2 = LIA_WG_OVERSUB2;
-// Decode kernel: at most this many waves per CU (three 4-wave workgroups measured best on
-// 16-bit pools; FP8 pools run 2-wave workgroups, so six of them).
-constexpr uint32_t kMaxWavesPerCU = 12;
+// Decode kernel: at most this many waves per CU (three 2-wave workgroups measured best on
+// 16-bit pools at head_dim 128, four 2-wave workgroups on FP8 pools).  Fewer, longer
+// splits also shrink the combine.
+#ifndef LIA_MAX_WAVES
+#define LIA_MAX_WAVES 6
+#endif
+constexpr uint32_t kMaxWavesPerCU = LIA_MAX_WAVES;
+#ifndef LIA_MAX_WAVES_FP8
+#define LIA_MAX_WAVES_FP8 8
+#endif
+constexpr uint32_t kMaxWavesPerCU8 = LIA_MAX_WAVES_FP8;
+static uint32_t max_waves(int kv) { return kv == LIA_FP8_E4M3 ? kMaxWavesPerCU8 : kMaxWavesPerCU; }
 
 static uint32_t decode_waves(uint32_t d, int kv) { return kv == LIA_FP8_E4M3 ? d / 64 : d / LIA_SW16; }
 
 // Resident workgroups per CU allowed for a launch of NT column tiles.
 static uint32_t max_per_cu(uint32_t d, uint32_t nt, int kv) {
-    return nt == kWideNT ? kMaxPerCU : kMaxWavesPerCU / decode_waves(d, kv);
+    return nt == kWideNT ? kMaxPerCU : max_waves(kv) / decode_waves(d, kv);
 }
 
 // Upper bound on attention workgroups per launch of a configuration: sizes the plan and
@@ -1768,7 +1791,7 @@ static uint32_t max_per_cu(uint32_t d, uint32_t nt, int kv) {
 static uint32_t max_workgroups(const lia_attention_config *c) {
     uint32_t cus = lia_device_cus();
     if (!cus) cus = 256;
-    const uint32_t per = max(kMaxPerCU, kMaxWavesPerCU / decode_waves(c->head_dim, c->kv_dtype));
+    const uint32_t per = max(kMaxPerCU, max_waves(c->kv_dtype) / decode_waves(c->head_dim, c->kv_dtype));
     return cus * per * kOversub2 / 2;
 }
 

@@ -181,4 +181,10 @@ __device__ __forceinline__ u32x4 buffer_load16(__amdgpu_buffer_rsrc_t r, uint32_
     return __builtin_bit_cast(u32x4, __builtin_amdgcn_raw_buffer_load_b128(r, (int)voffset, 0, 0));
 }
 
+// Cache-policy operand of a buffer load: 0 (default) or 2 (nt, non-temporal: data read once).
+template <int AUX = 0>
+__device__ __forceinline__ u32x4 buffer_load16_p(__amdgpu_buffer_rsrc_t r, uint32_t voffset) {
+    return __builtin_bit_cast(u32x4, __builtin_amdgcn_raw_buffer_load_b128(r, (int)voffset, 0, AUX));
+}
+
 } // namespace lia

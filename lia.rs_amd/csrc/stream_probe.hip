@@ -26,6 +26,7 @@
 #include <cstdlib>
 #include <random>
 #include <vector>
+#include <type_traits>
 
 typedef uint32_t u32x4 __attribute__((ext_vector_type(4)));
 
@@ -38,10 +39,12 @@ typedef uint32_t u32x4 __attribute__((ext_vector_type(4)));
         }                                                                                \
     } while (0)
 
+// AUX: cache policy of the load (0 default, 2 non-temporal)
+template <int AUX = 0>
 __device__ __forceinline__ u32x4 load16(const void *base, uint32_t bytes, uint32_t off) {
     const __amdgpu_buffer_rsrc_t r =
         __builtin_amdgcn_make_buffer_rsrc(const_cast<void *>(base), 0, bytes, 0x00020000);
-    return __builtin_bit_cast(u32x4, __builtin_amdgcn_raw_buffer_load_b128(r, off, 0, 0));
+    return __builtin_bit_cast(u32x4, __builtin_amdgcn_raw_buffer_load_b128(r, off, 0, AUX));
 }
 
 struct Range {
@@ -62,7 +65,7 @@ enum { SLICES = 0, HEAD_ROWS = 1, TOKEN_ROWS = 2 };
 // One workgroup of 256 threads per range, the next chunk's loads issued before the current
 // chunk is folded.  NLP: loads per plane per wave and chunk (a 32-token chunk of S-byte
 // spans is 32*S/1024 loads per plane; slots past it are bounded to nothing).
-template <int MODE, int NLP>
+template <int MODE, int NLP, int AUX>
 __global__ __launch_bounds__(256) void paged_read(Pool p, const Range *ranges, uint32_t *sink) {
     __shared__ uint32_t pages[kMaxPages];
     const Range w = ranges[blockIdx.x];
@@ -98,7 +101,7 @@ __global__ __launch_bounds__(256) void paged_read(Pool p, const Range *ranges, u
             const bool live = tok < 32 && byte < span && tt < ctx; // (slices at D 64: waves 0-1)
             const uint32_t page = live ? pages[(tt >> p.page_shift) - first_page] : 0u;
             const uint8_t *base = (isv ? p.v : p.k) + (size_t)page * P * p.row_bytes;
-            b[i] = load16(base, live ? P * p.row_bytes : 0u,
+            b[i] = load16<AUX>(base, live ? P * p.row_bytes : 0u,
                           (tt & (P - 1)) * p.row_bytes + base_off + byte);
         }
     };
@@ -239,7 +242,7 @@ int main(int argc, char **argv) {
     }
     // paged patterns: units' chunks laid end to end, cut into equal ranges (3 workgroups per
     // CU, as the decode kernel runs), split where a range crosses units
-    auto paged = [&](int mode, const char *name) {
+    auto paged = [&](int mode, bool nt, const char *name) {
         const bool rows = mode == TOKEN_ROWS;
         std::vector<Range> rs;
         std::vector<std::pair<uint32_t, uint32_t>> units; // (seq, head)
@@ -267,18 +270,26 @@ int main(int argc, char **argv) {
         const uint32_t wgs = rs.size();
         const double us = timed([&](uint32_t c) {
             const Pool pool{kp[c], vp[c], dtable, dctx, stride, shift, row_bytes, head_bytes};
-            if (mode == SLICES) paged_read<SLICES, 2><<<wgs, 256>>>(pool, dranges, sink);
-            else if (mode == HEAD_ROWS) paged_read<HEAD_ROWS, 2><<<wgs, 256>>>(pool, dranges, sink);
-            else if (nlp_rows <= 2) paged_read<TOKEN_ROWS, 2><<<wgs, 256>>>(pool, dranges, sink);
-            else if (nlp_rows <= 4) paged_read<TOKEN_ROWS, 4><<<wgs, 256>>>(pool, dranges, sink);
-            else paged_read<TOKEN_ROWS, 8><<<wgs, 256>>>(pool, dranges, sink);
+            auto launch = [&](auto aux) {
+                constexpr int A = decltype(aux)::value;
+                if (mode == SLICES) paged_read<SLICES, 2, A><<<wgs, 256>>>(pool, dranges, sink);
+                else if (mode == HEAD_ROWS) paged_read<HEAD_ROWS, 2, A><<<wgs, 256>>>(pool, dranges, sink);
+                else if (nlp_rows <= 2) paged_read<TOKEN_ROWS, 2, A><<<wgs, 256>>>(pool, dranges, sink);
+                else if (nlp_rows <= 4) paged_read<TOKEN_ROWS, 4, A><<<wgs, 256>>>(pool, dranges, sink);
+                else paged_read<TOKEN_ROWS, 8, A><<<wgs, 256>>>(pool, dranges, sink);
+            };
+            if (nt) launch(std::integral_constant<int, 2>{});
+            else launch(std::integral_constant<int, 0>{});
         });
         printf("{\"pattern\": \"%s\", \"us\": %.3f, \"GBps\": %.1f, \"bytes\": %.0f, \"workgroups\": %u}\n",
                name, us, live_bytes / us / 1e3, live_bytes, wgs);
     };
-    paged(SLICES, "slices");
-    paged(HEAD_ROWS, "head_rows");
-    paged(TOKEN_ROWS, "token_rows");
+    paged(SLICES, false, "slices");
+    paged(HEAD_ROWS, false, "head_rows");
+    paged(TOKEN_ROWS, false, "token_rows");
+    paged(SLICES, true, "slices_nt");
+    paged(HEAD_ROWS, true, "head_rows_nt");
+    paged(TOKEN_ROWS, true, "token_rows_nt");
     CHECK(hipDeviceSynchronize());
     return 0;
 }
