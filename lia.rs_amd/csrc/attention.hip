@@ -469,7 +469,7 @@ struct Cfg {
     // token, two loads per tile), 64 dims of an FP8 pool (64 bytes).  A lane loads 16
     // contiguous bytes of a token per 16-token tile and load (its A-operand k slots), so
     // every load instruction reads 16 tokens x 64 bytes.
-    static constexpr int SW = FP8 ? 64 : LIA_SW16;
+    static constexpr int SW = FP8 ? 64 : (LIA_SW16 < D ? LIA_SW16 : D);
     static constexpr int AUX = FP8 ? LIA_KV_AUX_FP8 : LIA_KV_AUX; // cache policy of the K/V loads
     static constexpr int WAVES = D / SW;            // one wave per slice
     static constexpr int KS = SW / 32;              // k-steps of S^T = K Q^T per tile
@@ -493,7 +493,9 @@ __device__ __forceinline__ uint32_t swz(uint32_t row) { return 2 * ((row >> 1) &
 // same banks otherwise) land on distinct banks.
 template <int SW>
 __device__ __forceinline__ uint32_t vswz(uint32_t row) {
-    return SW == 32 ? swz(row) : 2 * ((row >> 2) & 1);
+    if constexpr (SW == 32) return swz(row);
+    else if constexpr (SW == 64) return 2 * ((row >> 2) & 1);
+    else return 2 * (row & 7); // 256-byte rows: the 8 rows of a transpose read on distinct banks
 }
 
 template <int D, int KVT>
@@ -958,7 +960,10 @@ __device__ __forceinline__ void store_record(const AttnParams &p, size_t rb, con
 
 // Three workgroups per CU (one wave per SIMD each) is the measured best, so the kernel
 // may use the registers of 3 waves per SIMD (168) instead of squeezing into 4's (128).
-constexpr int kMinWavesPerEU = 3;
+#ifndef LIA_MIN_WAVES_EU
+#define LIA_MIN_WAVES_EU 3
+#endif
+constexpr int kMinWavesPerEU = LIA_MIN_WAVES_EU;
 
 template <int D, int NT, int KVT>
 __global__ __launch_bounds__(D / 32 * 64, kMinWavesPerEU) void attention_kernel(AttnParams p) {
@@ -1779,7 +1784,7 @@ constexpr uint32_t kMaxWavesPerCU = LIA_MAX_WAVES;
 constexpr uint32_t kMaxWavesPerCU8 = LIA_MAX_WAVES_FP8;
 static uint32_t max_waves(int kv) { return kv == LIA_FP8_E4M3 ? kMaxWavesPerCU8 : kMaxWavesPerCU; }
 
-static uint32_t decode_waves(uint32_t d, int kv) { return kv == LIA_FP8_E4M3 ? d / 64 : d / LIA_SW16; }
+static uint32_t decode_waves(uint32_t d, int kv) { return kv == LIA_FP8_E4M3 ? d / 64 : (d > LIA_SW16 ? d / LIA_SW16 : 1); }
 
 // Resident workgroups per CU allowed for a launch of NT column tiles.
 static uint32_t max_per_cu(uint32_t d, uint32_t nt, int kv) {
