@@ -27,6 +27,24 @@ class Case:
         rng = np.random.default_rng(seed + 1000)
         P = g.page_size
         tokens = batch.pool_pages * P
+        if fill == "fp8_codes":
+            # FP8 pools drawn as codes: every finite e4m3fn byte (0x7F / 0xFF are NaN) with
+            # per-(page, head) scales, no float pool to quantise (the 64-sequence pool of
+            # config 5 holds 430M values per plane)
+            assert g.kv_dtype == FP8
+            n = tokens * g.hkv * g.d
+
+            def draw():  # uniform over the 254 finite codes: 0..0x7E, 0x80..0xFE
+                c = rng.integers(0, 254, n, dtype=np.uint8)
+                c += c >= 0x7F
+                return c
+
+            self.kc = draw()
+            self.vc = draw()
+            self.k_scales = rng.uniform(0.002, 0.01, batch.pool_pages * g.hkv).astype(np.float32)
+            self.v_scales = rng.uniform(0.002, 0.01, batch.pool_pages * g.hkv).astype(np.float32)
+            self._finish(batch, rng)
+            return
         kf = rng.standard_normal((tokens, g.hkv, g.d), dtype=np.float32)
         vf = rng.standard_normal((tokens, g.hkv, g.d), dtype=np.float32)
         if fill == "uniform":
@@ -44,6 +62,10 @@ class Case:
         else:
             self.kc = O.from_f32(kf, g.kv_dtype).reshape(-1)
             self.vc = O.from_f32(vf, g.kv_dtype).reshape(-1)
+        self._finish(batch, rng)
+
+    def _finish(self, batch, rng):
+        g = self.g
         qf = rng.standard_normal((batch.n_rows, g.hq, g.d), dtype=np.float32)
         if g.q_dtype == BF16:
             self.q_store = O.from_f32(qf, BF16)
