@@ -1464,15 +1464,18 @@ __global__ __launch_bounds__(64 * LIA_WIDE_WAVES, LIA_WIDE_NTW == 2 ? 2 : 4) voi
                     }
                 }
             } else {
-                // split record: O normalised by its own mass, in f16 (|O/l| <= max |V|, relative
-                // error 2^-11; half the record traffic of f32), with the mass and maximum in f32
+                // split record: O normalised by its own mass in the pool's 16-bit type (|O/l| <=
+                // max |V|, so it stays in range; relative error 2^-11 in f16, 2^-9 in bf16, the
+                // rounding of a bf16 output; half the record traffic of f32), with the mass and
+                // maximum in f32
                 const size_t rb = (size_t)rec * COLS + col;
                 uint16_t *po = (uint16_t *)p.part_o + rb * D + 4 * g;
                 const float inv = lt > 0.0f ? 1.0f / lt : 0.0f;
 #pragma unroll
                 for (int n = 0; n < W::DT; n++) {
                     const f32x4 v = st.o[nt][n] * inv;
-                    *(u32x2 *)(po + 16 * n) = u32x2{pack2<false>(v.x, v.y), pack2<false>(v.z, v.w)};
+                    *(u32x2 *)(po + 16 * n) = u32x2{pack2<KVT == LIA_BF16>(v.x, v.y),
+                                                    pack2<KVT == LIA_BF16>(v.z, v.w)};
                 }
                 if (g == 0) {
                     p.part_ml[rb * 2] = st.m[nt];
@@ -1603,7 +1606,7 @@ __global__ __launch_bounds__(kCombineThreads) void combine_kernel(AttnParams p) 
 constexpr uint32_t kWideCombineCols = LIA_WCC;
 constexpr uint32_t kWideCombinePasses = 2;
 
-template <int D>
+template <int D, bool BF>
 __global__ __launch_bounds__(256) void combine_wide_kernel(AttnParams p) {
     constexpr uint32_t Q = D / 4, RPP = 64 / Q, COLS = 16 * kWideNTDev;
     constexpr uint32_t CW = kWideCombineCols, KP = kWideCombinePasses;
@@ -1614,7 +1617,8 @@ __global__ __launch_bounds__(256) void combine_wide_kernel(AttnParams p) {
     const uint32_t ncols = (md.nrows_hk & 0xffffu) * p.group;
     if (md.n == 0 || col0 >= ncols) return;
     const uint32_t n = md.n, rec0 = md.rec0, q = lane % Q, rg = lane / Q;
-    // records hold O / l in f16 (four values per quad), so a record weighs w * l
+    // records hold O / l in f16, or bf16 for bf16 pools (BF), four values per quad, so a
+    // record weighs w * l
     const u32x2 *po = (const u32x2 *)p.part_o;
     float M[CW], den[CW];
     float4 num[CW];
@@ -1636,8 +1640,12 @@ __global__ __launch_bounds__(256) void combine_wide_kernel(AttnParams p) {
                 const uint32_t r = base + k * RPP + rg;
                 const size_t rb = (size_t)(rec0 + min(r, n - 1)) * COLS + min(col0 + c, ncols - 1);
                 const u32x2 h = po[rb * Q + q];
-                o[c][k] = make_float4(f16_to_f32(h.x & 0xffffu), f16_to_f32(h.x >> 16),
-                                      f16_to_f32(h.y & 0xffffu), f16_to_f32(h.y >> 16));
+                if constexpr (BF)
+                    o[c][k] = make_float4(bf16_to_f32(h.x & 0xffffu), bf16_to_f32(h.x >> 16),
+                                          bf16_to_f32(h.y & 0xffffu), bf16_to_f32(h.y >> 16));
+                else
+                    o[c][k] = make_float4(f16_to_f32(h.x & 0xffffu), f16_to_f32(h.x >> 16),
+                                          f16_to_f32(h.y & 0xffffu), f16_to_f32(h.y >> 16));
                 const float2 ml = ((const float2 *)p.part_ml)[rb];
                 m[c][k] = ml.x;
                 l[c][k] = r < n ? ml.y : 0.0f;
@@ -1998,11 +2006,15 @@ static int run_stages(int stages, const lia_attention_config *c, uint32_t n_seqs
         if (c->head_dim == 128) {
             if (NT == 1) LIA_COMBINE(128, 1);
             else if (NT == 2) LIA_COMBINE(128, 2);
-            else hipLaunchKernelGGL((combine_wide_kernel<128>), wgrid, dim3(256), 0, s, p);
+            else if (c->kv_dtype == LIA_BF16)
+                hipLaunchKernelGGL((combine_wide_kernel<128, true>), wgrid, dim3(256), 0, s, p);
+            else hipLaunchKernelGGL((combine_wide_kernel<128, false>), wgrid, dim3(256), 0, s, p);
         } else {
             if (NT == 1) LIA_COMBINE(64, 1);
             else if (NT == 2) LIA_COMBINE(64, 2);
-            else hipLaunchKernelGGL((combine_wide_kernel<64>), wgrid, dim3(256), 0, s, p);
+            else if (c->kv_dtype == LIA_BF16)
+                hipLaunchKernelGGL((combine_wide_kernel<64, true>), wgrid, dim3(256), 0, s, p);
+            else hipLaunchKernelGGL((combine_wide_kernel<64, false>), wgrid, dim3(256), 0, s, p);
         }
 #undef LIA_COMBINE
     }

@@ -21,7 +21,7 @@ def u32_dev(a):
 
 
 class Case:
-    def __init__(self, batch, seed=0, fill="normal"):
+    def __init__(self, batch, seed=0, fill="normal", v_scale=1.0):
         g = batch.geom
         self.batch, self.g = batch, g
         rng = np.random.default_rng(seed + 1000)
@@ -50,6 +50,8 @@ class Case:
         if fill == "uniform":
             kf = rng.uniform(-1, 1, kf.shape).astype(np.float32)
             vf = rng.uniform(-1, 1, vf.shape).astype(np.float32)
+        if v_scale != 1.0:
+            vf *= np.float32(v_scale)
         self.k_scales = self.v_scales = None
         if g.kv_dtype == FP8:
             layout = O.KVLayout(g.hkv, g.d, P, batch.pool_pages, FP8)

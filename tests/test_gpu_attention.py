@@ -159,6 +159,20 @@ def test_config3_mixed_prefill_full_size(lia, wl):
     _check(G.Case(wl.config3(seed=0), seed=0), lia, "cfg3")
 
 
+def test_prefill_bf16_values_beyond_f16_range(lia, wl):
+    """A bf16 pool with |V| around 2e5 (beyond f16's 65504) through the prefill kernel's split
+    records and their combine: the records keep the pool's type, so nothing overflows."""
+    b = wl.custom([300, 1000 + 77, 2000 + 40], [300, 77, 40], seed=12)
+    case = G.Case(b, seed=12, v_scale=2e5)
+    print("[case] prefill bf16 |V| ~ 2e5", flush=True)
+    got = case.run(lia)
+    ref = case.f64()
+    mx, mean = G.errors(got, ref)
+    print(f"[case] prefill bf16 |V| ~ 2e5: max_abs={mx:.3e} mean_abs={mean:.3e}", flush=True)
+    assert np.all(np.isfinite(got))
+    assert mx < 2e-2 * 2e5 and mean < 2e-3 * 2e5
+
+
 @pytest.mark.parametrize("kv,d,page", [(F16, 128, 32), (BF16, 64, 16)])
 def test_prefill_kernel_geometries(lia, wl, kv, d, page):
     """Prefill units of 128 columns over other page sizes, head_dim 64 and f16 pools, with
