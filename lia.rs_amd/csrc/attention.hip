@@ -437,10 +437,11 @@ __global__ __launch_bounds__(256) void plan_kernel(uint32_t n_seqs, const uint32
 
 // ------------------------------------------------------------------ the attention kernel
 //
-// A workgroup has D/32 wavefronts; wave w owns head_dim slice [32w, 32w+32).  Every wave
-// walks every 32-token chunk of the workgroup's block range: it loads its 32-dim slice of
-// K (registers, MFMA A operand) and V (direct-to-LDS), computes its partial S^T = K_w Q_w^T
-// with one MFMA per 16-token tile, and the partial scores are summed across the waves
+// A workgroup has D/SW wavefronts; wave w owns head_dim slice [SW w, SW w + SW) (SW = 64
+// dims on 16-bit and FP8 pools).  Every wave walks every 32-token chunk of the workgroup's
+// block range: it loads its slice of K (registers, MFMA A operand) and V (direct-to-LDS on
+// 16-bit pools, through registers on FP8 pools), computes its partial S^T = K_w Q_w^T with
+// SW/32 MFMAs per 16-token tile, and the partial scores are summed across the waves
 // through LDS (one barrier per chunk).  Each wave then runs the same online softmax on the
 // same scores and accumulates O^T for its own d slice.  Work inside a workgroup is
 // therefore split evenly whatever the segment lengths, and no end-of-segment merge is
@@ -958,13 +959,15 @@ __device__ __forceinline__ void store_record(const AttnParams &p, size_t rb, con
     }
 }
 
-// Three workgroups per CU (one wave per SIMD each) is the measured best, so the kernel
-// may use the registers of 3 waves per SIMD (168) instead of squeezing into 4's (128).
+// At most 6 (16-bit pools) or 8 (FP8) decode waves run per CU, under 2 per SIMD, so the
+// kernel may use the registers of 3 waves per SIMD (168) instead of squeezing into 4's (128).
 #ifndef LIA_MIN_WAVES_EU
 #define LIA_MIN_WAVES_EU 3
 #endif
 constexpr int kMinWavesPerEU = LIA_MIN_WAVES_EU;
 
+// The workgroup-size bound (D/32 waves) is looser than the D/SW waves launched: the
+// exact bound changes register allocation and measured 1 % slower on a batch-8 bf16 decode.
 template <int D, int NT, int KVT>
 __global__ __launch_bounds__(D / 32 * 64, kMinWavesPerEU) void attention_kernel(AttnParams p) {
     using C = Cfg<D, KVT>;

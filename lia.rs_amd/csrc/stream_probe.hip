@@ -3,14 +3,16 @@
 //
 // Reads the K and V planes of a paged pool the way a decode layer does - every live token
 // of every (sequence, KV head) once - with loads that do nothing but fold the data into a
-// register, so the time is the memory system's alone.  Four access patterns:
+// register, so the time is the memory system's alone.  Five access patterns, the paged
+// ones also with the non-temporal cache policy (`_nt`):
 //   contiguous  both planes read front to back (the pool's bytes, no paging): the practical
 //               read ceiling for a transfer of this size;
 //   contiguous_1gib  one launch reading 1 GiB front to back: the sustained rate, without the
 //               ramp and tail a launch of a few tens of microseconds pays;
-//   slices      the decode kernel's mapping: a 4-wave workgroup per block range of a
-//               (sequence, KV head) unit, wave w loading the 64-byte slice [64w, 64w+64) of
-//               each token's head row (one load = 16 tokens x 64 bytes);
+//   slices      per-wave 64-byte d slices (the decode kernel's mapping on FP8 pools): a
+//               4-wave workgroup per block range of a (sequence, KV head) unit, wave w
+//               loading bytes [64w, 64w+64) of each token's head row (one load = 16 tokens x
+//               64 bytes);
 //   head_rows   whole head rows: one load = 64*16/(2D) tokens x 2D bytes, the waves of a
 //               workgroup taking consecutive tokens of each 32-token chunk;
 //   token_rows  whole token rows (every KV head): units are sequences.
