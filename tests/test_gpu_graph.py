@@ -1,6 +1,7 @@
 """Graph capture of a whole paged step and the output-row gather.
 
-The step (device packing, plan, fused append + partial attention, merge) is captured once
+The step (device packing, plan, the KV append - fused into the attention launch on 16-bit
+pools, the quantising append on FP8 pools - partial attention, merge) is captured once
 and replayed several times with new queries written between replays by ordinary eager work;
 every replay must equal the eager execution of the same step bit for bit (the reference
 replays captured paged graphs the same way, src/inference/paging.rs:215-259)."""
@@ -9,21 +10,40 @@ import pytest
 import torch
 
 import gpu_data as G
-from gpu_data import BF16
+from gpu_data import BF16, FP8
 
 pytestmark = pytest.mark.gpu
 
 
-def _setup(lia, wl, seed):
-    b = wl.custom([300, 1200, 17, 5000, 64], [1, 1, 3, 1, 64], seed=seed)
+BATCHES = {
+    # decode, MTP-like and prefill rows mixed (the decode kernel)
+    "mixed": (([300, 1200, 17, 5000, 64], [1, 1, 3, 1, 64]), BF16),
+    # long chunks with prefixes (the prefill kernel and its combine)
+    "prefill": (([300, 1000 + 77, 2000 + 40], [300, 77, 40]), BF16),
+    # an FP8 pool: quantising append, then attention over e4m3 pages
+    "fp8": (([300, 1200, 17, 5000, 64], [1, 1, 3, 1, 64]), FP8),
+}
+
+
+def _setup(lia, wl, kind, seed):
+    (ctx, q_len), kv = BATCHES[kind]
+    b = wl.custom(ctx, q_len, geom=wl.Geometry(kv_dtype=kv), seed=seed)
     case = G.Case(b, seed=seed)
     g = b.geom
     dev = case.device()
     W = g.hkv * g.d
     slots = b.slot_mapping().astype(np.int64)
-    newk = G.to_dev(case.kc.reshape(-1, W)[slots].copy(), torch.bfloat16)
-    newv = G.to_dev(case.vc.reshape(-1, W)[slots].copy(), torch.bfloat16)
+    if kv == FP8:
+        rng = np.random.default_rng(seed)
+        newk = G.to_dev(G.O.from_f32(rng.standard_normal((b.n_rows, W), dtype=np.float32) * 0.01, BF16),
+                        torch.bfloat16)
+        newv = G.to_dev(G.O.from_f32(rng.standard_normal((b.n_rows, W), dtype=np.float32) * 0.01, BF16),
+                        torch.bfloat16)
+    else:
+        newk = G.to_dev(case.kc.reshape(-1, W)[slots].copy(), torch.bfloat16)
+        newv = G.to_dev(case.vc.reshape(-1, W)[slots].copy(), torch.bfloat16)
     cfg = case.config(lia)
+    layout = lia.KVLayout(g.hkv, g.d, g.page_size, b.pool_pages, kv)
     ws = torch.zeros(lia.workspace_bytes(cfg), dtype=torch.uint8, device="cuda")
     meta = dict(
         seq_slots=G.u32_dev(np.arange(b.n_seqs)), q_lens=G.u32_dev(b.q_len), cached=G.u32_dev(b.cached),
@@ -40,14 +60,21 @@ def _setup(lia, wl, seed):
                         meta["positions"], meta["sequences"], meta["slots"], meta["status"])
         lia.attention_plan(cfg, b.n_seqs, b.n_rows, meta["cu"], meta["positions"], meta["sequences"],
                            ws, pages=dev["pages"])
-        lia.attention_partial_append(cfg, b.n_seqs, dev["pages"], meta["slots"], dev["q"], newk, newv,
-                                     dev["kc"], dev["vc"], out, ws)
+        if kv == FP8:
+            lia.kv_append(layout, newk, newv, dev["kc"], dev["vc"], slot_mapping=meta["slots"],
+                          k_scales=dev["k_scales"], v_scales=dev["v_scales"])
+            lia.attention_partial(cfg, b.n_seqs, dev["pages"], dev["q"], dev["kc"], dev["vc"], out, ws,
+                                  k_scales=dev["k_scales"], v_scales=dev["v_scales"])
+        else:
+            lia.attention_partial_append(cfg, b.n_seqs, dev["pages"], meta["slots"], dev["q"], newk,
+                                         newv, dev["kc"], dev["vc"], out, ws)
         lia.attention_merge(cfg, b.n_seqs, b.n_rows, out, ws)
     return b, case, dev, step, out, meta
 
 
-def test_graph_replays_equal_eager(lia, wl):
-    b, case, dev, step, out, meta = _setup(lia, wl, 31)
+@pytest.mark.parametrize("kind", list(BATCHES))
+def test_graph_replays_equal_eager(lia, wl, kind):
+    b, case, dev, step, out, meta = _setup(lia, wl, kind, 31)
     pool_k, pool_v = dev["kc"].clone(), dev["vc"].clone()
     rng = np.random.default_rng(5)
     qs = [G.to_dev(G.O.from_f32(rng.standard_normal(tuple(dev["q"].shape), dtype=np.float32), BF16),
@@ -70,7 +97,7 @@ def test_graph_replays_equal_eager(lia, wl):
             step()
     torch.cuda.synchronize()
     for i, q in enumerate(qs):
-        print(f"[case] graph replay {i}", flush=True)
+        print(f"[case] graph replay {kind} {i}", flush=True)
         dev["q"].copy_(q)
         dev["kc"].copy_(pool_k)
         dev["vc"].copy_(pool_v)
@@ -80,11 +107,17 @@ def test_graph_replays_equal_eager(lia, wl):
         torch.cuda.synchronize()
         assert torch.equal(out.view(torch.int16), expected[i][0].view(torch.int16)), i
         assert torch.equal(dev["kc"], expected[i][1]), i
-    # the replayed output is also right against the f64 oracle (last query set)
+    # the replayed output is also right against the f64 oracle on the pool the step left
+    # (last query set)
+    store = np.uint8 if case.g.kv_dtype == FP8 else np.uint16
+    case.kc = dev["kc"].cpu().numpy().view(store).reshape(-1)
+    case.vc = dev["vc"].cpu().numpy().view(store).reshape(-1)
     case.q_store = qs[-1].view(torch.int16).cpu().numpy().view(np.uint16)
     case.q32 = G.O.to_f32(case.q_store, BF16)
     mx, mean = G.errors(out.float().cpu().numpy(), case.f64())
-    assert mx < 2e-2 and mean < 2e-3
+    tol = (5e-2, 5e-3) if case.g.kv_dtype == FP8 else (2e-2, 2e-3)
+    print(f"[case] graph {kind}: max_abs={mx:.3e} mean_abs={mean:.3e}", flush=True)
+    assert mx < tol[0] and mean < tol[1]
 
 
 @pytest.mark.parametrize("width,offset", [(2048, 0), (2048 + 4, 0), (7, 0), (256, 1)])
