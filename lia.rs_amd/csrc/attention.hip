@@ -6,12 +6,13 @@
 // attends keys 0 .. positions[last row of the block], tiled in 32-token blocks.
 //
 // Scheduling is balanced over workgroups rather than over units: the key blocks of all
-// units are laid end to end and workgroup w of N takes blocks [w*B/N, (w+1)*B/N).  The
-// four wavefronts of a workgroup interleave the 32-token chunks of its range and merge
-// their online-softmax states in LDS at the end of every unit segment.  A unit covered by
-// one workgroup is written normalised straight to `out`; a unit split across workgroups
-// leaves one partial record per workgroup (unnormalised O, reference max, mass) and the
-// combine kernel merges them - the reference's split-K partial + merge
+// units are laid end to end and workgroup w of N takes blocks [w*B/N, (w+1)*B/N).  In the
+// decode kernel the waves of a workgroup split head_dim and walk the same 32-token chunks,
+// summing their partial scores through LDS; in the prefill kernel (wide_kernel) each wave
+// owns 16 of a unit's 128 columns and all waves share each chunk's K/V staged in LDS.  A
+// unit covered by one workgroup is written normalised straight to `out`; a unit split
+// across workgroups leaves one partial record per workgroup (O, reference max, mass) and
+// the combine kernels merge them - the reference's split-K partial + merge
 // (src/gpu/kernels/llama_flash_kernel.rs:321-376, src/gpu/kernels/llama_merge.rs:10-76)
 // with splits chosen for load balance instead of a batch-uniform span.
 //
