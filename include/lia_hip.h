@@ -153,12 +153,13 @@ typedef struct lia_kv_layout {
  * with slot(r) = slot_mapping[r] when slot_mapping != NULL, else computed from
  * positions/sequences/pages/stride exactly as the reference does.  Values are converted
  * from src_dtype (LIA_F32, LIA_F16 or LIA_BF16) to the pool dtype with round-to-nearest-even
- * (FP8: divided by the page's scale first, saturated to +-448).
+ * (FP8: divided by the page's scale first, saturated to +-448; a page whose scale is still 0,
+ * never quantised, takes scale 1 and the append writes 1 into k_scales / v_scales).
  */
 int lia_kv_append(const lia_kv_layout *layout, uint32_t rows, const uint32_t *positions,
                   const uint32_t *sequences, const uint32_t *pages, uint32_t stride,
                   const uint32_t *slot_mapping, int32_t src_dtype, const void *k, const void *v,
-                  void *kc, void *vc, const float *k_scales, const float *v_scales,
+                  void *kc, void *vc, float *k_scales, float *v_scales,
                   lia_stream_t stream);
 
 /*
@@ -180,14 +181,15 @@ int lia_rope_coefficients(uint32_t rows, uint32_t head_dim, float base, const ui
  *   x'[i + d/2] = fma(x[i + d/2], cos_i, f32(x[i] * sin_i))       (i < d/2)
  * Rotated queries go to query ([rows][num_q_heads][head_dim], LIA_F32 or LIA_BF16); rotated
  * K and unrotated V are appended exactly as lia_kv_append appends f32 rows (slot_mapping or
- * positions/sequences/pages/stride; FP8 pools divide by the page scale).  input, query and
+ * positions/sequences/pages/stride; FP8 pools divide by the page scale, a scale of 0 taking 1
+ * as in lia_kv_append).  input, query and
  * coefficients 16-byte aligned.
  */
 int lia_rope_kv_append(const lia_kv_layout *layout, uint32_t num_q_heads, uint32_t rows,
                        const uint32_t *positions, const uint32_t *sequences, const uint32_t *pages,
                        uint32_t stride, const uint32_t *slot_mapping, const float *coefficients,
                        const float *input, void *query, int32_t query_dtype, void *kc, void *vc,
-                       const float *k_scales, const float *v_scales, lia_stream_t stream);
+                       float *k_scales, float *v_scales, lia_stream_t stream);
 
 /*
  * FP8 page quantisation: converts n_pages whole pages (page ids in page_ids) of K and V

@@ -3,6 +3,18 @@
 
 namespace lia {
 
+// FP8 page scale for an append.  A page appended to before it was ever quantised holds
+// scale 0; it takes scale 1, which the appending threads record (every writer stores the
+// same value, and readers after the append see 1).
+__device__ __forceinline__ float append_scale(float *scales, size_t at) {
+    float s = scales[at];
+    if (s == 0.0f) {
+        s = 1.0f;
+        scales[at] = 1.0f;
+    }
+    return s;
+}
+
 // Per-step packing on the device.  One workgroup scans the per-sequence new-token counts
 // into cu_seqlens and then every thread fills rows: position = cached + i, sequence =
 // table row, slot = pages[seq * stride + pos / P] * P + pos % P (the slot rule of
@@ -114,8 +126,8 @@ __global__ __launch_bounds__(256) void append_kernel(uint32_t rows, uint32_t wid
                                                      uint32_t page_shift,
                                                      const uint32_t *slot_mapping, int src_kind,
                                                      const void *k, const void *v, void *kc,
-                                                     void *vc, const float *k_scales,
-                                                     const float *v_scales) {
+                                                     void *vc, float *k_scales,
+                                                     float *v_scales) {
     const size_t i = ((size_t)blockIdx.x * 256 + threadIdx.x);
     const uint32_t quads = width / 4;
     if (i >= (size_t)rows * quads) return;
@@ -147,7 +159,8 @@ __global__ __launch_bounds__(256) void append_kernel(uint32_t rows, uint32_t wid
     size_t dst = (size_t)slot * width + e0;
     if constexpr (KVT == LIA_FP8_E4M3) {
         uint32_t page = slot >> page_shift, h = e0 / hd;
-        float ks = k_scales[(size_t)page * hkv + h], vs = v_scales[(size_t)page * hkv + h];
+        const float ks = append_scale(k_scales, (size_t)page * hkv + h);
+        const float vs = append_scale(v_scales, (size_t)page * hkv + h);
         uint32_t kw = 0, vw = 0;
 #pragma unroll
         for (int j = 0; j < 4; j++) {
@@ -253,7 +266,7 @@ __global__ __launch_bounds__(256) void rope_append_kernel(
     uint32_t rows, uint32_t hq, uint32_t hkv, uint32_t d, const uint32_t *positions,
     const uint32_t *sequences, const uint32_t *pages, uint32_t stride, uint32_t page_shift,
     const uint32_t *slot_mapping, const float *coefficients, const float *input, void *query,
-    int query_bf16, void *kc, void *vc, const float *k_scales, const float *v_scales) {
+    int query_bf16, void *kc, void *vc, float *k_scales, float *v_scales) {
 #pragma clang fp contract(off)
     const uint32_t half = d / 2, quads = half / 4, heads = hq + hkv;
     const uint32_t i = blockIdx.x * 256 + threadIdx.x; // the host bounds the grid to 32 bits
@@ -299,8 +312,8 @@ __global__ __launch_bounds__(256) void rope_append_kernel(
     float ks = 1.0f, vs = 1.0f;
     if constexpr (KVT == LIA_FP8_E4M3) {
         const size_t ps = (size_t)(slot >> page_shift) * hkv + kh;
-        ks = k_scales[ps];
-        vs = v_scales[ps];
+        ks = append_scale(k_scales, ps);
+        vs = append_scale(v_scales, ps);
     }
     const size_t at = ((size_t)slot * hkv + kh) * d + d0;
     const float *v = input + r * width + (size_t)(hq + hkv + kh) * d;
@@ -361,7 +374,7 @@ extern "C" int lia_rope_kv_append(const lia_kv_layout *L, uint32_t num_q_heads, 
                                   const uint32_t *pages, uint32_t stride,
                                   const uint32_t *slot_mapping, const float *coefficients,
                                   const float *input, void *query, int32_t query_dtype, void *kc,
-                                  void *vc, const float *k_scales, const float *v_scales,
+                                  void *vc, float *k_scales, float *v_scales,
                                   lia_stream_t stream) {
     if (!L || !coefficients || !input || !query || !kc || !vc) return LIA_E_ARG;
     if (L->head_dim != 64 && L->head_dim != 128) return LIA_E_UNSUPPORTED;
@@ -415,8 +428,8 @@ extern "C" int lia_pack_device(uint32_t n_seqs, const uint32_t *seq_slots, const
 extern "C" int lia_kv_append(const lia_kv_layout *L, uint32_t rows, const uint32_t *positions,
                              const uint32_t *sequences, const uint32_t *pages, uint32_t stride,
                              const uint32_t *slot_mapping, int32_t src_dtype, const void *k,
-                             const void *v, void *kc, void *vc, const float *k_scales,
-                             const float *v_scales, lia_stream_t stream) {
+                             const void *v, void *kc, void *vc, float *k_scales,
+                             float *v_scales, lia_stream_t stream) {
     if (!L || !k || !v || !kc || !vc) return LIA_E_ARG;
     if (rows == 0) return LIA_OK;
     if (!slot_mapping && (!positions || !sequences || !pages || stride == 0)) return LIA_E_ARG;

@@ -244,7 +244,7 @@ static inline uint32_t slot_of(uint32_t position, uint32_t seq, const uint32_t *
 void lo_kv_append(const lia_kv_layout *L, uint32_t rows, const uint32_t *positions,
                   const uint32_t *sequences, const uint32_t *pages, uint32_t stride,
                   const uint32_t *slot_mapping, int32_t src_dtype, const void *k, const void *v,
-                  void *kc, void *vc, const float *k_scales, const float *v_scales) {
+                  void *kc, void *vc, float *k_scales, float *v_scales) {
     uint32_t W = L->num_kv_heads * L->head_dim;
     for (uint32_t r = 0; r < rows; r++) {
         uint32_t slot = slot_mapping ? slot_mapping[r]
@@ -265,8 +265,12 @@ void lo_kv_append(const lia_kv_layout *L, uint32_t rows, const uint32_t *positio
                 break;
             case LIA_FP8_E4M3: {
                 uint32_t h = i / L->head_dim;
-                float ks = k_scales[(size_t)page * L->num_kv_heads + h];
-                float vs = v_scales[(size_t)page * L->num_kv_heads + h];
+                /* a page never quantised (scale 0) takes scale 1, recorded by the append */
+                float *ksp = &k_scales[(size_t)page * L->num_kv_heads + h];
+                float *vsp = &v_scales[(size_t)page * L->num_kv_heads + h];
+                if (*ksp == 0.0f) *ksp = 1.0f;
+                if (*vsp == 0.0f) *vsp = 1.0f;
+                float ks = *ksp, vs = *vsp;
                 ((uint8_t *)kc)[at] = lo_f32_to_e4m3(kv / ks);
                 ((uint8_t *)vc)[at] = lo_f32_to_e4m3(vv / vs);
                 break;
@@ -552,8 +556,8 @@ void lo_rotary_cache(uint32_t rows, uint32_t stride, uint32_t page_size, const u
 void lo_rope_kv_append(const lia_kv_layout *L, uint32_t hq, uint32_t rows, const uint32_t *positions,
                        const uint32_t *sequences, const uint32_t *pages, uint32_t stride,
                        const uint32_t *slot_mapping, const float *coefficients, const float *input,
-                       void *query, int32_t query_dtype, void *kc, void *vc, const float *k_scales,
-                       const float *v_scales) {
+                       void *query, int32_t query_dtype, void *kc, void *vc, float *k_scales,
+                       float *v_scales) {
     const uint32_t d = L->head_dim, half = d / 2, hkv = L->num_kv_heads;
     const size_t width = (size_t)(hq + 2 * hkv) * d;
     float *kr = (float *)malloc((size_t)rows * hkv * d * sizeof(float));

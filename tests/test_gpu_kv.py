@@ -36,6 +36,9 @@ def _append_case(O, lia, wl, kv, src, page, use_slots, rows_per_seq=(1, 3, 40), 
     if kv == FP8:
         k_scales = rng.uniform(0.005, 0.02, b.pool_pages * g.hkv).astype(np.float32)
         v_scales = rng.uniform(0.005, 0.02, b.pool_pages * g.hkv).astype(np.float32)
+        # pages never quantised (scale 0) take scale 1, which the append records
+        k_scales[rng.random(k_scales.size) < 0.3] = 0.0
+        v_scales[rng.random(v_scales.size) < 0.3] = 0.0
     layout_o = O.KVLayout(g.hkv, g.d, page, b.pool_pages, kv)
     layout_p = lia.KVLayout(g.hkv, g.d, page, b.pool_pages, kv)
     pos, seq, flat, slots = b.positions(), b.sequences(), b.flat_table(), b.slot_mapping()
@@ -55,6 +58,8 @@ def _append_case(O, lia, wl, kv, src, page, use_slots, rows_per_seq=(1, 3, 40), 
     gk = dkc.cpu().numpy().view(store)
     gv = dvc.cpu().numpy().view(store)
     assert np.array_equal(gk, kc) and np.array_equal(gv, vc)
+    if kv == FP8:
+        assert np.array_equal(dks.cpu().numpy(), k_scales) and np.array_equal(dvs.cpu().numpy(), v_scales)
 
 
 @pytest.mark.parametrize("kv", [F16, BF16, FP8])

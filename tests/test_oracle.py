@@ -200,6 +200,40 @@ def test_kv_append_brute_force(O, dtype):
     assert np.array_equal(kc, ek) and np.array_equal(vc, ev)
 
 
+def test_fp8_append_scale_rule(O):
+    """FP8 append: values divided by the page's scale and rounded to e4m3 (torch's
+    float8_e4m3fn cast); a page whose scale is 0 (never quantised) takes scale 1 and the
+    append writes 1 into the scale arrays, pages not appended to keep 0."""
+    rng = np.random.default_rng(8)
+    H, D, P, pool = 2, 64, 16, 6
+    layout = O.KVLayout(H, D, P, pool, FP8)
+    slots = np.array([0 * P + 3, 2 * P + 5, 2 * P + 6, 4 * P + 0], np.uint32)
+    k = rng.standard_normal((4, H * D)).astype(np.float32)
+    v = rng.standard_normal((4, H * D)).astype(np.float32)
+    ks = np.zeros(pool * H, np.float32)
+    vs = np.zeros(pool * H, np.float32)
+    ks[2 * H:3 * H] = [0.01, 0.02]   # page 2 quantised before, pages 0 and 4 never
+    vs[2 * H:3 * H] = [0.03, 0.04]
+    kc = np.zeros(pool * P * H * D, np.uint8)
+    vc = np.zeros_like(kc)
+    zeros = np.zeros(4, np.uint32)
+    O.kv_append(layout, zeros, zeros, zeros, 0, k, v, kc, vc, slot_mapping=slots, k_scales=ks, v_scales=vs)
+    want_k = np.zeros(pool * H, np.float32)
+    want_v = np.zeros(pool * H, np.float32)
+    want_k[[0, 1, 8, 9]] = 1.0
+    want_v[[0, 1, 8, 9]] = 1.0
+    want_k[4:6], want_v[4:6] = [0.01, 0.02], [0.03, 0.04]
+    assert np.array_equal(ks, want_k) and np.array_equal(vs, want_v)
+    e4m3 = lambda a: torch.from_numpy(a).to(torch.float8_e4m3fn).view(torch.uint8).numpy()
+    for r, slot in enumerate(slots):
+        page = slot // P
+        scale_k = np.repeat(ks[page * H:(page + 1) * H], D)
+        scale_v = np.repeat(vs[page * H:(page + 1) * H], D)
+        at = slot * H * D
+        assert np.array_equal(kc[at:at + H * D], e4m3(k[r] / scale_k))
+        assert np.array_equal(vc[at:at + H * D], e4m3(v[r] / scale_v))
+
+
 def test_kv_quantize_pages_closed_form(O):
     rng = np.random.default_rng(6)
     H, D, P, pool = 2, 64, 16, 6
