@@ -301,7 +301,10 @@ int lia_paged_attention(const lia_attention_config *config, uint32_t n_seqs, uin
  *                          (replaces gpu::llama_attention::partial, llama_attention.rs:24-159).
  *   lia_attention_merge:   combines the partial records into out (replaces
  *                          gpu::llama_attention::merge, llama_attention.rs:163-207).
- * n_seqs / n_rows must be the same in all three calls of one plan.
+ * n_seqs / n_rows must be the same in all three calls of one plan, and cu_seqlens must describe
+ * exactly n_rows rows (cu_seqlens[n_seqs] == n_rows, as lia_pack_rows / lia_pack_device write
+ * it).  Device metadata is not read back by the host: a plan whose rows would need more
+ * units than the workspace was sized for schedules no work, and out is left unwritten.
  */
 int lia_attention_plan(const lia_attention_config *config, uint32_t n_seqs, uint32_t n_rows,
                        const uint32_t *cu_seqlens, const uint32_t *positions,
