@@ -1952,7 +1952,11 @@ static int run_stages(int stages, const lia_attention_config *c, uint32_t n_seqs
     const uint32_t group = c->num_q_heads / c->num_kv_heads;
     const uint32_t NT = nt_for(n_rows, n_seqs, group, c->kv_dtype);
     const uint32_t n_wg = workgroups_for(c, NT);
-    const uint32_t rpc = (16 * NT) / group;
+    // rows per column block; with as many rows as sequences (decode, possibly with some
+    // sequences adding no rows and others several) one row per block, so every unit has
+    // `group` columns and there are n_rows units per KV head (the merge grid below relies
+    // on both)
+    const uint32_t rpc = (NT == 1 && n_rows == n_seqs) ? 1 : (16 * NT) / group;
     uint8_t *ws = (uint8_t *)workspace;
     AttnParams p;
     p.q = q; p.kc = kc; p.vc = vc; p.k_scales = k_scales; p.v_scales = v_scales;
@@ -1999,8 +2003,8 @@ static int run_stages(int stages, const lia_attention_config *c, uint32_t n_seqs
         // units this NT can produce: rows in blocks of rpc per sequence and KV head
         uint32_t units_nt = (c->max_rows / (rpc ? rpc : 1) + n_seqs + 1) * c->num_kv_heads;
         uint32_t cols = 16 * NT;
-        if (n_rows == n_seqs) {
-            // one row per sequence: exactly one unit per (sequence, KV head), `group` columns
+        if (NT == 1 && n_rows == n_seqs) {
+            // one row per column block (rpc = 1): n_rows units per KV head, `group` columns
             units_nt = n_seqs * c->num_kv_heads;
             cols = group < cols ? group : cols;
         }

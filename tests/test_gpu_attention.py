@@ -144,6 +144,32 @@ def test_config5_fp8_full_size(lia, wl):
     assert np.max(np.abs(got - ref)) < 2e-3
 
 
+@pytest.mark.parametrize("q_len", [[1, 0, 3, 0, 1], [0, 0, 200, 0, 1], [0, 1, 0, 0, 0]])
+def test_sequences_without_rows(lia, wl, q_len):
+    """Sequences that add no rows this step (repeated cu_seqlens entries) next to decode, MTP
+    and prefill rows: device packing equals the host packing and attention the oracle."""
+    ctx = [500, 300, 1000 + 200, 64, 4097]
+    b = wl.custom(ctx, q_len, seed=21)
+    case = G.Case(b, seed=21)
+    print(f"[case] sequences without rows q_len={q_len}", flush=True)
+    n, rows, P = b.n_seqs, b.n_rows, b.geom.page_size
+    dev = {k: torch.full((rows + (k == "cu"),), -7, dtype=torch.int32, device="cuda")
+           for k in ("cu", "positions", "sequences", "slots")}
+    dev["cu"] = torch.full((n + 1,), -7, dtype=torch.int32, device="cuda")
+    status = torch.full((1,), -7, dtype=torch.int32, device="cuda")
+    lia.pack_device(G.u32_dev(np.arange(n)), G.u32_dev(b.q_len), G.u32_dev(b.cached),
+                    G.u32_dev(b.flat_table()), b.stride, P, b.pool_pages, b.stride * P, rows,
+                    dev["cu"], dev["positions"], dev["sequences"], dev["slots"], status)
+    torch.cuda.synchronize()
+    assert status.item() == 0
+    got = {k: v.cpu().numpy().view(np.uint32) for k, v in dev.items()}
+    assert np.array_equal(got["cu"], b.cu_seqlens())
+    assert np.array_equal(got["positions"], b.positions())
+    assert np.array_equal(got["sequences"], b.sequences())
+    assert np.array_equal(got["slots"], b.slot_mapping())
+    _check(case, lia, f"no-row sequences {q_len}")
+
+
 def test_repeat_calls_are_identical(lia, wl):
     b = wl.custom([5000, 17, 900], [1, 1, 3], seed=8)
     case = G.Case(b, seed=8)
