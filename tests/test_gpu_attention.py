@@ -144,7 +144,8 @@ def test_config5_fp8_full_size(lia, wl):
     assert np.max(np.abs(got - ref)) < 2e-3
 
 
-@pytest.mark.parametrize("q_len", [[1, 0, 3, 0, 1], [0, 0, 200, 0, 1], [0, 1, 0, 0, 0]])
+@pytest.mark.parametrize("q_len", [[1, 0, 3, 0, 1], [0, 0, 200, 0, 1], [0, 1, 0, 0, 0],
+                                   [3, 0, 4, 0, 2]])
 def test_sequences_without_rows(lia, wl, q_len):
     """Sequences that add no rows this step (repeated cu_seqlens entries) next to decode, MTP
     and prefill rows: device packing equals the host packing and attention the oracle."""
@@ -168,6 +169,18 @@ def test_sequences_without_rows(lia, wl, q_len):
     assert np.array_equal(got["sequences"], b.sequences())
     assert np.array_equal(got["slots"], b.slot_mapping())
     _check(case, lia, f"no-row sequences {q_len}")
+
+
+@pytest.mark.parametrize("kv", [BF16, FP8])
+@pytest.mark.parametrize("page", [64, 128])
+def test_large_pages(lia, wl, kv, page):
+    """Pages of 64 and 128 tokens (a 32-token chunk inside one page): decode and MTP rows with
+    contexts around page and chunk edges, then prefill chunks with prefixes."""
+    g = wl.Geometry(kv_dtype=kv, page_size=page)
+    b = wl.custom([1, 63, 64, 65, 700, 4100], [1, 1, 2, 3, 1, 1], geom=g, seed=23)
+    _check(G.Case(b, seed=23), lia, f"pages of {page} kv={kv} decode/MTP")
+    b = wl.custom([300, 1000 + 77, 129], [300, 77, 129], geom=g, seed=24)
+    _check(G.Case(b, seed=24), lia, f"pages of {page} kv={kv} prefill")
 
 
 def test_repeat_calls_are_identical(lia, wl):
