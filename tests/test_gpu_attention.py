@@ -183,6 +183,17 @@ def test_large_pages(lia, wl, kv, page):
     _check(G.Case(b, seed=24), lia, f"pages of {page} kv={kv} prefill")
 
 
+@pytest.mark.parametrize("hq,hkv", [(32, 1), (24, 1), (64, 2)])
+def test_large_groups(lia, wl, hq, hkv):
+    """GQA groups of 24 and 32 (the largest accepted): two 16-column tiles hold one row, or
+    128 / group rows in a prefill unit."""
+    g = wl.Geometry(hq=hq, hkv=hkv, d=128)
+    b = wl.custom([1, 17, 700, 4100], [1, 1, 3, 1], geom=g, seed=25)
+    _check(G.Case(b, seed=25), lia, f"group {hq // hkv} decode/MTP")
+    b = wl.custom([300, 1000 + 77], [300, 77], geom=g, seed=26)
+    _check(G.Case(b, seed=26), lia, f"group {hq // hkv} prefill")
+
+
 def test_repeat_calls_are_identical(lia, wl):
     b = wl.custom([5000, 17, 900], [1, 1, 3], seed=8)
     case = G.Case(b, seed=8)
