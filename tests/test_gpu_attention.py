@@ -194,6 +194,16 @@ def test_large_groups(lia, wl, hq, hkv):
     _check(G.Case(b, seed=26), lia, f"group {hq // hkv} prefill")
 
 
+@pytest.mark.parametrize("kv", [BF16, FP8])
+def test_maximum_context(lia, wl, kv):
+    """The reference's longest request (131,072 tokens, models/minicpm5.rs:15) decoding next to
+    a 4-row MTP sequence ending at the same length, plus a short one."""
+    g = wl.Geometry(kv_dtype=kv)
+    b = wl.custom([131072, 131072, 33], [1, 4, 1], geom=g, seed=27)
+    print(f"[case] maximum context kv={kv}", flush=True)
+    _check(G.Case(b, seed=27), lia, f"context 131072 kv={kv}")
+
+
 def test_repeat_calls_are_identical(lia, wl):
     b = wl.custom([5000, 17, 900], [1, 1, 3], seed=8)
     case = G.Case(b, seed=8)
