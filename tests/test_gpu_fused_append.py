@@ -90,6 +90,13 @@ def test_fused_prefill_chunks(lia, wl, hq, hkv):
     _check(G.Case(wl.custom(ctx, q, geom=g, seed=15), seed=15), lia, f"prefill hq={hq} hkv={hkv}", 15)
 
 
+@pytest.mark.parametrize("q_len", [[1, 0, 3, 0, 1], [0, 2, 0, 64, 0]])
+def test_fused_sequences_without_rows(lia, wl, q_len):
+    """Sequences adding no rows next to decode, MTP and prefill rows, through the fused launch."""
+    ctx = [500, 300, 1000 + 200, 64 + 64, 4097]
+    _check(G.Case(wl.custom(ctx, q_len, seed=18), seed=18), lia, f"no-row sequences {q_len}", 18)
+
+
 def test_fused_matches_unfused(lia, wl):
     """Same output as kv_append + partial + merge to within accumulation order."""
     b = wl.custom([5000, 17, 900, 64], [1, 1, 3, 64], seed=16)
