@@ -204,6 +204,30 @@ def test_maximum_context(lia, wl, kv):
     _check(G.Case(b, seed=27), lia, f"context 131072 kv={kv}")
 
 
+def test_capacity_does_not_change_results(lia, wl):
+    """A configuration sized for far more rows and sequences than the batch (a larger
+    workspace, more unit and record slots) gives bit-identical outputs."""
+    b = wl.custom([5000, 17, 900, 64, 300], [1, 1, 3, 64, 0], seed=28)
+    case = G.Case(b, seed=28)
+    dev = case.device()
+    g = b.geom
+    outs = []
+    for max_seqs, max_rows in ((b.n_seqs, b.n_rows), (64, 4096)):
+        cfg = lia.AttentionConfig(g.hq, g.hkv, g.d, g.page_size, b.pool_pages, b.stride, g.q_dtype,
+                                  g.kv_dtype, g.out_dtype, g.scale, max_seqs, max_rows, int(b.ctx.max()))
+        ws = torch.zeros(lia.workspace_bytes(cfg), dtype=torch.uint8, device="cuda")
+        out = torch.full((b.n_rows, g.hq, g.d), float("nan"), dtype=torch.bfloat16, device="cuda")
+        lia.paged_attention(cfg, b.n_seqs, dev["cu"], dev["positions"], dev["sequences"], dev["pages"],
+                            dev["q"], dev["kc"], dev["vc"], out, ws)
+        torch.cuda.synchronize()
+        outs.append(out.view(torch.int16).cpu().numpy())
+    print("[case] capacity", flush=True)
+    assert np.array_equal(outs[0], outs[1])
+    got = torch.from_numpy(outs[1]).view(torch.bfloat16).float().numpy()
+    mx, mean = G.errors(got, case.f64())
+    assert mx < 2e-2 and mean < 2e-3
+
+
 def test_repeat_calls_are_identical(lia, wl):
     b = wl.custom([5000, 17, 900], [1, 1, 3], seed=8)
     case = G.Case(b, seed=8)
