@@ -228,6 +228,34 @@ def test_capacity_does_not_change_results(lia, wl):
     assert mx < 2e-2 and mean < 2e-3
 
 
+@pytest.mark.parametrize("rows_kind", ["decode", "mixed"])
+def test_many_sequences(lia, wl, rows_kind):
+    """1,500 sequences: more than the 1,024 the plan keeps in LDS (its general path) and than
+    one packing workgroup covers; decode only, and mixed with sequences adding 0 or 3 rows."""
+    rng = np.random.default_rng(29)
+    n = 1500
+    q = np.ones(n, np.int64) if rows_kind == "decode" else rng.choice([0, 1, 1, 3], n)
+    ctx = rng.integers(1, 300, n) + q
+    b = wl.custom(ctx, q, seed=29)
+    print(f"[case] many sequences {rows_kind}: rows {b.n_rows}", flush=True)
+    P = b.geom.page_size
+    dev = {k: torch.full((b.n_rows,), -7, dtype=torch.int32, device="cuda")
+           for k in ("positions", "sequences", "slots")}
+    dev["cu"] = torch.full((n + 1,), -7, dtype=torch.int32, device="cuda")
+    status = torch.full((1,), -7, dtype=torch.int32, device="cuda")
+    lia.pack_device(G.u32_dev(np.arange(n)), G.u32_dev(b.q_len), G.u32_dev(b.cached),
+                    G.u32_dev(b.flat_table()), b.stride, P, b.pool_pages, b.stride * P, b.n_rows,
+                    dev["cu"], dev["positions"], dev["sequences"], dev["slots"], status)
+    torch.cuda.synchronize()
+    assert status.item() == 0
+    got = {k: v.cpu().numpy().view(np.uint32) for k, v in dev.items()}
+    assert np.array_equal(got["cu"], b.cu_seqlens())
+    assert np.array_equal(got["positions"], b.positions())
+    assert np.array_equal(got["sequences"], b.sequences())
+    assert np.array_equal(got["slots"], b.slot_mapping())
+    _check(G.Case(b, seed=29), lia, f"many sequences {rows_kind}")
+
+
 def test_repeat_calls_are_identical(lia, wl):
     b = wl.custom([5000, 17, 900], [1, 1, 3], seed=8)
     case = G.Case(b, seed=8)
