@@ -256,6 +256,21 @@ def test_many_sequences(lia, wl, rows_kind):
     _check(G.Case(b, seed=29), lia, f"many sequences {rows_kind}")
 
 
+@pytest.mark.parametrize("kv", [BF16, F16])
+def test_prefill_few_units_long_prefix(lia, wl, kv):
+    """A short chunk after a long prefix on the prefill kernel: one or two 128-column units per
+    KV head take every workgroup, so each unit leaves hundreds of split records and the
+    combine runs many record batches."""
+    g = wl.Geometry(kv_dtype=kv)
+    for ctx, q, seed in (([65536 + 32], [32], 30), ([30000 + 16, 20000 + 40], [16, 40], 31)):
+        got, ref = _check(G.Case(wl.custom(ctx, q, geom=g, seed=seed), seed=seed), lia,
+                          f"chunks {q} after {ctx} kv={kv}")
+        # averages over tens of thousands of keys are small: also within 2 % of their scale
+        scale = float(np.max(np.abs(ref)))
+        print(f"[case] max |ref| {scale:.3e}", flush=True)
+        assert np.max(np.abs(got - ref)) < 2e-2 * scale
+
+
 def test_repeat_calls_are_identical(lia, wl):
     b = wl.custom([5000, 17, 900], [1, 1, 3], seed=8)
     case = G.Case(b, seed=8)
