@@ -183,10 +183,10 @@ def test_large_pages(lia, wl, kv, page):
     _check(G.Case(b, seed=24), lia, f"pages of {page} kv={kv} prefill")
 
 
-@pytest.mark.parametrize("hq,hkv", [(32, 1), (24, 1), (64, 2)])
-def test_large_groups(lia, wl, hq, hkv):
-    """GQA groups of 24 and 32 (the largest accepted): two 16-column tiles hold one row, or
-    128 / group rows in a prefill unit."""
+@pytest.mark.parametrize("hq,hkv", [(32, 1), (24, 1), (64, 2), (16, 16), (16, 8), (32, 16)])
+def test_group_extremes(lia, wl, hq, hkv):
+    """GQA groups of 24 and 32 (the largest accepted: two 16-column tiles hold one row, or
+    128 / group rows in a prefill unit) and of 1 and 2 (8 and 16 KV heads: 8-16 rows per tile)."""
     g = wl.Geometry(hq=hq, hkv=hkv, d=128)
     b = wl.custom([1, 17, 700, 4100], [1, 1, 3, 1], geom=g, seed=25)
     _check(G.Case(b, seed=25), lia, f"group {hq // hkv} decode/MTP")
