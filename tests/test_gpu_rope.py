@@ -48,8 +48,13 @@ def _run(lia, O, hq, hkv, d, kv, qdt, page, use_slots, seed):
     if kv == FP8:
         k_scales = rng.uniform(0.005, 0.03, pool_pages * hkv).astype(np.float32)
         v_scales = rng.uniform(0.005, 0.03, pool_pages * hkv).astype(np.float32)
+        k_scales[rng.random(k_scales.size) < 0.3] = 0.0  # never quantised: take scale 1
+        v_scales[rng.random(v_scales.size) < 0.3] = 0.0
     qref = np.zeros(rows * hq * d, np.uint16 if qdt == BF16 else np.float32)
     kref, vref = kc.copy(), vc.copy()
+    # device copies first: the oracle records the scales of never-quantised pages in place
+    dks = G.to_dev(k_scales) if k_scales is not None else None
+    dvs = G.to_dev(v_scales) if v_scales is not None else None
     O.rope_kv_append(layout_o, hq, positions, seqs, flat, stride, coeffs, combined, qref, qdt, kref,
                      vref, slot_mapping=slots if use_slots else None, k_scales=k_scales,
                      v_scales=v_scales)
@@ -60,8 +65,7 @@ def _run(lia, O, hq, hkv, d, kv, qdt, page, use_slots, seed):
     kw = dict(slot_mapping=G.u32_dev(slots)) if use_slots else dict(
         positions=G.u32_dev(positions), sequences=G.u32_dev(seqs), pages=G.u32_dev(flat), stride=stride)
     lia.rope_kv_append(layout, hq, G.to_dev(coeffs), G.to_dev(combined), q, dkc, dvc,
-                       k_scales=G.to_dev(k_scales) if k_scales is not None else None,
-                       v_scales=G.to_dev(v_scales) if v_scales is not None else None, **kw)
+                       k_scales=dks, v_scales=dvs, **kw)
     torch.cuda.synchronize()
     qgot = q.view(torch.int16).cpu().numpy().view(np.uint16) if qdt == BF16 else q.cpu().numpy()
     if qdt == BF16:
@@ -70,6 +74,8 @@ def _run(lia, O, hq, hkv, d, kv, qdt, page, use_slots, seed):
         assert np.array_equal(qgot.reshape(-1).view(np.uint32), qref.view(np.uint32))
     assert np.array_equal(dkc.cpu().numpy().view(store), kref)
     assert np.array_equal(dvc.cpu().numpy().view(store), vref)
+    if kv == FP8:  # the oracle's arrays hold the recorded scales
+        assert np.array_equal(dks.cpu().numpy(), k_scales) and np.array_equal(dvs.cpu().numpy(), v_scales)
 
 
 def test_reference_geometry(lia, O):
