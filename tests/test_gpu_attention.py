@@ -271,6 +271,15 @@ def test_prefill_few_units_long_prefix(lia, wl, kv):
         assert np.max(np.abs(got - ref)) < 2e-2 * scale
 
 
+@pytest.mark.parametrize("d,q", [(128, 4), (64, 2), (128, 1)])
+def test_single_sequence_small_merge(lia, wl, d, q):
+    """One long sequence verifying a few draft rows (or decoding): the merge grid is small, so
+    each record row is merged by two workgroups, on the two-tile and the one-tile path."""
+    g = wl.Geometry(d=d, hq=16 if d == 128 else 8)
+    b = wl.custom([20000 + q], [q], geom=g, seed=32)
+    _check(G.Case(b, seed=32), lia, f"single sequence d={d} rows={q}")
+
+
 def test_repeat_calls_are_identical(lia, wl):
     b = wl.custom([5000, 17, 900], [1, 1, 3], seed=8)
     case = G.Case(b, seed=8)
