@@ -2013,13 +2013,16 @@ static int run_stages(int stages, const lia_attention_config *c, uint32_t n_seqs
         }
         dim3 grid(units_nt < L.max_units ? units_nt : L.max_units, cols);
         // a small merge (few units, as in a decode batch of a few long sequences) splits each
-        // record row over two workgroups: measured 0.6 us faster per layer at 128 workgroups,
-        // slower on grids of hundreds or thousands
-        const bool split = grid.x * grid.y < 256;
-        grid.z = split ? 2 : 1;
+        // record row over two workgroups (measured 0.6 us faster per layer at 128 workgroups,
+        // slower on grids of hundreds or thousands), and over four when units hold hundreds of
+        // records (one or two long sequences: a batch of 256 records per pass instead of 128)
+        const uint32_t per_unit = n_wg / (grid.x ? grid.x : 1); // records per unit, roughly
+        const uint32_t split = per_unit >= 128 ? 4 : grid.x * grid.y < 256 ? 2 : 1;
+        grid.z = split;
 #define LIA_COMBINE(DD, NN)                                                                      \
     do {                                                                                         \
-        if (split) hipLaunchKernelGGL((combine_kernel<DD, NN, 2>), grid, dim3(kCombineThreads), 0, s, p); \
+        if (split == 4) hipLaunchKernelGGL((combine_kernel<DD, NN, 4>), grid, dim3(kCombineThreads), 0, s, p); \
+        else if (split == 2) hipLaunchKernelGGL((combine_kernel<DD, NN, 2>), grid, dim3(kCombineThreads), 0, s, p); \
         else hipLaunchKernelGGL((combine_kernel<DD, NN, 1>), grid, dim3(kCombineThreads), 0, s, p);       \
     } while (0)
         const dim3 wgrid(grid.x, 16 * kWideNT / (4 * kWideCombineCols));
