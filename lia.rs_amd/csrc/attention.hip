@@ -947,13 +947,29 @@ __device__ __forceinline__ void append_rows(const AttnParams &p, uint32_t wg, ui
 
 // One column's split record: unnormalised O for this wave's d slice (SW dims), reference
 // max and mass.
-template <int D, int SW>
+// Record rows of 16-bit pools hold O / l in the pool's type (|O/l| <= max |V|, so the row is
+// in range; half the record traffic of f32); FP8 pools, whose values carry a page scale, keep
+// unnormalised f32 rows.
+template <int KVT>
+constexpr bool kRecord16 = KVT != LIA_FP8_E4M3;
+
+template <int D, int SW, int KVT>
 __device__ __forceinline__ void store_record(const AttnParams &p, size_t rb, const f32x4 (&o)[SW / 16],
                                              float m, float l, uint32_t wave) {
     const uint32_t g = lane_id() >> 4;
-    float *po = p.part_o + rb * D + SW * wave + 4 * g;
+    if constexpr (kRecord16<KVT>) {
+        uint16_t *po = (uint16_t *)p.part_o + rb * D + SW * wave + 4 * g;
+        const float inv = l > 0.0f ? 1.0f / l : 0.0f;
 #pragma unroll
-    for (int n = 0; n < SW / 16; n++) *(f32x4 *)(po + 16 * n) = o[n];
+        for (int n = 0; n < SW / 16; n++) {
+            const f32x4 v = o[n] * inv;
+            *(u32x2 *)(po + 16 * n) = u32x2{pack2<KVT == LIA_BF16>(v.x, v.y), pack2<KVT == LIA_BF16>(v.z, v.w)};
+        }
+    } else {
+        float *po = p.part_o + rb * D + SW * wave + 4 * g;
+#pragma unroll
+        for (int n = 0; n < SW / 16; n++) *(f32x4 *)(po + 16 * n) = o[n];
+    }
     if (wave == 0 && g == 0) {
         p.part_ml[rb * 2] = m;
         p.part_ml[rb * 2 + 1] = l;
@@ -1088,7 +1104,7 @@ __global__ __launch_bounds__(D / 32 * 64, kMinWavesPerEU) void attention_kernel(
                     }
                 }
             } else {
-                store_record<D, C::SW>(p, (size_t)rec * COLS + col, st.o[nt], st.m[nt], lt, wave);
+                store_record<D, C::SW, KVT>(p, (size_t)rec * COLS + col, st.o[nt], st.m[nt], lt, wave);
             }
         }
         lo = seg_end;
@@ -1518,7 +1534,8 @@ __device__ __forceinline__ float wave_max(float v) {
     return v;
 }
 
-template <int D, int NT, int SPLIT>
+// REC: record rows in f32 unnormalised (0), or normalised in f16 (1) or bf16 (2).
+template <int D, int NT, int SPLIT, int REC>
 __global__ __launch_bounds__(kCombineThreads) void combine_kernel(AttnParams p) {
     constexpr uint32_t QF = D / 4;                 // float4 quads per record row
     constexpr uint32_t Q = QF / SPLIT;             // quads of this workgroup's share (blockIdx.z)
@@ -1547,7 +1564,17 @@ __global__ __launch_bounds__(kCombineThreads) void combine_kernel(AttnParams p) 
             // a branch would each be waited for at the branch's join
             const uint32_t r = base + k * RPP + rg;
             const size_t rb = (size_t)(rec0 + min(r, n - 1)) * COLS + col;
-            o[k] = po[rb * QF + qoff + q];
+            if constexpr (REC == 0) {
+                o[k] = po[rb * QF + qoff + q];
+            } else {
+                const u32x2 h = ((const u32x2 *)p.part_o)[rb * QF + qoff + q];
+                if constexpr (REC == 2)
+                    o[k] = make_float4(bf16_to_f32(h.x & 0xffffu), bf16_to_f32(h.x >> 16),
+                                       bf16_to_f32(h.y & 0xffffu), bf16_to_f32(h.y >> 16));
+                else
+                    o[k] = make_float4(f16_to_f32(h.x & 0xffffu), f16_to_f32(h.x >> 16),
+                                       f16_to_f32(h.y & 0xffffu), f16_to_f32(h.y >> 16));
+            }
             const float2 ml = ((const float2 *)p.part_ml)[rb];
             m[k] = ml.x;
             l[k] = r < n ? ml.y : 0.0f;
@@ -1571,12 +1598,13 @@ __global__ __launch_bounds__(kCombineThreads) void combine_kernel(AttnParams p) 
         }
 #pragma unroll
         for (uint32_t k = 0; k < kCombinePasses; k++) {
-            const float w = l[k] > 0.0f ? fast_exp2(m[k] - M) : 0.0f;
+            // normalised rows weigh by their mass too
+            const float w = l[k] > 0.0f ? fast_exp2(m[k] - M) * (REC ? l[k] : 1.0f) : 0.0f;
             num.x = fmaf(w, o[k].x, num.x);
             num.y = fmaf(w, o[k].y, num.y);
             num.z = fmaf(w, o[k].z, num.z);
             num.w = fmaf(w, o[k].w, num.w);
-            den = fmaf(w, l[k], den);
+            den = REC ? den + w : fmaf(w, l[k], den);
         }
     }
     // record groups rg share the quad q: sum them (den likewise counts every record once)
@@ -1724,6 +1752,13 @@ constexpr uint32_t kWideNT = kWideNTDev;
 static inline uint32_t nt_for(uint32_t n_rows, uint32_t n_seqs, uint32_t group, int kv_dtype) {
     if (n_rows >= 16 * n_seqs && kv_dtype != LIA_FP8_E4M3 && group <= 32) return kWideNT;
     return (n_rows > n_seqs || group > 16) ? 2 : 1;
+}
+
+template <int D, int NT, int REC>
+static void launch_combine(uint32_t split, dim3 grid, const AttnParams &p, hipStream_t s) {
+    if (split == 4) hipLaunchKernelGGL((combine_kernel<D, NT, 4, REC>), grid, dim3(kCombineThreads), 0, s, p);
+    else if (split == 2) hipLaunchKernelGGL((combine_kernel<D, NT, 2, REC>), grid, dim3(kCombineThreads), 0, s, p);
+    else hipLaunchKernelGGL((combine_kernel<D, NT, 1, REC>), grid, dim3(kCombineThreads), 0, s, p);
 }
 
 static Layout layout_for(const lia_attention_config *c, uint32_t n_wg) {
@@ -2016,14 +2051,15 @@ static int run_stages(int stages, const lia_attention_config *c, uint32_t n_seqs
         // record row over two workgroups (measured 0.6 us faster per layer at 128 workgroups,
         // slower on grids of hundreds or thousands), and over four when units hold hundreds of
         // records (one or two long sequences: a batch of 256 records per pass instead of 128)
+        const int rec = c->kv_dtype == LIA_BF16 ? 2 : c->kv_dtype == LIA_F16 ? 1 : 0;
         const uint32_t per_unit = n_wg / (grid.x ? grid.x : 1); // records per unit, roughly
         const uint32_t split = per_unit >= 128 ? 4 : grid.x * grid.y < 256 ? 2 : 1;
         grid.z = split;
 #define LIA_COMBINE(DD, NN)                                                                      \
     do {                                                                                         \
-        if (split == 4) hipLaunchKernelGGL((combine_kernel<DD, NN, 4>), grid, dim3(kCombineThreads), 0, s, p); \
-        else if (split == 2) hipLaunchKernelGGL((combine_kernel<DD, NN, 2>), grid, dim3(kCombineThreads), 0, s, p); \
-        else hipLaunchKernelGGL((combine_kernel<DD, NN, 1>), grid, dim3(kCombineThreads), 0, s, p);       \
+        if (rec == 1) launch_combine<DD, NN, 1>(split, grid, p, s);                               \
+        else if (rec == 2) launch_combine<DD, NN, 2>(split, grid, p, s);                          \
+        else launch_combine<DD, NN, 0>(split, grid, p, s);                                        \
     } while (0)
         const dim3 wgrid(grid.x, 16 * kWideNT / (4 * kWideCombineCols));
         if (c->head_dim == 128) {
