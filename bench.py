@@ -51,24 +51,7 @@ def parse():
     ap.add_argument("--config", type=int, default=2, choices=(2, 3, 4, 5),
                     help="3, 4 or 5: time one layer of that BASELINE configuration's attention "
                          "(a parity workload, not the headline line) and print its own JSON line")
-    ap.add_argument("--stream-probe", action="store_true",
-                    help="only run the streaming-rate probe on the config-2 pool shape: the read "
-                         "ceiling of the kernel's page pattern and of other load mappings")
-    ap.add_argument("--copy-calibration", type=int, default=0, metavar="MIB",
-                    help="only run device copies of MIB MiB (the counter calibration kernel)")
     return ap.parse_args()
-
-
-def copy_calibration(mib):
-    """A plain device-to-device copy of known size, for scaling the FETCH_SIZE / WRITE_SIZE
-    counters: 5 copies of `mib` MiB (each reads and writes mib MiB)."""
-    import torch
-    src = torch.ones(mib << 18, dtype=torch.float32, device="cuda")
-    dst = torch.empty_like(src)
-    for _ in range(5):
-        dst.copy_(src)
-    torch.cuda.synchronize()
-    log(f"copied {mib} MiB x 5")
 
 
 def load_traffic(path, kernel_us, layer_bytes):
@@ -184,36 +167,40 @@ def side_config(args):
     }), flush=True)
 
 
-def stream_probe(args):
-    """The probe program built beside the library (csrc/stream_probe.hip), run on the
-    config-2 pool shape: pages of 16 tokens, 2 KV heads, head_dim 128, the seed's contexts,
-    8 pool copies rotated so no launch reads cache-resident data.  Prints its JSON lines."""
-    import subprocess
-    from __graft_entry__ import package
-    package()
-    import lia_rs_amd.workloads as wl
-    b = wl.config2(seed=args.seed, layers=1)
-    g = b.geom
-    exe = os.path.join(ROOT, "lia.rs_amd", "stream_probe")
-    if not os.path.exists(exe):
-        raise SystemExit("stream_probe is not built (run __graft_entry__.build())")
-    cmd = [exe, str(g.page_size), str(g.hkv), str(g.d), "8", *[str(int(c)) for c in b.ctx]]
-    log("running " + " ".join(cmd))
-    r = subprocess.run(cmd, stdout=subprocess.PIPE, timeout=300)
-    sys.stdout.write(r.stdout.decode())
-    sys.stdout.flush()
-    if r.returncode:
-        raise SystemExit(f"stream_probe exited with {r.returncode}")
+def cpu_baseline(args, b, g, kpool, vpool, q, layer_bytes, L):
+    """The oracle's scalar split-K + merge (kernels/llama.rs:63-159, 201-290) on one layer of
+    the batch, compiled here at -O3 -march=native with OpenMP over (row, head, split): one
+    warm-up run, then at least 5 timed runs (more until args.cpu_seconds), median reported."""
+    import tempfile
+    import torch
+    from oracle import build as OB
+    from oracle import oracle as O
+    path = OB.build_baseline(os.path.join(tempfile.mkdtemp(prefix="lia_cpu_"), "baseline.so"))
+    blib = O.baseline_lib(path)
+    kc = kpool.view(torch.int16).cpu().numpy().view(np.uint16).reshape(-1)
+    vc = vpool.view(torch.int16).cpu().numpy().view(np.uint16).reshape(-1)
+    q32 = q.float().cpu().numpy()
+    geom = O.geom(g.hq, g.hkv, g.d, g.page_size, b.stride, g.kv_dtype, g.scale)
+    pos_h, seq_h, flat_h = b.positions(), b.sequences(), b.flat_table()
+    run = lambda: O.paged_attention_f32(geom, pos_h, seq_h, flat_h, q32, kc, vc, span=256, lib_=blib)
+    run()  # warm-up
+    times, t_start = [], time.perf_counter()
+    while len(times) < 5 or (time.perf_counter() - t_start < args.cpu_seconds and len(times) < 4 * L):
+        t0 = time.perf_counter()
+        run()
+        times.append(time.perf_counter() - t0)
+    per_layer = float(np.median(times))
+    threads = int(blib.lo_omp_threads())
+    return {"value": round(b.n_rows / (per_layer * L), 4), "unit": "tokens/s",
+            "cores": threads, "kind": "port",
+            "sample": f"median of {len(times)} runs (after 1 warm-up) of one layer of the config-2 "
+                      f"batch (8 rows, sum ctx {int(b.ctx.sum())}) in f32 split-K (span 256) + merge, "
+                      f"gcc -O3 -march=native, OpenMP {threads} threads, scaled to {L} layers; "
+                      f"{per_layer * 1e3:.1f} ms/layer, {layer_bytes / per_layer / 1e9:.2f} GB/s"}
 
 
 def main():
     args = parse()
-    if args.stream_probe:
-        stream_probe(args)
-        return
-    if args.copy_calibration:
-        copy_calibration(args.copy_calibration)
-        return
     if args.config != 2:
         side_config(args)
         return
@@ -330,27 +317,7 @@ def main():
     # ---- the reference algorithm on the host cores (bounded sample, one layer repeated)
     cpu = None
     if not args.no_cpu:
-        from oracle import oracle as O
-        kc = kpool[0].view(torch.int16).cpu().numpy().view(np.uint16).reshape(-1)
-        vc = vpool[0].view(torch.int16).cpu().numpy().view(np.uint16).reshape(-1)
-        q32 = qs[0].float().cpu().numpy()
-        geom = O.geom(g.hq, g.hkv, g.d, P, b.stride, g.kv_dtype, g.scale)
-        pos_h, seq_h, flat_h = b.positions(), b.sequences(), b.flat_table()
-        reps, t0 = 0, time.perf_counter()
-        while True:
-            O.paged_attention_f32(geom, pos_h, seq_h, flat_h, q32, kc, vc, span=256)
-            reps += 1
-            el = time.perf_counter() - t0
-            if el >= args.cpu_seconds or reps >= 4 * L:
-                break
-        per_layer = el / reps
-        threads = int(os.environ.get("OMP_NUM_THREADS", os.cpu_count() or 1))
-        cpu = {"value": round(b.n_rows / (per_layer * L), 4), "unit": "tokens/s",
-               "cores": threads, "kind": "port",
-               "sample": f"{reps} x one layer of the config-2 batch (8 rows, sum ctx "
-                         f"{int(b.ctx.sum())}) in f32 split-K (span 256) + merge, "
-                         f"scaled to {L} layers; {per_layer * 1e3:.1f} ms/layer, "
-                         f"{layer_bytes / per_layer / 1e9:.2f} GB/s"}
+        cpu = cpu_baseline(args, b, g, kpool[0], vpool[0], qs[0], layer_bytes, L)
         log(f"cpu baseline: {cpu}")
 
     out = {

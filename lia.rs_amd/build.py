@@ -14,8 +14,6 @@ OBJ = os.path.join(HERE, "_build")
 OUT = os.path.join(HERE, "liblia_hip.so")
 HIPCC = os.environ.get("HIPCC", "/opt/rocm/bin/hipcc")
 SOURCES = ["attention.hip", "kv.hip", "transfer.hip", "sampling.hip", "host.cpp", "page_cache.cpp"]
-# stand-alone measurement programs (not linked into the library): csrc/<name>.hip -> <name>
-TOOLS = ["stream_probe"]
 DEVICE_FLAGS = ["--offload-arch=gfx950", "-Xclang", "-target-feature", "-Xclang", "-packed-fp32-ops"]
 COMMON = ["-O3", "-fPIC", "-std=c++17", "-Wall", "-Wno-unused-result"]
 
@@ -50,17 +48,6 @@ def build(verbose: bool = False) -> str:
     if verbose:
         print(" ".join(cmd), flush=True)
     subprocess.run(cmd, check=True)
-    for tool in TOOLS:
-        cmd = [HIPCC, *COMMON, *DEVICE_FLAGS, os.path.join(CSRC, tool + ".hip"), "-o", os.path.join(HERE, tool)]
-        if verbose:
-            print(" ".join(cmd), flush=True)
-        r = subprocess.run(cmd, stdout=subprocess.PIPE, stderr=subprocess.STDOUT)
-        text = "\n".join(line for line in r.stdout.decode(errors="replace").splitlines()
-                         if "packed-fp32-ops" not in line)
-        if text.strip():
-            print(text, file=sys.stderr)
-        if r.returncode != 0:
-            raise RuntimeError(f"{tool} build failed")
     return OUT
 
 

@@ -55,10 +55,6 @@ __device__ __forceinline__ uint32_t unit_head(const UnitDesc &u) { return u.nrow
 // the range's first unit and the physical pages of the first four logical pages the range
 // reads, so a workgroup issues its first K/V loads one dependent load after launch.
 constexpr uint32_t kPrePages = 4;
-#ifndef LIA_XCD_MAJOR
-#define LIA_XCD_MAJOR 1
-#endif
-constexpr bool kXcdMajor = LIA_XCD_MAJOR;
 struct WorkDesc {
     uint32_t unit;            // first unit of the range
     uint32_t lo, hi;          // block range [lo, hi)
@@ -257,7 +253,7 @@ __device__ void plan_lds(uint32_t n_seqs, const uint32_t *cu, const uint32_t *po
         merge[u] = m;
     }
     auto range_lo = [&](uint32_t w) { return (uint32_t)((uint64_t)w * B / N); };
-    const bool xcd_major = kXcdMajor && N == n_wg && N % 8 == 0;
+    const bool xcd_major = N == n_wg && N % 8 == 0;
     const uint32_t per = N / 8;
     // Work descriptors four at a time, so the page-table reads of all four are in flight
     // together (unconditional loads: an entry not needed reads cu[0] and is replaced by 0).
@@ -401,7 +397,7 @@ __global__ __launch_bounds__(256) void plan_kernel(uint32_t n_seqs, const uint32
     // Range r of the flat block order runs on workgroup (r % per) * 8 + r / per, so the
     // workgroups of one XCD (workgroup i runs on XCD i % 8) take contiguous ranges and share
     // the keys of neighbouring units in their L2.  Records are indexed by range.
-    const bool xcd_major = kXcdMajor && N == n_wg && N % 8 == 0;
+    const bool xcd_major = N == n_wg && N % 8 == 0;
     const uint32_t per = N / 8;
     for (uint32_t w = t; w < N; w += 256) {
         const uint32_t r = xcd_major ? (w % 8) * per + w / 8 : w;
@@ -448,19 +444,9 @@ __global__ __launch_bounds__(256) void plan_kernel(uint32_t n_seqs, const uint32
 // therefore split evenly whatever the segment lengths, and no end-of-segment merge is
 // needed: each wave writes its own slice of the output or of the split record.
 
-// Dims per wave of a 16-bit pool (64: a wave reads whole 128-byte lines of a token; 32
-// halves the lines).  Cache policy of the K/V loads per pool type: 2 (non-temporal) on
-// 16-bit pools, where each wave reads whole lines, 0 on FP8 pools, whose 64-byte slices
+// Cache policy of the K/V loads per pool type: 2 (non-temporal) on 16-bit pools, where
+// each wave reads whole 128-byte lines of a token, 0 on FP8 pools, whose 64-byte slices
 // share a line between two waves.
-#ifndef LIA_SW16
-#define LIA_SW16 64
-#endif
-#ifndef LIA_KV_AUX
-#define LIA_KV_AUX 2
-#endif
-#ifndef LIA_KV_AUX_FP8
-#define LIA_KV_AUX_FP8 0
-#endif
 
 template <int D, int KVT>
 struct Cfg {
@@ -471,8 +457,8 @@ struct Cfg {
     // token, two loads per tile), 64 dims of an FP8 pool (64 bytes).  A lane loads 16
     // contiguous bytes of a token per 16-token tile and load (its A-operand k slots), so
     // every load instruction reads 16 tokens x 64 bytes.
-    static constexpr int SW = FP8 ? 64 : (LIA_SW16 < D ? LIA_SW16 : D);
-    static constexpr int AUX = FP8 ? LIA_KV_AUX_FP8 : LIA_KV_AUX; // cache policy of the K/V loads
+    static constexpr int SW = 64;
+    static constexpr int AUX = FP8 ? 0 : 2; // cache policy of the K/V loads
     static constexpr int WAVES = D / SW;            // one wave per slice
     static constexpr int KS = SW / 32;              // k-steps of S^T = K Q^T per tile
     static constexpr int DTW = SW / 16;             // 16-dim tiles of O per wave
@@ -485,20 +471,10 @@ struct Cfg {
     static constexpr int NV = FP8 ? 2 : 32 / VRPI;  // V loads per chunk
 };
 
-// Staged V rows hold 32 16-bit values (4 chunks of 16 bytes); chunk c of row r sits in
-// slot c ^ swz(r), which keeps the transpose reads of a 16-lane group (rows 4q..4q+3,
-// chunks {2n, 2n+1}) on distinct banks.
-__device__ __forceinline__ uint32_t swz(uint32_t row) { return 2 * ((row >> 1) & 1); }
-
-// Swizzle of a staged V row of SW 16-bit values: 32-value rows as above; 64-value rows
-// (128 bytes) flip the chunk pair by row bit 2, so rows r and r + 4 of a transpose read (the
-// same banks otherwise) land on distinct banks.
-template <int SW>
-__device__ __forceinline__ uint32_t vswz(uint32_t row) {
-    if constexpr (SW == 32) return swz(row);
-    else if constexpr (SW == 64) return 2 * ((row >> 2) & 1);
-    else return 2 * (row & 7); // 256-byte rows: the 8 rows of a transpose read on distinct banks
-}
+// Staged V rows hold 64 16-bit values (8 chunks of 16 bytes); chunk c of row r sits in slot
+// c ^ vswz(r), which flips the chunk pair by row bit 2 so rows r and r + 4 of a transpose
+// read (the same banks otherwise) land on distinct banks.
+__device__ __forceinline__ uint32_t vswz(uint32_t row) { return 2 * ((row >> 2) & 1); }
 
 template <int D, int KVT>
 struct Chunk {
@@ -657,7 +633,7 @@ __device__ __forceinline__ void load_chunk(const AttnParams &p, Chunk<D, KVT> &c
             const __amdgpu_buffer_rsrc_t vr =
                 make_rsrc(vbase + (size_t)tp.page[j] * P * row_bytes, tp.live[j] * row_bytes);
             const uint32_t row = C::VRPI * s + lane / C::CPR;
-            const uint32_t chunk = (lane % C::CPR) ^ vswz<C::SW>(row);
+            const uint32_t chunk = (lane % C::CPR) ^ vswz(row);
             const uint32_t off = (((t + 16 * j) & (P - 1)) + (row & 15)) * row_bytes + slice_off + 16 * chunk;
             auto *dst = (__attribute__((address_space(3))) void *)(stage + s * 512);
             if constexpr (C::AUX == 2)
@@ -731,8 +707,8 @@ __device__ __forceinline__ void compute_chunk(const AttnParams &p, const Chunk<D
             const u32x2 a = e4m3x4_to_f16x4_scaled(c.v[j].x), b = e4m3x4_to_f16x4_scaled(c.v[j].y);
             const u32x2 e = e4m3x4_to_f16x4_scaled(c.v[j].z), f = e4m3x4_to_f16x4_scaled(c.v[j].w);
             uint16_t *dst = stage + row * C::SW;
-            *(u32x4 *)(dst + ((c0 ^ vswz<C::SW>(row)) * 8)) = u32x4{a.x, a.y, b.x, b.y};
-            *(u32x4 *)(dst + (((c0 + 1) ^ vswz<C::SW>(row)) * 8)) = u32x4{e.x, e.y, f.x, f.y};
+            *(u32x4 *)(dst + ((c0 ^ vswz(row)) * 8)) = u32x4{a.x, a.y, b.x, b.y};
+            *(u32x4 *)(dst + (((c0 + 1) ^ vswz(row)) * 8)) = u32x4{e.x, e.y, f.x, f.y};
         }
     } else {
         wait_vmcnt<VW>(); // this chunk's V is in LDS (VW = memory ops issued after its loads)
@@ -825,7 +801,7 @@ __device__ __forceinline__ void compute_chunk(const AttnParams &p, const Chunk<D
             // V^T operand: d rows 16n .. 16n+15 of the slice, k slots = tokens
             // {4g..4g+3, 16+4g..16+4g+3} (transpose reads of the staged rows).
             const uint32_t row0 = 4 * g + li / 4, ch = 2 * n + ((li & 3) >> 1);
-            const uint16_t *r0 = stage + row0 * C::SW + ((ch ^ vswz<C::SW>(row0)) * 8) + (li & 1) * 4;
+            const uint16_t *r0 = stage + row0 * C::SW + ((ch ^ vswz(row0)) * 8) + (li & 1) * 4;
             const uint16_t *r1 = r0 + 16 * C::SW; // row0 + 16 has the same swizzle
             s16x4 a0 = __builtin_amdgcn_ds_read_tr16_b64_v4i16(
                 (__attribute__((address_space(3))) s16x4 *)(r0));
@@ -978,10 +954,7 @@ __device__ __forceinline__ void store_record(const AttnParams &p, size_t rb, con
 
 // At most 6 (16-bit pools) or 8 (FP8) decode waves run per CU, under 2 per SIMD, so the
 // kernel may use the registers of 3 waves per SIMD (168) instead of squeezing into 4's (128).
-#ifndef LIA_MIN_WAVES_EU
-#define LIA_MIN_WAVES_EU 3
-#endif
-constexpr int kMinWavesPerEU = LIA_MIN_WAVES_EU;
+constexpr int kMinWavesPerEU = 3;
 
 // The workgroup-size bound (D/32 waves) is looser than the D/SW waves launched: the
 // exact bound changes register allocation and measured 1 % slower on a batch-8 bf16 decode.
@@ -1132,16 +1105,10 @@ __global__ __launch_bounds__(D / 32 * 64, kMinWavesPerEU) void attention_kernel(
 // i - 1, whose stage then receives chunk i + 2.  Work units, block ranges, the two key runs
 // (cached keys, this step's keys), the fused append and the split records are the decode
 // kernel's; records hold 128 columns.
-#ifndef LIA_WIDE_WAVES
-#define LIA_WIDE_WAVES 8
-#endif
-#ifndef LIA_WIDE_NTW
-#define LIA_WIDE_NTW 1
-#endif
 template <int D>
 struct WCfg {
-    static constexpr int WAVES = LIA_WIDE_WAVES;
-    static constexpr int NTW = LIA_WIDE_NTW;    // 16-column tiles per wave
+    static constexpr int WAVES = 8;
+    static constexpr int NTW = 1;               // 16-column tiles per wave
     static constexpr int THREADS = 64 * WAVES;
     static constexpr int COLS = 16 * NTW * WAVES;
     static constexpr int ROWB = 2 * D;          // bytes of one token's head (16-bit KV)
@@ -1380,7 +1347,7 @@ __device__ __forceinline__ void wide_range(const AttnParams &p, const uint8_t *k
 }
 
 template <int D, int KVT>
-__global__ __launch_bounds__(64 * LIA_WIDE_WAVES, LIA_WIDE_NTW == 2 ? 2 : 4) void wide_kernel(AttnParams p) {
+__global__ __launch_bounds__(512, 4) void wide_kernel(AttnParams p) {
     using W = WCfg<D>;
     constexpr uint32_t COLS = W::COLS;
     __shared__ __attribute__((aligned(16))) uint16_t k0[W::STAGE], k1[W::STAGE], k2[W::STAGE];
@@ -1520,13 +1487,7 @@ __global__ __launch_bounds__(64 * LIA_WIDE_WAVES, LIA_WIDE_NTW == 2 ? 2 : 4) voi
 // the record groups are summed through LDS at the end.
 constexpr uint32_t kCombineThreads = 256;
 constexpr uint32_t kCombinePasses = 8;
-#ifndef LIA_WIDE_WAVES
-#define LIA_WIDE_WAVES 8
-#endif
-#ifndef LIA_WIDE_NTW
-#define LIA_WIDE_NTW 1
-#endif
-constexpr uint32_t kWideNTDev = LIA_WIDE_NTW * LIA_WIDE_WAVES; // column tiles of a prefill unit
+constexpr uint32_t kWideNTDev = 8; // column tiles of a prefill unit (one per wave)
 
 __device__ __forceinline__ float wave_max(float v) {
 #pragma unroll
@@ -1635,10 +1596,7 @@ __global__ __launch_bounds__(kCombineThreads) void combine_kernel(AttnParams p) 
 // record's row as float4 quads (64 / (D/4) records per pass); the record groups are summed
 // with lane shuffles.  Same merge rule as combine_kernel.
 // Columns merged by one wave of combine_wide_kernel, and record passes loaded per batch.
-#ifndef LIA_WCC
-#define LIA_WCC 4
-#endif
-constexpr uint32_t kWideCombineCols = LIA_WCC;
+constexpr uint32_t kWideCombineCols = 4;
 constexpr uint32_t kWideCombinePasses = 2;
 
 template <int D, bool BF>
@@ -1811,30 +1769,15 @@ extern "C" uint32_t lia_device_cus(void) {
     return g_cus;
 }
 
-// Workgroups per CU: at most kMaxPerCU resident ones, times kOversub / 2 launched (an
-// oversubscribed grid lets the dispatcher hand later workgroups to whichever CU frees up).
-#ifndef LIA_MAX_WG_PER_CU
-#define LIA_MAX_WG_PER_CU 3
-#endif
-#ifndef LIA_WG_OVERSUB2
-#define LIA_WG_OVERSUB2 2
-#endif
-constexpr uint32_t kMaxPerCU = LIA_MAX_WG_PER_CU;
-constexpr uint32_t kOversub2 = LIA_WG_OVERSUB2;
-// Decode kernel: at most this many waves per CU (three 2-wave workgroups measured best on
-// 16-bit pools at head_dim 128, four 2-wave workgroups on FP8 pools).  Fewer, longer
-// splits also shrink the combine.
-#ifndef LIA_MAX_WAVES
-#define LIA_MAX_WAVES 6
-#endif
-constexpr uint32_t kMaxWavesPerCU = LIA_MAX_WAVES;
-#ifndef LIA_MAX_WAVES_FP8
-#define LIA_MAX_WAVES_FP8 8
-#endif
-constexpr uint32_t kMaxWavesPerCU8 = LIA_MAX_WAVES_FP8;
+// Prefill kernel: resident 8-wave workgroups per CU at most.  Decode kernel: at most this
+// many waves per CU (three 2-wave workgroups measured best on 16-bit pools at head_dim 128,
+// four 2-wave workgroups on FP8 pools).  Fewer, longer splits also shrink the combine.
+constexpr uint32_t kMaxPerCU = 3;
+constexpr uint32_t kMaxWavesPerCU = 6;
+constexpr uint32_t kMaxWavesPerCU8 = 8;
 static uint32_t max_waves(int kv) { return kv == LIA_FP8_E4M3 ? kMaxWavesPerCU8 : kMaxWavesPerCU; }
 
-static uint32_t decode_waves(uint32_t d, int kv) { return kv == LIA_FP8_E4M3 ? d / 64 : (d > LIA_SW16 ? d / LIA_SW16 : 1); }
+static uint32_t decode_waves(uint32_t d, int) { return d / 64; } // one wave per 64-dim slice
 
 // Resident workgroups per CU allowed for a launch of NT column tiles.
 static uint32_t max_per_cu(uint32_t d, uint32_t nt, int kv) {
@@ -1847,7 +1790,7 @@ static uint32_t max_workgroups(const lia_attention_config *c) {
     uint32_t cus = lia_device_cus();
     if (!cus) cus = 256;
     const uint32_t per = max(kMaxPerCU, max_waves(c->kv_dtype) / decode_waves(c->head_dim, c->kv_dtype));
-    return cus * per * kOversub2 / 2;
+    return cus * per;
 }
 
 template <int D, int NT, int KVT>
@@ -1902,7 +1845,7 @@ static uint32_t workgroups_for(const lia_attention_config *c, uint32_t nt) {
                             : (nt == 1 ? resident_kv<64, 1>(kv)
                                : nt == 2 ? resident_kv<64, 2>(kv) : resident_kv<64, kWideNT>(kv));
     if (per > max_per_cu(d, nt, kv)) per = max_per_cu(d, nt, kv);
-    uint32_t n = cus * per * kOversub2 / 2;
+    uint32_t n = cus * per;
     uint32_t cap = max_workgroups(c);
     return n < cap ? n : cap;
 }

@@ -26,10 +26,15 @@
  *                                          float64 check pins the steps): the bits of the
  *                                          reference's device math are parity unpinned
  *   lo_rope_kv_append ................... pinned (equals lo_rotary_cache on the reference
- *                                          geometry; equals rope + lo_kv_append elsewhere)
+ *                                          geometry; equals rope + lo_kv_append elsewhere);
+ *                                          the rotation by mathematics: position 0 is the
+ *                                          identity, pair norms are kept, basis vectors map
+ *                                          to the rotate-half (cos, sin) columns, and q.k
+ *                                          depends only on the position difference
  *   exp bits (ex2.approx in the reference) parity unpinned, tolerance-pinned only
  */
 #include <math.h>
+#include <omp.h>
 #include <stdint.h>
 #include <stdlib.h>
 #include <string.h>
@@ -470,6 +475,17 @@ void lo_paged_attention_f32(const lo_geom *g, uint32_t rows, uint32_t span,
         partial_one(g, r, h, p, span, positions, sequences, pages, q, kc, vc, k_scales, v_scales, record);
     }
     lo_merge(g->hq, g->d, 0, rows, maxparts, work, out);
+}
+
+/* OpenMP threads a parallel region of this library uses (reported with the CPU baseline). */
+int lo_omp_threads(void) {
+    int n = 1;
+#pragma omp parallel
+    {
+#pragma omp single
+        n = omp_get_num_threads();
+    }
+    return n;
 }
 
 /* ------------------------------------------------------------------------------------ */

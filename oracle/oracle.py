@@ -200,16 +200,24 @@ def merge(hq, d, query_start, queries, parts, partial, out):
     lib().lo_merge(hq, d, query_start, queries, parts, ptr(partial), ptr(out))
 
 
+def baseline_lib(path):
+    """The oracle built by build.build_baseline (-O3 -march=native) for timing on this host."""
+    b = C.CDLL(path)
+    b.lo_omp_threads.restype = C.c_int
+    return b
+
+
 def paged_attention_f32(g, positions, sequences, pages, q, kc, vc, span=256, k_scales=None,
-                        v_scales=None):
-    """Split-K scalar attention + merge over every row (the CPU baseline)."""
+                        v_scales=None, lib_=None):
+    """Split-K scalar attention + merge over every row (the CPU baseline); lib_ selects a
+    build of the oracle other than the checker's (baseline_lib)."""
     positions, sequences, pages = u32(positions), u32(sequences), u32(pages)
     q = np.ascontiguousarray(q, dtype=np.float32)
     rows = positions.size
     maxparts = int((positions.max() + span) // span) if rows else 1
     work = np.zeros(rows * g.hq * maxparts * (g.d + 2), np.float32)
     out = np.zeros((rows, g.hq, g.d), np.float32)
-    lib().lo_paged_attention_f32(C.byref(g), rows, span, ptr(positions), ptr(sequences), ptr(pages),
+    (lib_ or lib()).lo_paged_attention_f32(C.byref(g), rows, span, ptr(positions), ptr(sequences), ptr(pages),
                                  ptr(q), ptr(kc), ptr(vc), ptr(k_scales), ptr(v_scales), ptr(work),
                                  C.c_size_t(work.size), ptr(out))
     return out

@@ -507,3 +507,104 @@ def test_rope_coefficients_generalise_the_reference_table(O):
     angle = (positions[:, None].astype(np.float32) * inv[None, :]).astype(np.float32)
     assert np.array_equal(got[:, :, 0], np.cos(angle.astype(np.float64)).astype(np.float32))
     assert np.array_equal(got[:, :, 1], np.sin(angle.astype(np.float64)).astype(np.float32))
+
+
+# ------------------------------------------------------------------ RoPE: the mathematics
+#
+# The checks above compare the fused and separate restatements with each other.  These pin
+# the rotation itself with facts the mathematics fixes, independently of the oracle's
+# formula: a rotation by angle 0 is the identity, a rotation keeps each (i, i + d/2) pair's
+# length, rotating basis vectors gives (cos, sin) columns at exactly the "rotate half"
+# positions with the reference's signs (src/gpu/kernels/llama.rs:33-60: lane i < d/2 pairs
+# with i + d/2 and takes -sin), and the dot product of a rotated query and key depends only
+# on the distance between their positions.
+
+def _rope_all(O, positions, x, d, hq=1):
+    """Rotate rows x[rows][hq][d] (queries) with the generalised restatement; f32 output."""
+    positions = np.asarray(positions, np.uint32)
+    rows = positions.size
+    hkv = 1
+    combined = np.zeros((rows, hq + 2 * hkv, d), np.float32)
+    combined[:, :hq] = x
+    coeffs = O.rope_coefficients(positions, d)
+    layout = O.KVLayout(hkv, d, 16, rows, F16)
+    qout = np.zeros(rows * hq * d, np.float32)
+    kc = np.zeros(rows * 16 * hkv * d, np.uint16)
+    O.rope_kv_append(layout, hq, positions, np.zeros(rows, np.uint32),
+                     np.arange(rows, dtype=np.uint32), 1, coeffs, combined.reshape(rows, -1), qout,
+                     F32, kc, np.zeros_like(kc), slot_mapping=np.arange(rows, dtype=np.uint32) * 16)
+    return qout.reshape(rows, hq, d)
+
+
+@pytest.mark.parametrize("d", [64, 128])
+def test_rope_position_zero_is_identity(O, d):
+    rng = np.random.default_rng(d)
+    x = rng.standard_normal((4, 3, d)).astype(np.float32) * 10
+    x[0, 0, :4] = [0.0, -0.0, np.float32(1e-30), np.float32(-3e38)]
+    got = _rope_all(O, np.zeros(4, np.uint32), x, d, hq=3)
+    # bit-equal; a zero may change sign (x*1 - y*0 is -0 + +0 = +0 for x = -0, y < 0)
+    nz = x != 0
+    assert np.array_equal(got[nz].view(np.uint32), x[nz].view(np.uint32))
+    assert np.all(got[~nz] == 0)
+    if d == 128:  # the reference-geometry restatement (16 heads x 128 dims)
+        q = rng.standard_normal(2 * 16 * 128).astype(np.float32)
+        assert np.array_equal(O.rope(16, np.zeros(2, np.uint32), q).view(np.uint32), q.view(np.uint32))
+
+
+@pytest.mark.parametrize("d", [64, 128])
+def test_rope_basis_vectors_rotate_half(O, d):
+    """e_i -> cos(a_i) e_i + sin(a_i) e_{i+d/2};  e_{i+d/2} -> -sin(a_i) e_i + cos(a_i) e_{i+d/2},
+    with a_i = f32(pos * f32(1 / f32(5e6^(2i/d)))) evaluated here in numpy."""
+    half = d // 2
+    positions = np.array([1, 7, 1000, 131071], np.uint32)
+    x = np.zeros((positions.size, d, d), np.float32)
+    for i in range(d):
+        x[:, i, i] = 1.0
+    got = _rope_all(O, positions, x, d, hq=d)  # head h holds the basis vector e_h
+    e = (np.float32(2.0) * np.arange(half, dtype=np.float32)) / np.float32(d)
+    inv = np.float32(1.0) / np.power(np.float64(5e6), e.astype(np.float64)).astype(np.float32)
+    ang = (positions[:, None].astype(np.float32) * inv[None, :]).astype(np.float32)
+    c = np.cos(ang.astype(np.float64)).astype(np.float32)
+    s = np.sin(ang.astype(np.float64)).astype(np.float32)
+    for r in range(positions.size):
+        m = got[r]  # m[h] = rotation of e_h
+        want = np.zeros((d, d), np.float32)
+        for i in range(half):
+            want[i, i], want[i, i + half] = c[r, i], s[r, i]
+            want[i + half, i], want[i + half, i + half] = -s[r, i], c[r, i]
+        assert np.array_equal(m, want), f"position {positions[r]}"
+
+
+@pytest.mark.parametrize("d", [64, 128])
+def test_rope_preserves_pair_norms(O, d):
+    half = d // 2
+    rng = np.random.default_rng(5 + d)
+    positions = rng.integers(0, 131072, 64).astype(np.uint32)
+    x = rng.standard_normal((64, 2, d)).astype(np.float32)
+    got = _rope_all(O, positions, x, d, hq=2).astype(np.float64)
+    x64 = x.astype(np.float64)
+    n0 = np.hypot(x64[..., :half], x64[..., half:])
+    n1 = np.hypot(got[..., :half], got[..., half:])
+    # f32 cos/sin (cos^2 + sin^2 = 1 within ~2^-23), two rounded products and an fma
+    assert np.all(np.abs(n1 - n0) <= 8 * 2.0 ** -24 * n0 + 1e-37)
+
+
+@pytest.mark.parametrize("d", [64, 128])
+def test_rope_scores_depend_on_relative_position(O, d):
+    """<R(q, m), R(k, n)> = <R(q, m + s), R(k, n + s)> (f64 dot products of the f32 results).
+    Positions stay small so the f32 angles keep a phase error well under 1e-6."""
+    rng = np.random.default_rng(9 + d)
+    q = rng.standard_normal((1, 1, d)).astype(np.float32)
+    k = rng.standard_normal((1, 1, d)).astype(np.float32)
+    scale = float(np.linalg.norm(q) * np.linalg.norm(k))
+    for m, n in [(0, 0), (3, 0), (0, 5), (17, 9), (31, 32)]:
+        base = None
+        for shift in (0, 1, 8, 21):
+            rq = _rope_all(O, [m + shift], q, d)[0, 0].astype(np.float64)
+            rk = _rope_all(O, [n + shift], k, d)[0, 0].astype(np.float64)
+            dot = float(rq @ rk)
+            if base is None:
+                base = dot
+                if m == n:  # same position: the rotation cancels
+                    assert abs(dot - float(q[0, 0].astype(np.float64) @ k[0, 0].astype(np.float64))) <= 1e-5 * scale
+            assert abs(dot - base) <= 1e-5 * scale, (m, n, shift)
