@@ -489,6 +489,7 @@ struct Chunk {
 // i of the rows is "page" i of a base pointer at the sequence's first new row).
 struct PageWindow {
     uint32_t base;  // first logical page covered (wave-uniform)
+    uint32_t valid; // page ids below this are readable (pool_pages; no bound for new rows)
     uint32_t page;  // per lane: physical page of logical page base + lane (0 past the end)
     float ks, vs;   // per lane: FP8 scales of that page
 };
@@ -502,10 +503,12 @@ __device__ __forceinline__ void window_load(const AttnParams &p, PageWindow &w,
     const uint32_t idx = first + lane_id();
     w.base = first;
     if (!table) { // identity pages of the new rows
+        w.valid = kNone;
         w.page = idx;
         w.ks = w.vs = 1.0f;
         return;
     }
+    w.valid = p.pool_pages;
     w.page = (uint32_t)__builtin_amdgcn_raw_buffer_load_b32(make_rsrc(table, limit * 4), (int)(idx * 4), 0, 0);
     if constexpr (FP8) {
         const uint32_t n = p.pool_pages * p.hkv * 4;
@@ -517,7 +520,9 @@ __device__ __forceinline__ void window_load(const AttnParams &p, PageWindow &w,
 
 // Physical page, live-token count and FP8 scales of the two 16-token tiles of chunk t
 // (pages hold >= 16 tokens, so a tile lies in one page).  Tokens at or past tlim are not
-// live: their loads return zeros and move no data.
+// live: their loads return zeros and move no data.  A table entry outside the pool (a stale
+// or corrupt block table; packing reports it) has no live tokens either, so no load is
+// ever based outside the pool: its keys read as zeros.
 struct TilePages {
     uint32_t page[2], live[2];
     float ks[2], vs[2];
@@ -534,7 +539,7 @@ __device__ __forceinline__ TilePages tile_pages(const PageWindow &w, uint32_t t,
         const uint32_t rel = (t0 >> shift) - w.base;
         tp.page[j] = (uint32_t)__builtin_amdgcn_readlane((int)w.page, (int)(rel & 63));
         const uint32_t pstart = t0 & ~(P - 1);
-        tp.live[j] = (rel < 64 && tlim > pstart) ? min(tlim - pstart, P) : 0u;
+        tp.live[j] = (rel < 64 && tlim > pstart && tp.page[j] < w.valid) ? min(tlim - pstart, P) : 0u;
         if constexpr (FP8) {
             tp.ks[j] = __builtin_bit_cast(float, __builtin_amdgcn_readlane(__builtin_bit_cast(int, w.ks), (int)(rel & 63)));
             tp.vs[j] = __builtin_bit_cast(float, __builtin_amdgcn_readlane(__builtin_bit_cast(int, w.vs), (int)(rel & 63)));
@@ -548,7 +553,7 @@ __device__ __forceinline__ TilePages tile_pages(const PageWindow &w, uint32_t t,
 // The same from pages preloaded by the plan: pre[i] is the page of logical page lp0 + i
 // (wave-uniform values, selected without indexing).
 __device__ __forceinline__ TilePages tile_pages_pre(uint4 pre, uint32_t lp0, uint32_t t,
-                                                    uint32_t shift, uint32_t tlim) {
+                                                    uint32_t shift, uint32_t tlim, uint32_t valid) {
     TilePages tp;
     const uint32_t P = 1u << shift;
 #pragma unroll
@@ -557,7 +562,7 @@ __device__ __forceinline__ TilePages tile_pages_pre(uint4 pre, uint32_t lp0, uin
         const uint32_t rel = (t0 >> shift) - lp0;
         const uint32_t pstart = t0 & ~(P - 1);
         tp.page[j] = rel == 0 ? pre.x : rel == 1 ? pre.y : rel == 2 ? pre.z : pre.w;
-        tp.live[j] = (rel < kPrePages && tlim > pstart) ? min(tlim - pstart, P) : 0u;
+        tp.live[j] = (rel < kPrePages && tlim > pstart && tp.page[j] < valid) ? min(tlim - pstart, P) : 0u;
         tp.ks[j] = tp.vs[j] = 1.0f;
     }
     return tp;
@@ -850,8 +855,8 @@ __device__ __forceinline__ void run_range(const AttnParams &p, const uint8_t *kb
         // prologue: chunks wbeg and wbeg + 32 in flight, chunk wbeg computed
         TilePages tp0, tp1;
         if (!C::FP8 && use_pre) {
-            tp0 = tile_pages_pre(pre, wbeg >> shift, wbeg, shift, wend);
-            tp1 = tile_pages_pre(pre, wbeg >> shift, wbeg + 32, shift, wend);
+            tp0 = tile_pages_pre(pre, wbeg >> shift, wbeg, shift, wend, p.pool_pages);
+            tp1 = tile_pages_pre(pre, wbeg >> shift, wbeg + 32, shift, wend, p.pool_pages);
             use_pre = false;
         } else {
             tp0 = tile_pages<C::FP8>(win, wbeg, shift, wend);
@@ -913,7 +918,7 @@ __device__ __forceinline__ void append_rows(const AttnParams &p, uint32_t wg, ui
         const uint32_t plane = i / (p.n_rows * pieces), rem = i % (p.n_rows * pieces);
         const uint32_t r = rem / pieces, k = rem % pieces;
         const uint32_t slot = p.slots[r];
-        if (slot == kNone) continue;
+        if (slot == kNone || (slot >> p.page_shift) >= p.pool_pages) continue; // outside the pool
         const u32x4 *src = (const u32x4 *)((const uint8_t *)(plane ? p.newv : p.newk) + (size_t)r * row_bytes) + k;
         u32x4 *dst = (u32x4 *)((uint8_t *)(plane ? p.vc_w : p.kc_w) + (size_t)slot * row_bytes) + k;
         u32x4 x = *src;
@@ -921,11 +926,24 @@ __device__ __forceinline__ void append_rows(const AttnParams &p, uint32_t wg, ui
     }
 }
 
-// One column's split record: unnormalised O for this wave's d slice (SW dims), reference
-// max and mass.
-// Record rows of 16-bit pools hold O / l in the pool's type (|O/l| <= max |V|, so the row is
-// in range; half the record traffic of f32); FP8 pools, whose values carry a page scale, keep
-// unnormalised f32 rows.
+// Four values of a normalised 16-bit split record row in the pool's type.  O / l is a convex
+// combination of V rows up to the rounding of the MFMA's 16-bit weights, so it can pass
+// max |V| by a rounding step: f16 rows saturate finite values to +-65504 instead of
+// rounding them to infinity.
+template <int KVT>
+__device__ __forceinline__ u32x2 record_pack(f32x4 v) {
+    if constexpr (KVT == LIA_F16) {
+#pragma unroll
+        for (int i = 0; i < 4; i++)
+            if (fabsf(v[i]) > 65504.0f && fabsf(v[i]) < INFINITY) v[i] = copysignf(65504.0f, v[i]);
+    }
+    return u32x2{pack2<KVT == LIA_BF16>(v.x, v.y), pack2<KVT == LIA_BF16>(v.z, v.w)};
+}
+
+// One column's split record for this wave's d slice (SW dims), with the reference max and
+// mass.  With a 16-bit output, record rows of 16-bit pools hold O / l in the pool's type
+// (half the record traffic of f32; the rounding is within a bf16 output's).  Rows for f32
+// outputs, and rows of FP8 pools, whose values carry a page scale, are unnormalised f32.
 template <int KVT>
 constexpr bool kRecord16 = KVT != LIA_FP8_E4M3;
 
@@ -933,14 +951,11 @@ template <int D, int SW, int KVT>
 __device__ __forceinline__ void store_record(const AttnParams &p, size_t rb, const f32x4 (&o)[SW / 16],
                                              float m, float l, uint32_t wave) {
     const uint32_t g = lane_id() >> 4;
-    if constexpr (kRecord16<KVT>) {
+    if (kRecord16<KVT> && !p.out_f32) {
         uint16_t *po = (uint16_t *)p.part_o + rb * D + SW * wave + 4 * g;
         const float inv = l > 0.0f ? 1.0f / l : 0.0f;
 #pragma unroll
-        for (int n = 0; n < SW / 16; n++) {
-            const f32x4 v = o[n] * inv;
-            *(u32x2 *)(po + 16 * n) = u32x2{pack2<KVT == LIA_BF16>(v.x, v.y), pack2<KVT == LIA_BF16>(v.z, v.w)};
-        }
+        for (int n = 0; n < SW / 16; n++) *(u32x2 *)(po + 16 * n) = record_pack<KVT>(o[n] * inv);
     } else {
         float *po = p.part_o + rb * D + SW * wave + 4 * g;
 #pragma unroll
@@ -1318,8 +1333,8 @@ __device__ __forceinline__ void wide_range(const AttnParams &p, const uint8_t *k
         window_load<false>(p, win, table, wbeg >> shift, page_limit, hk);
         TilePages tp0, tp1;
         if (use_pre) {
-            tp0 = tile_pages_pre(pre, wbeg >> shift, wbeg, shift, wend);
-            tp1 = tile_pages_pre(pre, wbeg >> shift, wbeg + 32, shift, wend);
+            tp0 = tile_pages_pre(pre, wbeg >> shift, wbeg, shift, wend, p.pool_pages);
+            tp1 = tile_pages_pre(pre, wbeg >> shift, wbeg + 32, shift, wend, p.pool_pages);
             use_pre = false;
         } else {
             tp0 = tile_pages<false>(win, wbeg, shift, wend);
@@ -1451,18 +1466,20 @@ __global__ __launch_bounds__(512, 4) void wide_kernel(AttnParams p) {
                     }
                 }
             } else {
-                // split record: O normalised by its own mass in the pool's 16-bit type (|O/l| <=
-                // max |V|, so it stays in range; relative error 2^-11 in f16, 2^-9 in bf16, the
-                // rounding of a bf16 output; half the record traffic of f32), with the mass and
-                // maximum in f32
+                // split record: O normalised by its own mass, in the pool's 16-bit type for a
+                // 16-bit output (relative error 2^-11 in f16, 2^-9 in bf16, the rounding of a
+                // bf16 output; half the record traffic of f32) or in f32 for an f32 output,
+                // with the mass and maximum in f32
                 const size_t rb = (size_t)rec * COLS + col;
-                uint16_t *po = (uint16_t *)p.part_o + rb * D + 4 * g;
                 const float inv = lt > 0.0f ? 1.0f / lt : 0.0f;
+                if (p.out_f32) {
+                    float *po = p.part_o + rb * D + 4 * g;
 #pragma unroll
-                for (int n = 0; n < W::DT; n++) {
-                    const f32x4 v = st.o[nt][n] * inv;
-                    *(u32x2 *)(po + 16 * n) = u32x2{pack2<KVT == LIA_BF16>(v.x, v.y),
-                                                    pack2<KVT == LIA_BF16>(v.z, v.w)};
+                    for (int n = 0; n < W::DT; n++) *(f32x4 *)(po + 16 * n) = st.o[nt][n] * inv;
+                } else {
+                    uint16_t *po = (uint16_t *)p.part_o + rb * D + 4 * g;
+#pragma unroll
+                    for (int n = 0; n < W::DT; n++) *(u32x2 *)(po + 16 * n) = record_pack<KVT>(st.o[nt][n] * inv);
                 }
                 if (g == 0) {
                     p.part_ml[rb * 2] = st.m[nt];
@@ -1599,7 +1616,8 @@ __global__ __launch_bounds__(kCombineThreads) void combine_kernel(AttnParams p) 
 constexpr uint32_t kWideCombineCols = 4;
 constexpr uint32_t kWideCombinePasses = 2;
 
-template <int D, bool BF>
+// REC: record rows normalised in f32 (0), f16 (1) or bf16 (2).
+template <int D, int REC>
 __global__ __launch_bounds__(256) void combine_wide_kernel(AttnParams p) {
     constexpr uint32_t Q = D / 4, RPP = 64 / Q, COLS = 16 * kWideNTDev;
     constexpr uint32_t CW = kWideCombineCols, KP = kWideCombinePasses;
@@ -1610,9 +1628,10 @@ __global__ __launch_bounds__(256) void combine_wide_kernel(AttnParams p) {
     const uint32_t ncols = (md.nrows_hk & 0xffffu) * p.group;
     if (md.n == 0 || col0 >= ncols) return;
     const uint32_t n = md.n, rec0 = md.rec0, q = lane % Q, rg = lane / Q;
-    // records hold O / l in f16, or bf16 for bf16 pools (BF), four values per quad, so a
-    // record weighs w * l
+    // records hold O / l (f32, f16 or bf16 per REC), four values per quad, so a record
+    // weighs w * l
     const u32x2 *po = (const u32x2 *)p.part_o;
+    const float4 *pf = (const float4 *)p.part_o;
     float M[CW], den[CW];
     float4 num[CW];
 #pragma unroll
@@ -1632,13 +1651,17 @@ __global__ __launch_bounds__(256) void combine_wide_kernel(AttnParams p) {
             for (uint32_t k = 0; k < KP; k++) {
                 const uint32_t r = base + k * RPP + rg;
                 const size_t rb = (size_t)(rec0 + min(r, n - 1)) * COLS + min(col0 + c, ncols - 1);
-                const u32x2 h = po[rb * Q + q];
-                if constexpr (BF)
-                    o[c][k] = make_float4(bf16_to_f32(h.x & 0xffffu), bf16_to_f32(h.x >> 16),
-                                          bf16_to_f32(h.y & 0xffffu), bf16_to_f32(h.y >> 16));
-                else
-                    o[c][k] = make_float4(f16_to_f32(h.x & 0xffffu), f16_to_f32(h.x >> 16),
-                                          f16_to_f32(h.y & 0xffffu), f16_to_f32(h.y >> 16));
+                if constexpr (REC == 0) {
+                    o[c][k] = pf[rb * Q + q];
+                } else {
+                    const u32x2 h = po[rb * Q + q];
+                    if constexpr (REC == 2)
+                        o[c][k] = make_float4(bf16_to_f32(h.x & 0xffffu), bf16_to_f32(h.x >> 16),
+                                              bf16_to_f32(h.y & 0xffffu), bf16_to_f32(h.y >> 16));
+                    else
+                        o[c][k] = make_float4(f16_to_f32(h.x & 0xffffu), f16_to_f32(h.x >> 16),
+                                              f16_to_f32(h.y & 0xffffu), f16_to_f32(h.y >> 16));
+                }
                 const float2 ml = ((const float2 *)p.part_ml)[rb];
                 m[c][k] = ml.x;
                 l[c][k] = r < n ? ml.y : 0.0f;
@@ -1982,7 +2005,8 @@ static int run_stages(int stages, const lia_attention_config *c, uint32_t n_seqs
     }
     if (stages & kMerge) {
         // units this NT can produce: rows in blocks of rpc per sequence and KV head
-        uint32_t units_nt = (c->max_rows / (rpc ? rpc : 1) + n_seqs + 1) * c->num_kv_heads;
+        // (sum over sequences of ceil(rows / rpc) <= n_rows / rpc + n_seqs)
+        uint32_t units_nt = (n_rows / (rpc ? rpc : 1) + n_seqs + 1) * c->num_kv_heads;
         uint32_t cols = 16 * NT;
         if (NT == 1 && n_rows == n_seqs) {
             // one row per column block (rpc = 1): n_rows units per KV head, `group` columns
@@ -1994,8 +2018,10 @@ static int run_stages(int stages, const lia_attention_config *c, uint32_t n_seqs
         // record row over two workgroups (measured 0.6 us faster per layer at 128 workgroups,
         // slower on grids of hundreds or thousands), and over four when units hold hundreds of
         // records (one or two long sequences: a batch of 256 records per pass instead of 128)
-        const int rec = c->kv_dtype == LIA_BF16 ? 2 : c->kv_dtype == LIA_F16 ? 1 : 0;
-        const uint32_t per_unit = n_wg / (grid.x ? grid.x : 1); // records per unit, roughly
+        // record rows: f32 for f32 outputs and FP8 pools, else the pool's 16-bit type
+        const int rec = p.out_f32 ? 0 : c->kv_dtype == LIA_BF16 ? 2 : c->kv_dtype == LIA_F16 ? 1 : 0;
+        const uint32_t est_units = max((n_rows + rpc - 1) / rpc, n_seqs) * c->num_kv_heads;
+        const uint32_t per_unit = n_wg / est_units; // records per unit, roughly
         const uint32_t split = per_unit >= 128 ? 4 : grid.x * grid.y < 256 ? 2 : 1;
         grid.z = split;
 #define LIA_COMBINE(DD, NN)                                                                      \
@@ -2008,15 +2034,15 @@ static int run_stages(int stages, const lia_attention_config *c, uint32_t n_seqs
         if (c->head_dim == 128) {
             if (NT == 1) LIA_COMBINE(128, 1);
             else if (NT == 2) LIA_COMBINE(128, 2);
-            else if (c->kv_dtype == LIA_BF16)
-                hipLaunchKernelGGL((combine_wide_kernel<128, true>), wgrid, dim3(256), 0, s, p);
-            else hipLaunchKernelGGL((combine_wide_kernel<128, false>), wgrid, dim3(256), 0, s, p);
+            else if (rec == 0) hipLaunchKernelGGL((combine_wide_kernel<128, 0>), wgrid, dim3(256), 0, s, p);
+            else if (rec == 2) hipLaunchKernelGGL((combine_wide_kernel<128, 2>), wgrid, dim3(256), 0, s, p);
+            else hipLaunchKernelGGL((combine_wide_kernel<128, 1>), wgrid, dim3(256), 0, s, p);
         } else {
             if (NT == 1) LIA_COMBINE(64, 1);
             else if (NT == 2) LIA_COMBINE(64, 2);
-            else if (c->kv_dtype == LIA_BF16)
-                hipLaunchKernelGGL((combine_wide_kernel<64, true>), wgrid, dim3(256), 0, s, p);
-            else hipLaunchKernelGGL((combine_wide_kernel<64, false>), wgrid, dim3(256), 0, s, p);
+            else if (rec == 0) hipLaunchKernelGGL((combine_wide_kernel<64, 0>), wgrid, dim3(256), 0, s, p);
+            else if (rec == 2) hipLaunchKernelGGL((combine_wide_kernel<64, 2>), wgrid, dim3(256), 0, s, p);
+            else hipLaunchKernelGGL((combine_wide_kernel<64, 1>), wgrid, dim3(256), 0, s, p);
         }
 #undef LIA_COMBINE
     }

@@ -19,6 +19,23 @@ __device__ __forceinline__ float append_scale(float *scales, size_t at) {
 // into cu_seqlens and then every thread fills rows: position = cached + i, sequence =
 // table row, slot = pages[seq * stride + pos / P] * P + pos % P (the slot rule of
 // src/inference/paging.rs:163-166 and src/gpu/kernels/llama.rs:174-177).
+//
+// Checks, as Engine::run_paged makes them on the host (paging.rs:137-172):
+//   - every table entry a sequence attends (logical pages 0 .. ceil((cached + q_len) / P) - 1)
+//     that is neither a pool page nor the "no page" marker: LIA_E_PAGE_RANGE, ahead of every
+//     row check (paging.rs:139-144 checks the tables first);
+//   - per row, in row order: position >= context (LIA_E_POSITION), the row's page missing
+//     (LIA_E_MISSING_PAGE), its slot written by an earlier row (LIA_E_DUPLICATE_SLOT,
+//     paging.rs:163-166); a cached page marked missing is reported at the sequence's first
+//     row as LIA_E_MISSING_PAGE (the attention kernels would read it).
+// Positions within a sequence are consecutive by construction.  On failure cu_seqlens is
+// written all zero and every slot as "no slot", so a plan built from them schedules no work,
+// no append writes the pool and the attention output is left untouched.
+constexpr uint32_t kPackHash = 8192;  // LDS slot hash (open addressing, load <= 1/2 per pass)
+constexpr uint32_t kPackPass = kPackHash / 2;
+
+__device__ __forceinline__ uint32_t slot_hash(uint32_t s) { return (s * 2654435761u) >> 19; } // 13 bits
+
 __global__ __launch_bounds__(1024) void pack_kernel(uint32_t n_seqs, const uint32_t *seq_slots,
                                                     const uint32_t *q_lens, const uint32_t *cached,
                                                     const uint32_t *pages, uint32_t stride,
@@ -27,33 +44,68 @@ __global__ __launch_bounds__(1024) void pack_kernel(uint32_t n_seqs, const uint3
                                                     uint32_t *cu, uint32_t *positions,
                                                     uint32_t *sequences, uint32_t *slot_mapping,
                                                     uint32_t *status) {
-    __shared__ uint32_t scan[1024], s_slot[1024], s_c0[1024];
+    __shared__ uint32_t scan[1024], pscan[1024], s_slot[1024], s_c0[1024];
+    __shared__ uint32_t h_key[kPackHash], h_row[kPackHash];
     // error: (row << 4) | code of the failing row with the lowest index, so the status is the
     // first failure in row order whatever the thread timing (codes are below 16)
-    __shared__ uint32_t carry, error;
+    __shared__ uint32_t carry, error, range_error;
     const uint32_t t = threadIdx.x;
-    if (t == 0) { carry = 0; error = 0xFFFFFFFFu; }
+    if (t == 0) { carry = 0; error = 0xFFFFFFFFu; range_error = 0; }
     __syncthreads();
     const uint32_t P = 1u << page_shift;
-    for (uint32_t base = 0; base < n_seqs; base += 1024) {
-        uint32_t b = base + t;
-        uint32_t n = b < n_seqs ? q_lens[b] : 0;
-        if (n_seqs <= 1024) { // kept for the rows below
-            s_slot[t] = b < n_seqs ? seq_slots[b] : 0u;
-            s_c0[t] = b < n_seqs ? cached[b] : 0u;
+    auto upper = [&](const uint32_t *arr, uint32_t n, uint32_t v) { // smallest b with arr[b] > v
+        uint32_t a = 0, e = n;
+        while (a < e) {
+            const uint32_t mid = (a + e) >> 1;
+            if (arr[mid] > v) e = mid; else a = mid + 1;
         }
+        return a;
+    };
+    for (uint32_t base = 0; base < n_seqs; base += 1024) {
+        const uint32_t b = base + t;
+        const uint32_t n = b < n_seqs ? q_lens[b] : 0;
+        const uint32_t slot = b < n_seqs ? seq_slots[b] : 0u, c0 = b < n_seqs ? cached[b] : 0u;
+        // logical pages the sequence attends, within its table row
+        const uint32_t keys = min(c0 + n, context);
+        const uint32_t npg = n ? min((keys + P - 1) >> page_shift, stride) : 0u;
+        s_slot[t] = slot;
+        s_c0[t] = c0;
         scan[t] = n;
+        pscan[t] = npg;
         __syncthreads();
         for (uint32_t off = 1; off < 1024; off <<= 1) {
-            uint32_t a = t >= off ? scan[t - off] : 0;
+            const uint32_t a = t >= off ? scan[t - off] : 0, c = t >= off ? pscan[t - off] : 0;
             __syncthreads();
             scan[t] += a;
+            pscan[t] += c;
             __syncthreads();
         }
-        uint32_t start = carry + scan[t] - n;
+        const uint32_t start = carry + scan[t] - n;
         if (b < n_seqs) {
             cu[b] = start;
             if (b == n_seqs - 1) cu[n_seqs] = start + n;
+        }
+        // table entries of this chunk of sequences, flattened and 8 loads in flight per thread
+        const uint32_t cnt = min(n_seqs - base, 1024u), total_pg = pscan[cnt - 1];
+        for (uint32_t e0 = t; e0 < total_pg; e0 += 8 * 1024) {
+            uint32_t v[8], bl[8], lp[8];
+#pragma unroll
+            for (int k = 0; k < 8; k++) {
+                const uint32_t e = min(e0 + k * 1024, total_pg - 1);
+                bl[k] = upper(pscan, cnt, e);
+                lp[k] = e - (bl[k] ? pscan[bl[k] - 1] : 0u);
+                v[k] = pages[(size_t)s_slot[bl[k]] * stride + lp[k]];
+            }
+#pragma unroll
+            for (int k = 0; k < 8; k++) {
+                if (e0 + k * 1024 >= total_pg) break;
+                if (v[k] != kNone && v[k] >= pool_pages) range_error = 1;
+                // a page wholly below the cached length marked missing
+                if (v[k] == kNone && (lp[k] + 1) * P <= s_c0[bl[k]]) {
+                    const uint32_t r0 = carry + (bl[k] ? scan[bl[k] - 1] : 0u);
+                    atomicMin(&error, (r0 << 4) | (uint32_t)(-LIA_E_MISSING_PAGE));
+                }
+            }
         }
         __syncthreads();
         if (t == 1023) carry += scan[1023];
@@ -78,32 +130,84 @@ __global__ __launch_bounds__(1024) void pack_kernel(uint32_t n_seqs, const uint3
         sequences[r] = slot;
         slot_mapping[r] = s;
     };
-    auto report = [&] {
-        __syncthreads();
-        if (t == 0) *status = error == 0xFFFFFFFFu ? 0u : (error & 15u);
-    };
     if (n_seqs <= 1024) {
         // Rows in parallel: row r belongs to the first sequence whose inclusive prefix sum
         // (scan, still in LDS) exceeds r.
         for (uint32_t r = t; r < total; r += 1024) {
-            uint32_t a = 0, e = n_seqs; // smallest b with scan[b] > r
-            while (a < e) {
-                const uint32_t mid = (a + e) >> 1;
-                if (scan[mid] > r) e = mid; else a = mid + 1;
-            }
-            const uint32_t start = a ? scan[a - 1] : 0u;
-            fill(r, r - start, s_slot[a], s_c0[a]);
+            const uint32_t a = upper(scan, n_seqs, r);
+            fill(r, r - (a ? scan[a - 1] : 0u), s_slot[a], s_c0[a]);
         }
-        report();
-        return;
+    } else {
+        // More sequences than the LDS copies hold: walk sequences, threads stride over each
+        // sequence's rows.
+        for (uint32_t b = 0; b < n_seqs; b++) {
+            const uint32_t start = cu[b], n = q_lens[b], slot = seq_slots[b], c0 = cached[b];
+            for (uint32_t i = t; i < n; i += 1024) fill(start + i, i, slot, c0);
+        }
     }
-    // More sequences than the LDS copies hold: walk sequences, threads stride over each
-    // sequence's rows.
-    for (uint32_t b = 0; b < n_seqs; b++) {
-        const uint32_t start = cu[b], n = q_lens[b], slot = seq_slots[b], c0 = cached[b];
-        for (uint32_t i = t; i < n; i += 1024) fill(start + i, i, slot, c0);
+    __threadfence_block(); // this workgroup's slot_mapping writes, read back below
+    __syncthreads();
+    // Duplicate slots: each pass hashes the slots of one hash class (at most kPackPass rows
+    // on average), keeping the lowest row per slot; a row whose slot has a lower row fails.
+    const uint32_t passes = (total + kPackPass - 1) / kPackPass;
+    for (uint32_t pass = 0; pass < passes; pass++) {
+        for (uint32_t i = t; i < kPackHash; i += 1024) { h_key[i] = kNone; h_row[i] = kNone; }
+        __syncthreads();
+        for (uint32_t r = t; r < total; r += 1024) {
+            const uint32_t s = slot_mapping[r];
+            if (s == kNone || (s % passes) != pass) continue;
+            uint32_t h = slot_hash(s), probes = 0;
+            while (probes < kPackHash) {
+                const uint32_t k = atomicCAS(&h_key[h], kNone, s);
+                if (k == kNone || k == s) { atomicMin(&h_row[h], r); break; }
+                h = (h + 1) & (kPackHash - 1);
+                probes++;
+            }
+            if (probes == kPackHash) { // table full (a pathological slot pattern): scan the rows
+                for (uint32_t q = 0; q < r; q++)
+                    if (slot_mapping[q] == s) { atomicMin(&error, (r << 4) | (uint32_t)(-LIA_E_DUPLICATE_SLOT)); break; }
+            }
+        }
+        __syncthreads();
+        for (uint32_t r = t; r < total; r += 1024) {
+            const uint32_t s = slot_mapping[r];
+            if (s == kNone || (s % passes) != pass) continue;
+            uint32_t h = slot_hash(s);
+            for (uint32_t probes = 0; probes < kPackHash; probes++) {
+                const uint32_t k = h_key[h];
+                if (k == s) {
+                    if (h_row[h] < r) atomicMin(&error, (r << 4) | (uint32_t)(-LIA_E_DUPLICATE_SLOT));
+                    break;
+                }
+                if (k == kNone) break;
+                h = (h + 1) & (kPackHash - 1);
+            }
+        }
+        __syncthreads();
     }
-    report();
+    const uint32_t code = range_error ? (uint32_t)(-LIA_E_PAGE_RANGE)
+                          : error == 0xFFFFFFFFu ? 0u : (error & 15u);
+    if (code) {
+        // nothing downstream may run on a rejected batch
+        for (uint32_t b = t; b <= n_seqs; b += 1024) cu[b] = 0;
+        for (uint32_t r = t; r < total; r += 1024) slot_mapping[r] = kNone;
+    }
+    if (t == 0) *status = code;
+}
+
+// Slot of append row r (slot_mapping[r], or the table's page of its position); kNone for
+// "no slot" and for any slot outside the pool, whose row is then not written.
+__device__ __forceinline__ uint32_t row_slot(uint32_t r, const uint32_t *slot_mapping,
+                                             const uint32_t *positions, const uint32_t *sequences,
+                                             const uint32_t *pages, uint32_t stride,
+                                             uint32_t page_shift, uint32_t pool_pages) {
+    if (slot_mapping) {
+        const uint32_t slot = slot_mapping[r];
+        return (slot >> page_shift) < pool_pages ? slot : kNone;
+    }
+    const uint32_t pos = positions[r];
+    const uint32_t page = pages[(size_t)sequences[r] * stride + (pos >> page_shift)];
+    return page < pool_pages ? page * (1u << page_shift) + (pos & ((1u << page_shift) - 1)) : kNone;
 }
 
 template <typename SRC>
@@ -123,7 +227,7 @@ __global__ __launch_bounds__(256) void append_kernel(uint32_t rows, uint32_t wid
                                                      uint32_t hkv, const uint32_t *positions,
                                                      const uint32_t *sequences,
                                                      const uint32_t *pages, uint32_t stride,
-                                                     uint32_t page_shift,
+                                                     uint32_t page_shift, uint32_t pool_pages,
                                                      const uint32_t *slot_mapping, int src_kind,
                                                      const void *k, const void *v, void *kc,
                                                      void *vc, float *k_scales,
@@ -132,14 +236,7 @@ __global__ __launch_bounds__(256) void append_kernel(uint32_t rows, uint32_t wid
     const uint32_t quads = width / 4;
     if (i >= (size_t)rows * quads) return;
     const uint32_t r = (uint32_t)(i / quads), e0 = (uint32_t)(i % quads) * 4;
-    uint32_t slot;
-    if (slot_mapping) {
-        slot = slot_mapping[r];
-    } else {
-        uint32_t pos = positions[r];
-        slot = pages[(size_t)sequences[r] * stride + (pos >> page_shift)] * (1u << page_shift) +
-               (pos & ((1u << page_shift) - 1));
-    }
+    const uint32_t slot = row_slot(r, slot_mapping, positions, sequences, pages, stride, page_shift, pool_pages);
     if (slot == kNone) return;
     float kx[4], vx[4];
     size_t src = (size_t)r * width + e0;
@@ -265,7 +362,7 @@ template <int KVT>
 __global__ __launch_bounds__(256) void rope_append_kernel(
     uint32_t rows, uint32_t hq, uint32_t hkv, uint32_t d, const uint32_t *positions,
     const uint32_t *sequences, const uint32_t *pages, uint32_t stride, uint32_t page_shift,
-    const uint32_t *slot_mapping, const float *coefficients, const float *input, void *query,
+    uint32_t pool_pages, const uint32_t *slot_mapping, const float *coefficients, const float *input, void *query,
     int query_bf16, void *kc, void *vc, float *k_scales, float *v_scales) {
 #pragma clang fp contract(off)
     const uint32_t half = d / 2, quads = half / 4, heads = hq + hkv;
@@ -300,14 +397,7 @@ __global__ __launch_bounds__(256) void rope_append_kernel(
         return;
     }
     const uint32_t kh = h - hq;
-    uint32_t slot;
-    if (slot_mapping) {
-        slot = slot_mapping[r];
-    } else {
-        const uint32_t pos = positions[r];
-        slot = pages[(size_t)sequences[r] * stride + (pos >> page_shift)] * (1u << page_shift) +
-               (pos & ((1u << page_shift) - 1));
-    }
+    const uint32_t slot = row_slot(r, slot_mapping, positions, sequences, pages, stride, page_shift, pool_pages);
     if (slot == kNone) return;
     float ks = 1.0f, vs = 1.0f;
     if constexpr (KVT == LIA_FP8_E4M3) {
@@ -394,7 +484,7 @@ extern "C" int lia_rope_kv_append(const lia_kv_layout *L, uint32_t num_q_heads, 
 #define LIA_ROPE(KVT)                                                                              \
     hipLaunchKernelGGL(rope_append_kernel<KVT>, grid, dim3(256), 0, s, rows, num_q_heads,          \
                        L->num_kv_heads, L->head_dim, positions, sequences, pages, stride, shift,   \
-                       slot_mapping, coefficients, input, query, qb, kc, vc, k_scales, v_scales)
+                       L->pool_pages, slot_mapping, coefficients, input, query, qb, kc, vc, k_scales, v_scales)
     switch (L->dtype) {
     case LIA_F16: LIA_ROPE(LIA_F16); break;
     case LIA_BF16: LIA_ROPE(LIA_BF16); break;
@@ -446,18 +536,18 @@ extern "C" int lia_kv_append(const lia_kv_layout *L, uint32_t rows, const uint32
     switch (L->dtype) {
     case LIA_F16:
         hipLaunchKernelGGL(append_kernel<LIA_F16>, grid, dim3(256), 0, s, rows, width, L->head_dim,
-                           L->num_kv_heads, positions, sequences, pages, stride, shift, slot_mapping,
-                           kind, k, v, kc, vc, k_scales, v_scales);
+                           L->num_kv_heads, positions, sequences, pages, stride, shift, L->pool_pages,
+                           slot_mapping, kind, k, v, kc, vc, k_scales, v_scales);
         break;
     case LIA_BF16:
         hipLaunchKernelGGL(append_kernel<LIA_BF16>, grid, dim3(256), 0, s, rows, width, L->head_dim,
-                           L->num_kv_heads, positions, sequences, pages, stride, shift, slot_mapping,
-                           kind, k, v, kc, vc, k_scales, v_scales);
+                           L->num_kv_heads, positions, sequences, pages, stride, shift, L->pool_pages,
+                           slot_mapping, kind, k, v, kc, vc, k_scales, v_scales);
         break;
     case LIA_FP8_E4M3:
         hipLaunchKernelGGL(append_kernel<LIA_FP8_E4M3>, grid, dim3(256), 0, s, rows, width,
                            L->head_dim, L->num_kv_heads, positions, sequences, pages, stride, shift,
-                           slot_mapping, kind, k, v, kc, vc, k_scales, v_scales);
+                           L->pool_pages, slot_mapping, kind, k, v, kc, vc, k_scales, v_scales);
         break;
     default:
         return LIA_E_UNSUPPORTED;

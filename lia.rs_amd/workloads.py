@@ -39,6 +39,7 @@ class Batch:
     name: str = ""
     layers: int = 1
     notes: list = field(default_factory=list)
+    shared: dict = field(default_factory=dict)  # sequence -> (donor, prefix pages shared)
 
     @property
     def n_seqs(self):
@@ -74,7 +75,8 @@ class Batch:
         return (flat[seq * self.stride + pos // P] * P + pos % P).astype(np.uint32)
 
     def kv_bytes(self):
-        """Algorithmic K+V bytes read by one attention pass (each key read once)."""
+        """Algorithmic K+V bytes read by one attention pass (each sequence's keys read once;
+        a shared prefix page is attended by each sequence that holds it)."""
         eb = 1 if self.geom.kv_dtype == FP8 else 2
         return int(self.ctx.sum()) * self.geom.hkv * self.geom.d * 2 * eb
 
@@ -144,16 +146,26 @@ def config2(seed=0, layers=40):
 
 def config3(seed=0):
     """Mixed chunked prefill + decode: chunks (new, cached) = (512, 0), (1024, 4096),
-    (2048, 8192) plus 5 decode sequences with ctx U[2048, 16384]."""
+    (2048, 8192) plus 5 decode sequences with ctx U[2048, 16384].  Prefix-cache hits share
+    pages by reference count: the 4096-token cached prefix of the second chunk (256 full,
+    immutable pages) is also the first 4096 tokens of the third chunk's prefix and of every
+    decode sequence whose cached keys cover it, so those tables start with the same 256
+    physical pages (src/inference/page_cache.rs:48-157 attaches a prefix hit that way)."""
     g = Geometry()
     rng = np.random.default_rng(seed)
     dec = rng.integers(2048, 16384, size=5, endpoint=True)
     ctx = np.array([512, 4096 + 1024, 8192 + 2048, *dec], dtype=np.int64)
     q = np.array([512, 1024, 2048, 1, 1, 1, 1, 1], dtype=np.int64)
-    pages = int(sum(-(-int(c) // 16) for c in ctx))
+    cached = ctx - q
+    shared_pages = 4096 // 16
+    shared = {s: (1, shared_pages) for s in range(2, 8) if cached[s] >= 4096}
+    pages = int(sum(-(-int(c) // 16) for c in ctx)) - shared_pages * len(shared)
     pool = pages + 64
-    return Batch(g, ctx, q, pool, _tables(rng, ctx, 16, pool), stride=-(-int(ctx.max()) // 16),
-                 name="cfg3_mixed")
+    b = Batch(g, ctx, q, pool, _tables(rng, ctx, 16, pool, shared=shared),
+              stride=-(-int(ctx.max()) // 16), name="cfg3_mixed")
+    b.notes.append(f"sequences {sorted(shared)} share sequence 1's first {shared_pages} pages")
+    b.shared = shared
+    return b
 
 
 def config4(seed=0):

@@ -316,3 +316,40 @@ def test_prefill_kernel_geometries(lia, wl, kv, d, page):
     g = wl.Geometry(hq=16, hkv=2, d=d, page_size=page, kv_dtype=kv, q_dtype=F32, out_dtype=F32)
     b = wl.custom([300, 1000 + 77, 40, 513], [300, 77, 40, 33], geom=g, seed=9)
     _check(G.Case(b, seed=9), lia, f"prefill kv={kv} d={d} page={page}")
+
+
+@pytest.mark.parametrize("kv", [BF16, F16])
+def test_f32_output_split_records_keep_f32_precision(lia, wl, O, kv):
+    """Long contexts split over many workgroups, f32 queries and outputs: the split records
+    are f32 (no 16-bit rounding of partial rows), so the error against the float64 oracle
+    stays at the level of the kernel's 16-bit MFMA operands, and the same batch with bf16
+    output (16-bit records) is no closer than that."""
+    g = wl.Geometry(hq=16, hkv=2, d=128, kv_dtype=kv, q_dtype=F32, out_dtype=F32)
+    b = wl.custom([30000, 12000, 4096], [1, 1, 1], geom=g, seed=51)
+    case = G.Case(b, seed=51)
+    got = case.run(lia)
+    ref = case.f64()
+    mx, mean = G.errors(got, ref)
+    cpu = O.paged_attention_f32(case.oracle_geom(), case.positions, case.sequences, case.flat,
+                                case.q32, case.kc, case.vc, span=256)
+    cmx, _ = G.errors(cpu, ref)
+    print(f"[case] f32 out split kv={kv}: max_abs={mx:.3e} mean_abs={mean:.3e} "
+          f"(oracle f32 split-K {cmx:.3e})", flush=True)
+    assert mx < 2e-3 and mean < 2e-4
+
+
+def test_f16_split_records_saturate_at_the_f16_maximum(lia, wl):
+    """An f16 pool whose V values sit at +-65504 over units split across workgroups, bf16
+    output (f16 records): a record row may exceed max |V| by a rounding step; it saturates
+    instead of becoming infinite, so the merged output stays finite and within tolerance."""
+    g = wl.Geometry(hq=16, hkv=2, d=128, kv_dtype=F16, q_dtype=BF16, out_dtype=BF16)
+    b = wl.custom([20000, 9000], [1, 1], geom=g, seed=52)
+    case = G.Case(b, seed=52)
+    v = np.where(np.random.default_rng(52).random(case.vc.size) < 0.5, 65504.0, -65504.0)
+    case.vc = v.astype(np.float16).view(np.uint16)
+    got = case.run(lia)
+    ref = case.f64()
+    mx, mean = G.errors(got, ref)
+    print(f"[case] f16 V at +-65504: max_abs={mx:.3e} mean_abs={mean:.3e}", flush=True)
+    assert np.all(np.isfinite(got))
+    assert mx < 2e-2 * 65504 and mean < 2e-3 * 65504

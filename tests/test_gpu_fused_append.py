@@ -139,3 +139,70 @@ def test_fused_append_canonicalises_nan_like_kv_append(lia, wl, O, kv):
     torch.cuda.synchronize()
     assert np.array_equal(dev["kc"].cpu().numpy().view(np.uint16), kexp)
     assert np.array_equal(dev["vc"].cpu().numpy().view(np.uint16), vexp)
+
+
+def test_config3_full_step_with_shared_prefix_pages(lia, wl, O):
+    """BASELINE config 3 at full size as a step: device packing builds cu_seqlens, positions,
+    sequences and the slot mapping from per-sequence counts (bit-exact against the oracle's
+    host packing), the plan, the attention launch with the new K/V appended into the pool,
+    and the merge.  The prefill chunks and decode rows share a 256-page cached prefix by
+    reference count.  Outputs against the float64 oracle; the pool against lo_kv_append of
+    the new rows into the pool as it was before the step."""
+    b = wl.config3(seed=0)
+    assert b.shared, "config 3 shares prefix pages"
+    case = G.Case(b, seed=0)
+    g = b.geom
+    P, W = g.page_size, g.hkv * g.d
+    print(f"[case] cfg3 step: rows={b.n_rows} seqs={b.n_seqs} {b.notes}", flush=True)
+    slots_h = b.slot_mapping()
+    kc0, vc0 = case.kc.reshape(-1, W), case.vc.reshape(-1, W)
+    newk, newv = kc0[slots_h.astype(np.int64)].copy(), vc0[slots_h.astype(np.int64)].copy()
+    # the pool before the step: the new rows' slots hold junk
+    rng = np.random.default_rng(33)
+    before_k, before_v = kc0.copy(), vc0.copy()
+    before_k[slots_h.astype(np.int64)] = rng.integers(0, 65535, newk.shape).astype(np.uint16)
+    before_v[slots_h.astype(np.int64)] = rng.integers(0, 65535, newv.shape).astype(np.uint16)
+    dkc = G.to_dev(before_k.reshape(-1), torch.int16)
+    dvc = G.to_dev(before_v.reshape(-1), torch.int16)
+    flat = G.u32_dev(b.flat_table())
+    rows = b.n_rows
+    cu = torch.zeros(b.n_seqs + 1, dtype=torch.int32, device="cuda")
+    positions = torch.zeros(rows, dtype=torch.int32, device="cuda")
+    sequences = torch.zeros_like(positions)
+    slots = torch.zeros_like(positions)
+    status = torch.full((1,), -1, dtype=torch.int32, device="cuda")
+    cfg = case.config(lia)
+    ws = torch.zeros(lia.workspace_bytes(cfg), dtype=torch.uint8, device="cuda")
+    out = torch.full((rows, g.hq, g.d), float("nan"), dtype=torch.bfloat16, device="cuda")
+    lia.pack_device(G.u32_dev(np.arange(b.n_seqs)), G.u32_dev(b.q_len), G.u32_dev(b.cached), flat,
+                    b.stride, P, b.pool_pages, b.stride * P, rows, cu, positions, sequences, slots,
+                    status)
+    lia.attention_plan(cfg, b.n_seqs, rows, cu, positions, sequences, ws, pages=flat)
+    lia.attention_partial_append(cfg, b.n_seqs, flat, slots, G.to_dev(case.q_store, torch.bfloat16),
+                                 G.to_dev(newk, torch.int16), G.to_dev(newv, torch.int16), dkc, dvc,
+                                 out, ws)
+    lia.attention_merge(cfg, b.n_seqs, rows, out, ws)
+    torch.cuda.synchronize()
+    assert status.item() == 0
+    # packing: the oracle's host packing of the same rows
+    lim = O.PagingLimits(b.n_seqs, b.stride * P, P, b.pool_pages, 1, rows)
+    st, packed = O.pack_rows(lim, [(0, int(p), int(s)) for p, s in zip(b.positions(), b.sequences())],
+                             [t.tolist() for t in b.tables], [])
+    assert st == 0
+    assert np.array_equal(cu.cpu().numpy().view(np.uint32), packed["cu_seqlens"])
+    assert np.array_equal(positions.cpu().numpy().view(np.uint32), packed["positions"])
+    assert np.array_equal(sequences.cpu().numpy().view(np.uint32), packed["sequences"])
+    assert np.array_equal(slots.cpu().numpy().view(np.uint32), packed["slot_mapping"])
+    # pool: lo_kv_append of the step's rows into the pool as it was before
+    kexp, vexp = before_k.reshape(-1).copy(), before_v.reshape(-1).copy()
+    layout = O.KVLayout(g.hkv, g.d, P, b.pool_pages, g.kv_dtype)
+    O.kv_append(layout, packed["positions"], packed["sequences"], b.flat_table(), b.stride, newk,
+                newv, kexp, vexp, src_dtype=g.kv_dtype)
+    assert np.array_equal(dkc.cpu().numpy().view(np.uint16), kexp)
+    assert np.array_equal(dvc.cpu().numpy().view(np.uint16), vexp)
+    got = out.float().cpu().numpy()
+    ref = case.f64()
+    mx, mean = G.errors(got, ref)
+    print(f"[case] cfg3 step: max_abs={mx:.3e} mean_abs={mean:.3e}", flush=True)
+    assert np.all(np.isfinite(got))
+    assert mx < 2e-2 and mean < 2e-3
