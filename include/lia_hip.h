@@ -127,8 +127,21 @@ uint32_t lia_decode_parts(uint32_t tokens, uint32_t span);
  *   table row seq_slots[b], q_lens[b] new tokens at positions cached[b] .. cached[b]+q_lens[b]-1.
  * Writes cu_seqlens[n_seqs+1], positions[rows], sequences[rows], slot_mapping[rows].
  * Rows beyond the batch total up to max_rows are left untouched.  status (device, one u32)
- * receives 0 or the first failing lia_status as a positive number (-status): a missing page
- * (table entry 0xFFFFFFFF or >= pool_pages), a position >= context, or too many rows.
+ * receives 0 or the first failing lia_status as a positive number (-status), with the
+ * reference's checks in its order (paging.rs:137-172):
+ *   LIA_E_PAGE_RANGE     a table entry the batch attends (logical pages 0 .. ceil((cached +
+ *                        q_len) / page_size) - 1 of each sequence with rows) that is neither
+ *                        below pool_pages nor 0xFFFFFFFF; reported ahead of any row check;
+ *   then per row, the lowest failing row first:
+ *   LIA_E_POSITION       position >= context;
+ *   LIA_E_MISSING_PAGE   the row's page is 0xFFFFFFFF (reported at a sequence's first row for
+ *                        a missing page wholly below its cached length);
+ *   LIA_E_DUPLICATE_SLOT the row's slot is written by an earlier row;
+ *   and LIA_E_ROWS when the rows exceed max_rows.
+ * On failure cu_seqlens is written all zero and slot_mapping[0 .. max_rows) as 0xFFFFFFFF
+ * (the arrays hold max_rows entries), so a plan built
+ * from them schedules no work and no append writes the pool: the step's outputs and the pool
+ * are left untouched without a host round trip.
  */
 int lia_pack_device(uint32_t n_seqs, const uint32_t *seq_slots, const uint32_t *q_lens,
                     const uint32_t *cached, const uint32_t *pages, uint32_t stride,

@@ -29,8 +29,8 @@ __device__ __forceinline__ float append_scale(float *scales, size_t at) {
 //     paging.rs:163-166); a cached page marked missing is reported at the sequence's first
 //     row as LIA_E_MISSING_PAGE (the attention kernels would read it).
 // Positions within a sequence are consecutive by construction.  On failure cu_seqlens is
-// written all zero and every slot as "no slot", so a plan built from them schedules no work,
-// no append writes the pool and the attention output is left untouched.
+// written all zero and all max_rows slots as "no slot", so a plan built from them schedules
+// no work, no append writes the pool and the attention output is left untouched.
 constexpr uint32_t kPackHash = 8192;  // LDS slot hash (open addressing, load <= 1/2 per pass)
 constexpr uint32_t kPackPass = kPackHash / 2;
 
@@ -112,8 +112,16 @@ __global__ __launch_bounds__(1024) void pack_kernel(uint32_t n_seqs, const uint3
         __syncthreads();
     }
     const uint32_t total = carry;
+    // rejects the batch: no sequence has rows, no row has a slot (all max_rows slots, so a
+    // launch given more rows than the batch holds finds none either)
+    auto reject = [&](uint32_t code) {
+        for (uint32_t b = t; b <= n_seqs; b += 1024) cu[b] = 0;
+        for (uint32_t r = t; r < max_rows; r += 1024) slot_mapping[r] = kNone;
+        if (t == 0) *status = code;
+    };
     if (total > max_rows) {
-        if (t == 0) *status = (uint32_t)(-LIA_E_ROWS);
+        __syncthreads(); // every cu write of the scan is done
+        reject((uint32_t)(-LIA_E_ROWS));
         return;
     }
     auto fill = [&](uint32_t r, uint32_t i, uint32_t slot, uint32_t c0) {
@@ -187,12 +195,8 @@ __global__ __launch_bounds__(1024) void pack_kernel(uint32_t n_seqs, const uint3
     }
     const uint32_t code = range_error ? (uint32_t)(-LIA_E_PAGE_RANGE)
                           : error == 0xFFFFFFFFu ? 0u : (error & 15u);
-    if (code) {
-        // nothing downstream may run on a rejected batch
-        for (uint32_t b = t; b <= n_seqs; b += 1024) cu[b] = 0;
-        for (uint32_t r = t; r < total; r += 1024) slot_mapping[r] = kNone;
-    }
-    if (t == 0) *status = code;
+    if (code) reject(code); // nothing downstream may run on a rejected batch
+    else if (t == 0) *status = 0;
 }
 
 // Slot of append row r (slot_mapping[r], or the table's page of its position); kNone for

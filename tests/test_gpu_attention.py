@@ -74,7 +74,7 @@ def test_reference_known_answer_vectors(lia, wl):
     mx, mean = G.errors(got, ref)
     print(f"[case] reference vectors: max_abs={mx:.3e} mean_abs={mean:.3e} (reference bar 3e-5)",
           flush=True)
-    assert mx < 1e-3 and mean < 1e-4
+    assert mx < 3e-5 and mean < 1e-5  # the reference's own bar (llama_attention.rs:393)
 
 
 def test_mtp_verify_rows(lia, wl):
@@ -335,7 +335,9 @@ def test_f32_output_split_records_keep_f32_precision(lia, wl, O, kv):
     cmx, _ = G.errors(cpu, ref)
     print(f"[case] f32 out split kv={kv}: max_abs={mx:.3e} mean_abs={mean:.3e} "
           f"(oracle f32 split-K {cmx:.3e})", flush=True)
-    assert mx < 2e-3 and mean < 2e-4
+    # measured 2.2e-4 (bf16 pool) and 3.0e-5 (f16 pool): the 16-bit MFMA operands, not the
+    # records, set the error
+    assert mx < (5e-4 if kv == BF16 else 1e-4) and mean < (1e-4 if kv == BF16 else 1e-5)
 
 
 def test_f16_split_records_saturate_at_the_f16_maximum(lia, wl):
