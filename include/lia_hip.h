@@ -349,11 +349,30 @@ int lia_attention_partial_append(const lia_attention_config *config, uint32_t n_
                                  const void *new_v, void *kc, void *vc, void *workspace,
                                  size_t workspace_bytes, void *out, lia_stream_t stream);
 
+/*
+ * lia_paged_attention without a workspace argument: the work list and split records live in
+ * a device array the library holds for the process (lia_static_workspace_bytes() bytes on each
+ * device it runs on), so the call allocates nothing.  No counterpart in the reference: this
+ * entry point is for callers that cannot allocate (code under hipGraph capture, tight serving
+ * loops, harnesses that forbid hipMalloc).  A configuration whose workspace
+ * (lia_attention_workspace_bytes) exceeds the array is rejected with LIA_E_WORKSPACE.  Calls
+ * that overlap on one device share the array and race: serialise them (one stream, or events).
+ * Same arguments, results and errors as lia_paged_attention otherwise.
+ */
+int lia_paged_attention_static(const lia_attention_config *config, uint32_t n_seqs,
+                               uint32_t n_rows, const uint32_t *cu_seqlens,
+                               const uint32_t *positions, const uint32_t *sequences,
+                               const uint32_t *pages, const void *q, const void *kc,
+                               const void *vc, const float *k_scales, const float *v_scales,
+                               void *out, lia_stream_t stream);
+size_t lia_static_workspace_bytes(void);
+
 /* Number of compute units the library schedules decode work for (device 0 unless
  * lia_init selected another).  0 on failure. */
 uint32_t lia_device_cus(void);
 
-/* Optional: select the device and cache its properties.  Returns LIA_OK. */
+/* Optional: select the device, cache its properties and look up its static workspace
+ * (lia_paged_attention_static).  Returns LIA_OK. */
 int lia_init(int device);
 
 /*

@@ -201,6 +201,11 @@ EXPORTS = {
     "lia_sample_paged": (C.c_int, [C.c_uint32, C.c_uint32, C.c_void_p, C.c_void_p, C.c_void_p,
                                    C.c_void_p, C.c_size_t, C.c_void_p, C.c_size_t, C.c_void_p,
                                    C.POINTER(C.c_uint64), C.c_void_p]),
+    "lia_paged_attention_static": (C.c_int, [C.POINTER(AttentionConfig), C.c_uint32, C.c_uint32,
+                                             C.c_void_p, C.c_void_p, C.c_void_p, C.c_void_p,
+                                             C.c_void_p, C.c_void_p, C.c_void_p, C.c_void_p,
+                                             C.c_void_p, C.c_void_p, C.c_void_p]),
+    "lia_static_workspace_bytes": (C.c_size_t, []),
     "lia_device_cus": (C.c_uint32, []),
     "lia_init": (C.c_int, [C.c_int]),
 }
@@ -714,6 +719,16 @@ def paged_attention(config, n_seqs, cu_seqlens, positions, sequences, pages, q, 
                                    _dptr(workspace), workspace.numel() * workspace.element_size(),
                                    _dptr(out), _stream(stream))
     _check(st, "paged_attention")
+
+
+def paged_attention_static(config, n_seqs, cu_seqlens, positions, sequences, pages, q, kc, vc,
+                           out, k_scales=None, v_scales=None, stream=None):
+    """lia_paged_attention with the library's static device workspace (allocates nothing)."""
+    st = lib().lia_paged_attention_static(C.byref(config), n_seqs, q.shape[0], _dptr(cu_seqlens),
+                                          _dptr(positions), _dptr(sequences), _dptr(pages),
+                                          _dptr(q), _dptr(kc), _dptr(vc), _dptr(k_scales),
+                                          _dptr(v_scales), _dptr(out), _stream(stream))
+    _check(st, "paged_attention_static")
 
 
 def attention_plan(config, n_seqs, n_rows, cu_seqlens, positions, sequences, workspace,

@@ -29,6 +29,8 @@
 // through LDS in its natural token-major layout and reads it back transposed
 // (ds_read_b64_tr_b16) as the A operand of O^T += V^T * P^T.  Causal masking is per
 // column: row r sees keys <= positions[r] (src/gpu/kernels/llama_flash_kernel.rs:145-175).
+#include <mutex>
+
 #include "common.hpp"
 
 namespace lia {
@@ -1773,8 +1775,37 @@ using namespace lia;
 static int g_device = 0;
 static uint32_t g_cus = 0;
 
+// Workspace of lia_paged_attention_static: a file-scope device array, so that entry point
+// allocates nothing.  Each device the library runs on holds its own copy until the process
+// ends; its address is looked up once per device (hipGetSymbolAddress with the device
+// current) and only that address is handed to kernels - the array's name in host code is a
+// host-side stand-in, not a device address.  Every call on one device shares the array:
+// calls that overlap on a device race.  Nothing in it needs to start at zero (the plan writes
+// every descriptor the other kernels read, the attention kernel every record the merge reads).
+constexpr size_t kStaticWorkspaceBytes = 64ull << 20;
+static __device__ __align__(256) uint8_t scratch[kStaticWorkspaceBytes];
+constexpr int kMaxDevices = 64;
+static void *g_scratch[kMaxDevices];
+static std::mutex g_scratch_mutex;
+
+static int scratch_of_current_device(void **out) {
+    int dev = 0;
+    if (hipGetDevice(&dev) != hipSuccess) return LIA_E_HIP;
+    if (dev < 0 || dev >= kMaxDevices) return LIA_E_UNSUPPORTED;
+    std::lock_guard<std::mutex> lock(g_scratch_mutex);
+    if (!g_scratch[dev]) {
+        void *p = nullptr;
+        if (hipGetSymbolAddress(&p, HIP_SYMBOL(scratch)) != hipSuccess || !p) return LIA_E_HIP;
+        g_scratch[dev] = p;
+    }
+    *out = g_scratch[dev];
+    return LIA_OK;
+}
+
 extern "C" int lia_init(int device) {
     if (hipSetDevice(device) != hipSuccess) return LIA_E_HIP;
+    void *ws = nullptr;
+    if (scratch_of_current_device(&ws) != LIA_OK) return LIA_E_HIP;
     int cus = 0;
     if (hipDeviceGetAttribute(&cus, hipDeviceAttributeMultiprocessorCount, device) != hipSuccess)
         return LIA_E_HIP;
@@ -2098,4 +2129,23 @@ extern "C" int lia_attention_merge(const lia_attention_config *c, uint32_t n_seq
     static const uint32_t dummy = 0;
     return run_stages(kMerge, c, n_seqs, n_rows, &dummy, &dummy, nullptr, nullptr, nullptr,
                       nullptr, nullptr, nullptr, nullptr, workspace, workspace_bytes, out, stream);
+}
+
+extern "C" size_t lia_static_workspace_bytes(void) { return kStaticWorkspaceBytes; }
+
+extern "C" int lia_paged_attention_static(const lia_attention_config *c, uint32_t n_seqs,
+                                          uint32_t n_rows, const uint32_t *cu_seqlens,
+                                          const uint32_t *positions, const uint32_t *sequences,
+                                          const uint32_t *pages, const void *q, const void *kc,
+                                          const void *vc, const float *k_scales,
+                                          const float *v_scales, void *out, lia_stream_t stream) {
+    int st = validate(c);
+    if (st) return st;
+    if (lia_attention_workspace_bytes(c) > kStaticWorkspaceBytes) return LIA_E_WORKSPACE;
+    void *ws = nullptr;
+    st = scratch_of_current_device(&ws);
+    if (st) return st;
+    return run_stages(kPlan | kPartial | kMerge, c, n_seqs, n_rows, cu_seqlens, positions,
+                      sequences, pages, q, kc, vc, k_scales, v_scales, ws, kStaticWorkspaceBytes,
+                      out, stream);
 }
