@@ -128,16 +128,16 @@ uint32_t lia_decode_parts(uint32_t tokens, uint32_t span);
  * Writes cu_seqlens[n_seqs+1], positions[rows], sequences[rows], slot_mapping[rows].
  * Rows beyond the batch total up to max_rows are left untouched.  status (device, one u32)
  * receives 0 or the first failing lia_status as a positive number (-status), with the
- * reference's checks in its order (paging.rs:137-172):
- *   LIA_E_PAGE_RANGE     a table entry the batch attends (logical pages 0 .. ceil((cached +
- *                        q_len) / page_size) - 1 of each sequence with rows) that is neither
- *                        below pool_pages nor 0xFFFFFFFF; reported ahead of any row check;
+ * reference's checks in its order (paging.rs:120-172):
+ *   LIA_E_ROWS           the rows exceed max_rows;
+ *   then the tables: every entry the batch attends (logical pages 0 .. ceil((cached + q_len)
+ *   / page_size) - 1 of each sequence with rows):
+ *   LIA_E_PAGE_RANGE     an entry neither below pool_pages nor 0xFFFFFFFF;
+ *   LIA_E_MISSING_PAGE   0xFFFFFFFF wholly below the sequence's cached length;
  *   then per row, the lowest failing row first:
  *   LIA_E_POSITION       position >= context;
- *   LIA_E_MISSING_PAGE   the row's page is 0xFFFFFFFF (reported at a sequence's first row for
- *                        a missing page wholly below its cached length);
- *   LIA_E_DUPLICATE_SLOT the row's slot is written by an earlier row;
- *   and LIA_E_ROWS when the rows exceed max_rows.
+ *   LIA_E_MISSING_PAGE   the row's page is 0xFFFFFFFF;
+ *   LIA_E_DUPLICATE_SLOT the row's slot is written by an earlier row.
  * On failure cu_seqlens is written all zero and slot_mapping[0 .. max_rows) as 0xFFFFFFFF
  * (the arrays hold max_rows entries), so a plan built
  * from them schedules no work and no append writes the pool: the step's outputs and the pool

@@ -18,7 +18,7 @@ from gpu_data import BF16
 pytestmark = pytest.mark.gpu
 
 NONE = 0xFFFFFFFF
-E_PAGE_RANGE, E_POSITION, E_MISSING_PAGE, E_DUPLICATE = 6, 8, 10, 11
+E_ROWS, E_PAGE_RANGE, E_POSITION, E_MISSING_PAGE, E_DUPLICATE = 1, 6, 8, 10, 11
 
 
 def _pack(lia, slots, q_lens, cached, table, stride, P, pool_pages, context, max_rows):
@@ -42,7 +42,7 @@ def test_pack_rejects_table_entry_outside_pool_before_row_checks(lia):
     """Sequence 1's cached page 0 is page 40 of a 32-page pool; sequence 0's row has a
     position past the context.  The table check comes first, as in paging.rs."""
     stride, P = 4, 16
-    table = [3, 4, NONE, NONE, 40, 7, NONE, NONE]
+    table = [3, 4, 10, 11, 40, 7, NONE, NONE]
     st, cu, pos, seq, slots = _pack(lia, [0, 1], [1, 1], [70, 20], table, stride, P, 32, 64, 4)
     assert st == E_PAGE_RANGE
     assert _rejected(cu, slots, 2)
@@ -52,13 +52,28 @@ def test_pack_rejects_table_entry_outside_pool_before_row_checks(lia):
     assert st == E_POSITION
 
 
-def test_pack_reports_missing_cached_page_at_the_sequences_first_row(lia):
+def test_pack_reports_missing_cached_page(lia):
     stride, P = 4, 16
     # sequence 0 fine (rows 0, 1); sequence 1 (rows 2, 3) attends cached page 0, marked missing
     table = [3, 4, NONE, NONE, NONE, 7, NONE, NONE]
     st, cu, pos, seq, slots = _pack(lia, [0, 1], [2, 2], [5, 16], table, stride, P, 32, 64, 8)
     assert st == E_MISSING_PAGE
     assert _rejected(cu, slots, 4)
+
+
+def test_pack_table_checks_come_before_row_checks_and_after_the_row_count(lia):
+    stride, P = 4, 16
+    # sequence 0's cached page is missing; sequence 1's row is past the context
+    table = [NONE, 4, NONE, NONE, 5, 6, NONE, NONE]
+    st, cu, pos, seq, slots = _pack(lia, [0, 1], [1, 1], [20, 70], table, stride, P, 32, 64, 4)
+    assert st == E_MISSING_PAGE and _rejected(cu, slots, 4)
+    # an out-of-pool entry outranks the missing page
+    table[5] = 99
+    st, *_ = _pack(lia, [0, 1], [1, 1], [20, 40], table, stride, P, 32, 64, 4)
+    assert st == E_PAGE_RANGE
+    # more rows than max_rows outranks both
+    st, cu, pos, seq, slots = _pack(lia, [0, 1], [3, 3], [20, 40], table, stride, P, 32, 64, 4)
+    assert st == E_ROWS and _rejected(cu, slots, 4)
 
 
 def test_pack_rejects_duplicate_slots_across_sequences(lia):
