@@ -1185,7 +1185,11 @@ template <int D, int KVT>
 struct WState {
     u32x4 qr[WCfg<D>::NTW][WCfg<D>::KT]; // Q^T operands of the wave's column tiles
     uint32_t lo, lim[WCfg<D>::NTW];
-    float m[WCfg<D>::NTW], l[WCfg<D>::NTW];
+    // per column: reference maximum of the scaled scores in the log2 domain (0 before the
+    // first live key) and the exponent above which it is raised (-inf before the first live
+    // key, then 2^8)
+    float m[WCfg<D>::NTW], thr[WCfg<D>::NTW];
+    f32x4 l[WCfg<D>::NTW];               // the mass, every row of the tile (MFMA against ones)
     f32x4 o[WCfg<D>::NTW][WCfg<D>::DT];
 };
 
@@ -1224,81 +1228,120 @@ __device__ __forceinline__ void load_q_full(const AttnParams &p, uint32_t row, u
     }
 }
 
-// One chunk (32 tokens at t) for this wave's 32 columns, from stages kst / vst.
+// One chunk (32 tokens at t) for this wave's 16 columns, from stages kst / vst.  `masked`: some
+// key of the chunk is outside some column's live range (the range's unaligned start, the
+// causal diagonal, the range end); only then are the scores masked, in a branch of their
+// own.  Otherwise every key is live for every valid column (padding columns attend zero
+// queries and are never written out).
+//
+// Online softmax in the log2 domain with a lazily raised reference m per column: the
+// exponent of a score s is e = s * scale_log2 - m (one fma), and the reference is raised only
+// when some lane of the wave holds an e above its column's threshold - 2^8 once the column
+// has a live key, any live key before - so the exponentials stay <= 2^8.  Only then does the
+// wave reduce the maxima across lanes and rescale O and the mass.  The mass is accumulated by
+// the matrix unit: an MFMA of a ones operand against P^T sums each column over the chunk's
+// keys, with the same rounded weights as O.
 template <int D, int KVT>
 __device__ __forceinline__ void wide_compute(const AttnParams &p, uint32_t t, WState<D, KVT> &st,
-                                             const uint16_t *kst, const uint16_t *vst) {
+                                             const uint16_t *kst, const uint16_t *vst, bool masked) {
     using W = WCfg<D>;
     constexpr bool MB = KVT == LIA_BF16;
     const uint32_t lane = lane_id(), g = lane >> 4, li = lane & 15;
     // S^T tiles: tokens 16j + (rows), columns 16nt + li
     constexpr int NTW = W::NTW;
+    // LDS byte offsets of the operand reads.  K: token row 16j + li, 16-byte chunk 4ks + g at
+    // position (4ks + g) ^ s, s = li % chunks-per-row (the staging swizzle) - i.e. kb ^ 64 ks
+    // with the row and the ks-independent bits in kb (row 16 + li swizzles like row li).  The
+    // XOR form keeps one address register per operand and the stage base an immediate.
+    const uint32_t sk = swz_k<D>(li);
+    const uint32_t kb = li * 2 * D + 64 * (sk >> 2) + 16 * (g ^ (sk & 3));
+    // operand reads one step ahead of their MFMAs (two buffers), so a read's LDS latency
+    // overlaps the previous MFMA instead of stalling the wave
+    auto kread = [&](int i) { // i = 2 ks + j: the two token tiles' chains alternate
+        return *(const u32x4 *)((const uint8_t *)kst + (kb ^ (64 * (i / 2))) + (i % 2) * 32 * D);
+    };
     f32x4 acc[2][NTW];
 #pragma unroll
-    for (int j = 0; j < 2; j++) {
+    for (int j = 0; j < 2; j++)
 #pragma unroll
         for (int nt = 0; nt < NTW; nt++) acc[j][nt] = f32x4{0.0f, 0.0f, 0.0f, 0.0f};
-        const uint32_t tr = 16 * j + li;
+    u32x4 ka[2];
+    ka[0] = kread(0);
 #pragma unroll
-        for (int ks = 0; ks < W::KT; ks++) {
-            const uint32_t c = 4 * ks + g;
-            const u32x4 a = *(const u32x4 *)(kst + tr * D + (c ^ swz_k<D>(tr)) * 8);
+    for (int i = 0; i < 2 * W::KT; i++) {
+        if (i + 1 < 2 * W::KT) ka[(i + 1) & 1] = kread(i + 1);
+        const int j = i % 2, ks = i / 2;
 #pragma unroll
-            for (int nt = 0; nt < NTW; nt++) acc[j][nt] = mfma16x16x32<MB>(a, st.qr[nt][ks], acc[j][nt]);
-        }
+        for (int nt = 0; nt < NTW; nt++) acc[j][nt] = mfma16x16x32<MB>(ka[i & 1], st.qr[nt][ks], acc[j][nt]);
+    }
+    if (masked) {
+#pragma unroll
+        for (int j = 0; j < 2; j++)
+#pragma unroll
+            for (int nt = 0; nt < NTW; nt++)
+#pragma unroll
+                for (int i = 0; i < 4; i++)
+                    if (t + 16 * j + 4 * g + i - st.lo >= st.lim[nt]) acc[j][nt][i] = -INFINITY;
     }
     u32x4 pb[NTW];
 #pragma unroll
     for (int nt = 0; nt < NTW; nt++) {
-        float x[2][4];
-        float mx = -INFINITY;
+        float e[2][4];
 #pragma unroll
         for (int j = 0; j < 2; j++)
 #pragma unroll
-            for (int i = 0; i < 4; i++) {
-                const uint32_t tok = t + 16 * j + 4 * g + i;
-                const float v = tok - st.lo < st.lim[nt] ? acc[j][nt][i] * p.scale_log2 : -INFINITY;
-                x[j][i] = v;
-                mx = fmaxf(mx, v);
-            }
-        mx = rows_max(mx);
-        const bool first = st.m[nt] == -INFINITY;
-        const bool raise = !first && mx > st.m[nt] + 8.0f;
-        if (__builtin_amdgcn_ballot_w64(raise)) {
-            const float factor = raise ? fast_exp2(st.m[nt] - mx) : 1.0f;
-            st.l[nt] *= factor;
+            for (int i = 0; i < 4; i++) e[j][i] = __builtin_fmaf(acc[j][nt][i], p.scale_log2, -st.m[nt]);
+        float mx = fmaxf(fmaxf(fmaxf(e[0][0], e[0][1]), fmaxf(e[0][2], e[0][3])),
+                         fmaxf(fmaxf(e[1][0], e[1][1]), fmaxf(e[1][2], e[1][3])));
+        if (__builtin_amdgcn_ballot_w64(mx > st.thr[nt])) { // wave-uniform: rare after the first chunk
+            mx = rows_max(mx);
+            if (mx > st.thr[nt]) { // the same in the 4 lanes of the column
+                const float factor = fast_exp2(-mx); // 0 before the column's first live key
+                st.l[nt] *= factor;
 #pragma unroll
-            for (int n = 0; n < W::DT; n++) st.o[nt][n] *= factor;
+                for (int n = 0; n < W::DT; n++) st.o[nt][n] *= factor;
+                st.m[nt] += mx;
+                st.thr[nt] = 8.0f;
+#pragma unroll
+                for (int j = 0; j < 2; j++)
+#pragma unroll
+                    for (int i = 0; i < 4; i++) e[j][i] -= mx;
+            }
         }
-        if (first || raise) st.m[nt] = mx;
-        const float muse = st.m[nt] == -INFINITY ? 0.0f : st.m[nt];
         float pr[2][4];
-        float sum = 0.0f;
 #pragma unroll
         for (int j = 0; j < 2; j++)
 #pragma unroll
-            for (int i = 0; i < 4; i++) {
-                const float e = fast_exp2(x[j][i] - muse);
-                sum += e;
-                pr[j][i] = e;
-            }
-        st.l[nt] += sum;
+            for (int i = 0; i < 4; i++) pr[j][i] = fast_exp2(e[j][i]);
         pb[nt] = u32x4{pack2<MB>(pr[0][0], pr[0][1]), pack2<MB>(pr[0][2], pr[0][3]),
                        pack2<MB>(pr[1][0], pr[1][1]), pack2<MB>(pr[1][2], pr[1][3])};
     }
-    // O^T += V^T P^T: V^T rows 16n .. 16n+15, k slots = tokens {4g..4g+3, 16+4g..16+4g+3}
-#pragma unroll
-    for (int n = 0; n < W::DT; n++) {
-        const uint32_t r0 = 4 * g + li / 4, c = 2 * n + ((li & 3) >> 1);
-        const uint16_t *a0p = vst + r0 * D + (c ^ swz_v<D>(r0)) * 8 + (li & 1) * 4;
-        const uint16_t *a1p = a0p + 16 * D; // row r0 + 16: same swizzle
+    // O^T += V^T P^T: V^T rows 16n .. 16n+15, k slots = tokens {4g..4g+3, 16+4g..16+4g+3}.
+    // The transpose read of row r0 = 4g + li/4, chunk 2n + b at position (2n + b) ^ swz_v(r0),
+    // is at vb ^ 32 n (row r0 + 16 swizzles like r0).
+    const uint32_t r0 = 4 * g + li / 4;
+    const uint32_t vb = r0 * 2 * D + 16 * ((li & 3) >> 1) + 8 * (li & 1) + 16 * swz_v<D>(r0);
+    auto vread = [&](int n) {
+        const uint8_t *a0p = (const uint8_t *)vst + (vb ^ (32 * n));
+        const uint8_t *a1p = a0p + 32 * D; // row r0 + 16
         const s16x4 a0 = __builtin_amdgcn_ds_read_tr16_b64_v4i16((__attribute__((address_space(3))) s16x4 *)(a0p));
         const s16x4 a1 = __builtin_amdgcn_ds_read_tr16_b64_v4i16((__attribute__((address_space(3))) s16x4 *)(a1p));
         const u32x2 b0 = __builtin_bit_cast(u32x2, a0), b1 = __builtin_bit_cast(u32x2, a1);
-        const u32x4 vt = u32x4{b0.x, b0.y, b1.x, b1.y};
+        return u32x4{b0.x, b0.y, b1.x, b1.y};
+    };
+    u32x4 vt[2];
+    vt[0] = vread(0);
 #pragma unroll
-        for (int nt = 0; nt < NTW; nt++) st.o[nt][n] = mfma16x16x32<MB>(vt, pb[nt], st.o[nt][n]);
+    for (int n = 0; n < W::DT; n++) {
+        if (n + 1 < W::DT) vt[(n + 1) & 1] = vread(n + 1);
+#pragma unroll
+        for (int nt = 0; nt < NTW; nt++) st.o[nt][n] = mfma16x16x32<MB>(vt[n & 1], pb[nt], st.o[nt][n]);
     }
+    // the mass: every row of the ones tile is the column's sum of this chunk's weights
+    constexpr uint32_t one2 = MB ? 0x3F803F80u : 0x3C003C00u;
+    const u32x4 ones = u32x4{one2, one2, one2, one2};
+#pragma unroll
+    for (int nt = 0; nt < NTW; nt++) st.l[nt] = mfma16x16x32<MB>(ones, pb[nt], st.l[nt]);
 }
 
 // One step: wait for chunk i (this wave's loads; the next chunk's loads stay in flight),
@@ -1306,27 +1349,32 @@ __device__ __forceinline__ void wide_compute(const AttnParams &p, uint32_t t, WS
 // Restrict stages: the compiler may keep the new loads in flight across the reads.
 constexpr int kWideStages = 3;
 
+// Chunk t needs the causal / range mask unless [t, t + 32) lies in [free_lo, free_hi), the
+// keys live for every valid column of the unit.
 template <int D, int KVT>
 __device__ __forceinline__ void wide_step(const AttnParams &p, uint32_t tn, const TilePages &tpn,
                                           uint16_t *__restrict__ kn, uint16_t *__restrict__ vn,
                                           uint32_t tc, const uint16_t *__restrict__ kc,
                                           const uint16_t *__restrict__ vc, const uint8_t *kbase,
                                           const uint8_t *vbase, uint32_t hk, uint32_t wave,
-                                          bool active, WState<D, KVT> &st) {
+                                          bool active, WState<D, KVT> &st, uint32_t free_lo,
+                                          uint32_t free_hi) {
     wait_vmcnt<(kWideStages - 2) * kWideLoads<D>>(); // the later chunks' loads stay in flight
     lds_barrier();
     wide_load<D>(p, tn, tpn, kbase, vbase, hk, wave, kn, vn);
-    if (active) wide_compute<D, KVT>(p, tc, st, kc, vc);
+    if (active) wide_compute<D, KVT>(p, tc, st, kc, vc, !(tc >= free_lo && tc + 32 <= free_hi));
 }
 
-// Keys [s_lo, s_hi) of one source into the running state (windows of at most 64 pages).
+// Keys [s_lo, s_hi) of one source into the running state (windows of at most 64 pages), through
+// three LDS stages (measured: a ring of four or five is slower).
 template <int D, int KVT>
 __device__ __forceinline__ void wide_range(const AttnParams &p, const uint8_t *kbase,
                                            const uint8_t *vbase, const uint32_t *table,
                                            uint32_t s_lo, uint32_t s_hi, bool use_pre, uint4 pre,
                                            uint32_t hk, uint32_t wave, bool active,
                                            WState<D, KVT> &st, uint16_t *k0, uint16_t *k1,
-                                           uint16_t *k2, uint16_t *v0, uint16_t *v1, uint16_t *v2) {
+                                           uint16_t *k2, uint16_t *v0, uint16_t *v1, uint16_t *v2,
+                                           uint32_t free_lo, uint32_t free_hi) {
     const uint32_t shift = p.page_shift;
     const uint32_t page_limit = (s_hi + (1u << shift) - 1) >> shift;
     for (uint32_t wbeg = s_lo & ~31u; wbeg < s_hi;) {
@@ -1349,13 +1397,13 @@ __device__ __forceinline__ void wide_range(const AttnParams &p, const uint8_t *k
         for (uint32_t t = wbeg;; t += 96) {
             // loads past wend carry no traffic
             wide_step<D, KVT>(p, t + 64, tile_pages<false>(win, t + 64, shift, wend), k2, v2, t, k0,
-                              v0, kbase, vbase, hk, wave, active, st);
+                              v0, kbase, vbase, hk, wave, active, st, free_lo, free_hi);
             if (t + 32 >= wend) break;
             wide_step<D, KVT>(p, t + 96, tile_pages<false>(win, t + 96, shift, wend), k0, v0, t + 32,
-                              k1, v1, kbase, vbase, hk, wave, active, st);
+                              k1, v1, kbase, vbase, hk, wave, active, st, free_lo, free_hi);
             if (t + 64 >= wend) break;
             wide_step<D, KVT>(p, t + 128, tile_pages<false>(win, t + 128, shift, wend), k1, v1, t + 64,
-                              k2, v2, kbase, vbase, hk, wave, active, st);
+                              k2, v2, kbase, vbase, hk, wave, active, st, free_lo, free_hi);
             if (t + 96 >= wend) break;
         }
         wait_vmcnt<0>(); // the trailing (empty) loads target stages about to be reused
@@ -1406,13 +1454,17 @@ __global__ __launch_bounds__(512, 4) void wide_kernel(AttnParams p) {
             const uint32_t ri = valid ? col / p.group : 0;
             climit[nt] = valid ? pos0 + ri + 1 : 0;
             load_q_full<D, KVT>(p, ud.rowbeg + ri, hk * p.group + col % p.group, valid, st.qr[nt]);
-            st.m[nt] = -INFINITY;
-            st.l[nt] = 0.0f;
+            st.m[nt] = 0.0f;
+            st.thr[nt] = -INFINITY;
+            st.l[nt] = f32x4{0.0f, 0.0f, 0.0f, 0.0f};
 #pragma unroll
             for (int n = 0; n < W::DT; n++) st.o[nt][n] = f32x4{0.0f, 0.0f, 0.0f, 0.0f};
         }
         const uint32_t a = lo - bs, e = seg_end - bs;
         auto key_of = [&](uint32_t i) { return i < cb ? 32 * i : min(kcache + 32 * (i - cb), kend); };
+        // per column the live keys of [r_lo, r_hi); keys [r_lo, free_hi) are live for every
+        // valid column (those of the unit's first row, whose causal limit is the lowest)
+        uint32_t free_hi = 0;
         auto set_limits = [&](uint32_t r_lo, uint32_t r_hi, uint32_t origin) {
             st.lo = r_lo;
 #pragma unroll
@@ -1420,19 +1472,21 @@ __global__ __launch_bounds__(512, 4) void wide_kernel(AttnParams p) {
                 const int w = (int)min(climit[nt] - origin, r_hi) - (int)r_lo;
                 st.lim[nt] = climit[nt] && w > 0 ? (uint32_t)w : 0u;
             }
+            const int w0 = (int)min(pos0 + 1 - origin, r_hi) - (int)r_lo;
+            free_hi = r_lo + (w0 > 0 ? (uint32_t)w0 : 0u);
         };
         const uint8_t *kpool = (const uint8_t *)p.kc, *vpool = (const uint8_t *)p.vc;
         if (!fused) {
             const uint32_t r_lo = key_of(a), r_hi = min(key_of(e), kend);
             set_limits(r_lo, r_hi, 0);
             wide_range<D, KVT>(p, kpool, vpool, table, r_lo, r_hi, use_pre, wd.pre, hk, wave, active,
-                               st, k0, k1, k2, v0, v1, v2);
+                               st, k0, k1, k2, v0, v1, v2, r_lo, free_hi);
         } else {
             if (a < cb) {
                 const uint32_t r_lo = 32 * a, r_hi = min(32 * min(e, cb), kcache);
                 set_limits(r_lo, r_hi, 0);
                 wide_range<D, KVT>(p, kpool, vpool, table, r_lo, r_hi, use_pre, wd.pre, hk, wave,
-                                   active, st, k0, k1, k2, v0, v1, v2);
+                                   active, st, k0, k1, k2, v0, v1, v2, r_lo, free_hi);
             }
             if (e > cb) {
                 const uint32_t r0 = ud.rowbeg - (pos0 - kcache);
@@ -1440,7 +1494,8 @@ __global__ __launch_bounds__(512, 4) void wide_kernel(AttnParams p) {
                 set_limits(r_lo, r_hi, kcache);
                 wide_range<D, KVT>(p, (const uint8_t *)p.newk + (size_t)r0 * row_bytes,
                                    (const uint8_t *)p.newv + (size_t)r0 * row_bytes, nullptr, r_lo,
-                                   r_hi, false, wd.pre, hk, wave, active, st, k0, k1, k2, v0, v1, v2);
+                                   r_hi, false, wd.pre, hk, wave, active, st, k0, k1, k2, v0, v1, v2,
+                                   r_lo, free_hi);
             }
         }
 
@@ -1448,8 +1503,7 @@ __global__ __launch_bounds__(512, 4) void wide_kernel(AttnParams p) {
         const uint32_t rec = (wd.flags >> 8) + u;
 #pragma unroll
         for (int nt = 0; nt < NTW; nt++) {
-            float lt = st.l[nt];
-            lt = rows_sum(lt);
+            const float lt = st.l[nt][0];
             const uint32_t col = 16 * NTW * wave + 16 * nt + li;
             if (col >= ncols) continue;
             const uint32_t row = ud.rowbeg + col / p.group;
@@ -1922,6 +1976,7 @@ static int validate(const lia_attention_config *c) {
     if (c->kv_dtype != LIA_F16 && c->kv_dtype != LIA_BF16 && c->kv_dtype != LIA_FP8_E4M3)
         return LIA_E_UNSUPPORTED;
     if (c->stride == 0 || c->max_seqs == 0 || c->max_rows == 0) return LIA_E_ARG;
+    if (!(c->scale > 0.0f) || !(c->scale < INFINITY)) return LIA_E_ARG; // the kernels rely on scale > 0
     return LIA_OK;
 }
 
