@@ -172,3 +172,11 @@ def test_stage_entry_points_ignore_what_they_do_not_read(lia):
     assert _plan(lia, cfg, a) == E_WORKSPACE
     a = _args(lia, cfg, cu=None, positions=None, sequences=None, pages=None, q=None, ws_bytes=1)
     assert _merge(lia, cfg, a) == E_WORKSPACE
+
+
+@pytest.mark.parametrize("scale", [0.0, -0.088, float("inf"), float("nan")])
+def test_scale_must_be_positive_and_finite(lia, scale):
+    """The kernels take maxima of raw scores and scale them afterwards, which needs a
+    positive scale (the reference's is 1/sqrt(head_dim))."""
+    cfg = _cfg(lia, scale=scale)
+    assert _paged(lia, cfg, _args(lia, cfg)) == E_ARG
