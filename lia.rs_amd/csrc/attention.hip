@@ -692,7 +692,15 @@ struct State {
     u32x4 qr[NT][Cfg<D, KVT>::KS];
     uint32_t lo;       // first key of the current range (wave-uniform)
     uint32_t lim[NT];  // per column: live keys of the range, counted from lo
-    float m[NT], l[NT];
+    uint32_t free_lo, free_hi; // keys live for every valid column of the unit (wave-uniform)
+    // per column: reference maximum of the scaled scores in the log2 domain (0 before the
+    // first live key) and the exponent above which it is raised (-inf before the first live
+    // key, then 2^8)
+    float m[NT], thr[NT];
+    // the mass: every row of an MFMA tile against ones on 16-bit pools; on FP8 pools (whose
+    // weights carry the V page scale) element 0 holds this lane's share, summed across lanes
+    // at the end
+    f32x4 l[NT];
     f32x4 o[NT][Cfg<D, KVT>::DTW];
 };
 
@@ -754,6 +762,13 @@ __device__ __forceinline__ void compute_chunk(const AttnParams &p, const Chunk<D
     // Only the LDS score exchange needs ordering (a full __syncthreads would also drain the
     // prefetch loads).
     lds_barrier();
+    // Online softmax per column nt*16 + li over tokens t + 16j + 4g + i (live when lo <= token
+    // < lo + lim): masked only when the chunk leaves [free_lo, free_hi); the exponent of a
+    // score is one fma against a lazily raised reference, which only a ballot of lanes above
+    // its threshold (2^8 once the column has a live key, any live key before) makes the wave
+    // reduce across lanes and rescale.  Numerator and denominator share the reference, so the
+    // normalised result is unchanged.
+    const bool masked = !(t >= st.free_lo && t + 32 <= st.free_hi);
 #pragma unroll
     for (int nt = 0; nt < NT; nt++) {
         f32x4 s[2];
@@ -763,44 +778,51 @@ __device__ __forceinline__ void compute_chunk(const AttnParams &p, const Chunk<D
 #pragma unroll
             for (int w = 1; w < C::WAVES; w++) s[j] += sx[((w * NT + nt) * 2 + j) * 64 + lane];
         }
-        // Online softmax for column nt*16 + li over tokens t + 16j + 4g + i (live when
-        // lo <= token < lo + lim, one unsigned compare), with a lazily
-        // updated reference maximum: exponentials are taken against m, which is raised
-        // (and O, l rescaled) only when a score exceeds it by more than 2^8.  Numerator
-        // and denominator share the reference, so the normalised result is unchanged.
-        float x[2][4];
-        float mx = -INFINITY;
+        float e[2][4];
 #pragma unroll
         for (int j = 0; j < 2; j++)
 #pragma unroll
-            for (int i = 0; i < 4; i++) {
-                const uint32_t tok = t + 16 * j + 4 * g + i;
-                const float v = tok - st.lo < st.lim[nt] ? s[j][i] * kscale[j] : -INFINITY;
-                x[j][i] = v;
-                mx = fmaxf(mx, v);
-            }
-        mx = rows_max(mx);
-        const bool first = st.m[nt] == -INFINITY;
-        const bool raise = !first && mx > st.m[nt] + 8.0f;
-        if (__builtin_amdgcn_ballot_w64(raise)) { // wave-uniform: rare after the first chunk
-            const float factor = raise ? fast_exp2(st.m[nt] - mx) : 1.0f;
-            st.l[nt] *= factor;
+            for (int i = 0; i < 4; i++) e[j][i] = __builtin_fmaf(s[j][i], kscale[j], -st.m[nt]);
+        // masked after the scaling: a tile with no live key has scale 0 on FP8 pools
+        if (masked) {
 #pragma unroll
-            for (int n = 0; n < C::DTW; n++) st.o[nt][n] *= factor;
+            for (int j = 0; j < 2; j++)
+#pragma unroll
+                for (int i = 0; i < 4; i++)
+                    if (t + 16 * j + 4 * g + i - st.lo >= st.lim[nt]) e[j][i] = -INFINITY;
         }
-        if (first || raise) st.m[nt] = mx;
-        const float muse = st.m[nt] == -INFINITY ? 0.0f : st.m[nt];
+        float mx = fmaxf(fmaxf(fmaxf(e[0][0], e[0][1]), fmaxf(e[0][2], e[0][3])),
+                         fmaxf(fmaxf(e[1][0], e[1][1]), fmaxf(e[1][2], e[1][3])));
+        if (__builtin_amdgcn_ballot_w64(mx > st.thr[nt])) { // wave-uniform: rare after the first chunk
+            mx = rows_max(mx);
+            if (mx > st.thr[nt]) { // the same in the 4 lanes of the column
+                const float factor = fast_exp2(-mx); // 0 before the column's first live key
+                st.l[nt] *= factor;
+#pragma unroll
+                for (int n = 0; n < C::DTW; n++) st.o[nt][n] *= factor;
+                st.m[nt] += mx;
+                st.thr[nt] = 8.0f;
+#pragma unroll
+                for (int j = 0; j < 2; j++)
+#pragma unroll
+                    for (int i = 0; i < 4; i++) e[j][i] -= mx;
+            }
+        }
         float pr[2][4];
         float sum = 0.0f;
 #pragma unroll
         for (int j = 0; j < 2; j++)
 #pragma unroll
             for (int i = 0; i < 4; i++) {
-                const float e = fast_exp2(x[j][i] - muse);
-                sum += e;
-                pr[j][i] = e * vscale[j];
+                const float x = fast_exp2(e[j][i]);
+                if constexpr (C::FP8) {
+                    sum += x;
+                    pr[j][i] = x * vscale[j];
+                } else {
+                    pr[j][i] = x;
+                }
             }
-        st.l[nt] += sum;
+        if constexpr (C::FP8) st.l[nt][0] += sum;
         const u32x4 pb = u32x4{pack2<C::MBF16>(pr[0][0], pr[0][1]), pack2<C::MBF16>(pr[0][2], pr[0][3]),
                                pack2<C::MBF16>(pr[1][0], pr[1][1]), pack2<C::MBF16>(pr[1][2], pr[1][3])};
 #pragma unroll
@@ -816,6 +838,11 @@ __device__ __forceinline__ void compute_chunk(const AttnParams &p, const Chunk<D
                 (__attribute__((address_space(3))) s16x4 *)(r1));
             u32x2 b0 = __builtin_bit_cast(u32x2, a0), b1 = __builtin_bit_cast(u32x2, a1);
             st.o[nt][n] = mfma16x16x32<C::MBF16>(u32x4{b0.x, b0.y, b1.x, b1.y}, pb, st.o[nt][n]);
+        }
+        if constexpr (!C::FP8) {
+            // the mass: the column's sum of this chunk's (rounded) weights, in every tile row
+            constexpr uint32_t one2 = C::MBF16 ? 0x3F803F80u : 0x3C003C00u;
+            st.l[nt] = mfma16x16x32<C::MBF16>(u32x4{one2, one2, one2, one2}, pb, st.l[nt]);
         }
     }
 }
@@ -969,14 +996,15 @@ __device__ __forceinline__ void store_record(const AttnParams &p, size_t rb, con
     }
 }
 
-// At most 6 (16-bit pools) or 8 (FP8) decode waves run per CU, under 2 per SIMD, so the
-// kernel may use the registers of 3 waves per SIMD (168) instead of squeezing into 4's (128).
-constexpr int kMinWavesPerEU = 3;
+// At most 6 (16-bit pools) or 8 (FP8) decode waves run per CU, so the kernel may use the
+// registers of 3 (168) or 2 (256) waves per SIMD instead of squeezing into 4's (128).
+template <int KVT>
+constexpr int kMinWavesPerEU = KVT == LIA_FP8_E4M3 ? 2 : 3;
 
 // The workgroup-size bound (D/32 waves) is looser than the D/SW waves launched: the
 // exact bound changes register allocation and measured 1 % slower on a batch-8 bf16 decode.
 template <int D, int NT, int KVT>
-__global__ __launch_bounds__(D / 32 * 64, kMinWavesPerEU) void attention_kernel(AttnParams p) {
+__global__ __launch_bounds__(D / 32 * 64, kMinWavesPerEU<KVT>) void attention_kernel(AttnParams p) {
     using C = Cfg<D, KVT>;
     constexpr uint32_t COLS = 16 * NT;
     // Two distinct LDS objects for the two V stages, so the compiler can tell a transpose
@@ -1026,8 +1054,9 @@ __global__ __launch_bounds__(D / 32 * 64, kMinWavesPerEU) void attention_kernel(
 #pragma unroll
             for (int ks = 0; ks < C::KS; ks++)
                 st.qr[nt][ks] = load_q<D, KVT>(p, ud.rowbeg + ri, hk * p.group + col % p.group, valid, wave, ks);
-            st.m[nt] = -INFINITY;
-            st.l[nt] = 0.0f;
+            st.m[nt] = 0.0f;
+            st.thr[nt] = -INFINITY;
+            st.l[nt] = f32x4{0.0f, 0.0f, 0.0f, 0.0f};
 #pragma unroll
             for (int n = 0; n < C::DTW; n++) st.o[nt][n] = f32x4{0.0f, 0.0f, 0.0f, 0.0f};
         }
@@ -1042,6 +1071,10 @@ __global__ __launch_bounds__(D / 32 * 64, kMinWavesPerEU) void attention_kernel(
                 const int w = (int)min(climit[nt] - origin, r_hi) - (int)r_lo;
                 st.lim[nt] = climit[nt] && w > 0 ? (uint32_t)w : 0u;
             }
+            // keys live for every valid column: those of the unit's first row
+            const int w0 = (int)min(pos0 + 1 - origin, r_hi) - (int)r_lo;
+            st.free_lo = r_lo;
+            st.free_hi = r_lo + (w0 > 0 ? (uint32_t)w0 : 0u);
         };
         const uint8_t *kpool = (const uint8_t *)p.kc, *vpool = (const uint8_t *)p.vc;
         if (!fused) {
@@ -1074,8 +1107,7 @@ __global__ __launch_bounds__(D / 32 * 64, kMinWavesPerEU) void attention_kernel(
         const uint32_t rec = (wd.flags >> 8) + u;
 #pragma unroll
         for (int nt = 0; nt < NT; nt++) {
-            float lt = st.l[nt];
-            lt = rows_sum(lt);
+            const float lt = C::FP8 ? rows_sum(st.l[nt][0]) : st.l[nt][0];
             const uint32_t col = nt * 16 + li;
             if (col >= ncols) continue;
             const uint32_t row = ud.rowbeg + col / p.group;
