@@ -66,8 +66,8 @@ def load_traffic(path, kernel_us, layer_bytes):
 def side_config(args):
     """One layer of BASELINE config 3 (mixed prefill + decode, MFMA-bound), 4 (MTP verify) or
     5 (FP8 decode) on resident synthetic data, timed as a step of its own: device packing,
-    the plan, the KV append of the step's rows (fused into the attention launch on 16-bit
-    pools, the separate quantising append on FP8 pools), split attention and the combine,
+    the plan, the KV append of the step's rows fused into the attention launch (quantised on
+    FP8 pools), split attention and the combine,
     replayed from a graph.  Prints a JSON line with the step time and the roofline of the
     layer's algorithmic work."""
     import torch
@@ -118,8 +118,8 @@ def side_config(args):
                         cu, positions, sequences, slots, status)
         lia.attention_plan(cfg, b.n_seqs, rows, cu, positions, sequences, ws, pages=flat)
         if fp8:
-            lia.kv_append(layout, newk, newv, kp, vp, slot_mapping=slots, k_scales=ks, v_scales=vs)
-            lia.attention_partial(cfg, b.n_seqs, flat, q, kp, vp, out, ws, k_scales=ks, v_scales=vs)
+            lia.attention_partial_append_fp8(cfg, b.n_seqs, flat, slots, q, newk, newv, kp, vp, ks, vs,
+                                             out, ws)
         else:
             lia.attention_partial_append(cfg, b.n_seqs, flat, slots, q, newk, newv, kp, vp, out, ws)
         lia.attention_merge(cfg, b.n_seqs, rows, out, ws)

@@ -335,7 +335,7 @@ int lia_attention_merge(const lia_attention_config *config, uint32_t n_seqs, uin
  * into lia_attention_partial: one launch does both.  Replaces the per-layer pair
  * llama_cache_paged + paged attention of the reference forward (src/gpu/kernels/llama.rs:162-183
  * followed by src/inference/llama.rs:253-288).  new_k / new_v: [n_rows][num_kv_heads][head_dim]
- * in the pool dtype (LIA_F16 or LIA_BF16; FP8 pools return LIA_E_UNSUPPORTED), 16-byte
+ * in the pool dtype (LIA_F16 or LIA_BF16; FP8 pools: lia_attention_partial_append_fp8), 16-byte
  * aligned.  The plan must come from the same packed rows: the first row of each sequence
  * sits at the sequence's cached length and its rows' keys are read from new_k / new_v, the
  * cached keys from the pool.  The pool afterwards holds the same bytes lia_kv_append
@@ -348,6 +348,23 @@ int lia_attention_partial_append(const lia_attention_config *config, uint32_t n_
                                  const uint32_t *slot_mapping, const void *q, const void *new_k,
                                  const void *new_v, void *kc, void *vc, void *workspace,
                                  size_t workspace_bytes, void *out, lia_stream_t stream);
+
+/*
+ * lia_attention_partial_append for FP8 pools: the step's rows new_k / new_v are bf16
+ * ([n_rows][num_kv_heads][head_dim], 16-byte aligned) and are appended exactly as
+ * lia_kv_append(src_dtype = LIA_BF16) appends them - divided by the scale of their page,
+ * rounded to e4m3 (saturating), a page whose scale is still 0 taking scale 1 and recording
+ * it in k_scales / v_scales - then attended from the pool (two launches on `stream`; every
+ * argument is checked before either is issued).  Other pool types return LIA_E_UNSUPPORTED
+ * (and lia_attention_partial_append returns it for FP8 pools).  No counterpart in the
+ * reference, whose KV cache is f16 only.
+ */
+int lia_attention_partial_append_fp8(const lia_attention_config *config, uint32_t n_seqs,
+                                     uint32_t n_rows, const uint32_t *pages,
+                                     const uint32_t *slot_mapping, const void *q,
+                                     const void *new_k, const void *new_v, void *kc, void *vc,
+                                     float *k_scales, float *v_scales, void *workspace,
+                                     size_t workspace_bytes, void *out, lia_stream_t stream);
 
 /*
  * lia_paged_attention without a workspace argument: the work list and split records live in

@@ -153,6 +153,11 @@ EXPORTS = {
                                                C.c_uint32, C.c_void_p, C.c_void_p, C.c_void_p,
                                                C.c_void_p, C.c_void_p, C.c_void_p, C.c_void_p,
                                                C.c_void_p, C.c_size_t, C.c_void_p, C.c_void_p]),
+    "lia_attention_partial_append_fp8": (C.c_int, [C.POINTER(AttentionConfig), C.c_uint32,
+                                                   C.c_uint32, C.c_void_p, C.c_void_p, C.c_void_p,
+                                                   C.c_void_p, C.c_void_p, C.c_void_p, C.c_void_p,
+                                                   C.c_void_p, C.c_void_p, C.c_void_p, C.c_size_t,
+                                                   C.c_void_p, C.c_void_p]),
     "lia_attention_partial": (C.c_int, [C.POINTER(AttentionConfig), C.c_uint32, C.c_uint32,
                                         C.c_void_p, C.c_void_p, C.c_void_p, C.c_void_p,
                                         C.c_void_p, C.c_void_p, C.c_void_p, C.c_size_t,
@@ -763,6 +768,17 @@ def attention_partial_append(config, n_seqs, pages, slot_mapping, q, new_k, new_
                                             workspace.numel() * workspace.element_size(),
                                             _dptr(out), _stream(stream))
     _check(st, "attention_partial_append")
+
+
+def attention_partial_append_fp8(config, n_seqs, pages, slot_mapping, q, new_k, new_v, kc, vc,
+                                 k_scales, v_scales, out, workspace, stream=None):
+    """Stage 2 with this step's KV append fused in, FP8 pools (lia_attention_partial_append_fp8):
+    new_k / new_v are the step's bf16 rows, quantised with their pages' scales."""
+    st = lib().lia_attention_partial_append_fp8(
+        C.byref(config), n_seqs, q.shape[0], _dptr(pages), _dptr(slot_mapping), _dptr(q),
+        _dptr(new_k), _dptr(new_v), _dptr(kc), _dptr(vc), _dptr(k_scales), _dptr(v_scales),
+        _dptr(workspace), workspace.numel() * workspace.element_size(), _dptr(out), _stream(stream))
+    _check(st, "attention_partial_append_fp8")
 
 
 def attention_merge(config, n_seqs, n_rows, out, workspace, stream=None):

@@ -2044,7 +2044,7 @@ static int run_stages(int stages, const lia_attention_config *c, uint32_t n_seqs
                       const uint32_t *sequences, const uint32_t *pages, const void *q,
                       const void *kc, const void *vc, const float *k_scales,
                       const float *v_scales, void *workspace, size_t workspace_bytes, void *out,
-                      lia_stream_t stream, const FusedAppend *fa = nullptr) {
+                      lia_stream_t stream, const FusedAppend *fa = nullptr, bool launch = true) {
     int st = validate(c);
     if (st) return st;
     if (n_seqs == 0 || n_seqs > c->max_seqs || n_rows == 0 || n_rows > c->max_rows) return LIA_E_ARG;
@@ -2071,6 +2071,7 @@ static int run_stages(int stages, const lia_attention_config *c, uint32_t n_seqs
     Layout L = layout_for(c, max_workgroups(c));
     if (workspace_bytes < L.total) return LIA_E_WORKSPACE;
     if ((uintptr_t)workspace & 255) return LIA_E_ALIGN;
+    if (!launch) return LIA_OK; // validation only
     const uint32_t group = c->num_q_heads / c->num_kv_heads;
     const uint32_t NT = nt_for(n_rows, n_seqs, group, c->kv_dtype);
     const uint32_t n_wg = workgroups_for(c, NT);
@@ -2208,6 +2209,34 @@ extern "C" int lia_attention_partial_append(const lia_attention_config *c, uint3
     const FusedAppend fa{new_k, new_v, slot_mapping};
     return run_stages(kPartial, c, n_seqs, n_rows, &dummy, &dummy, nullptr, pages, q, kc, vc,
                       nullptr, nullptr, workspace, workspace_bytes, out, stream, &fa);
+}
+
+// FP8 pools: the quantising append (lia_kv_append of bf16 rows through the slot mapping) and
+// the attention kernel over the pool, as two launches.  Quantising the new rows inside the
+// attention launch instead was measured slower on the config-5 decode step (the e4m3
+// conversions and divisions sit on the critical path of every unit's last workgroup).
+extern "C" int lia_attention_partial_append_fp8(const lia_attention_config *c, uint32_t n_seqs,
+                                                uint32_t n_rows, const uint32_t *pages,
+                                                const uint32_t *slot_mapping, const void *q,
+                                                const void *new_k, const void *new_v, void *kc,
+                                                void *vc, float *k_scales, float *v_scales,
+                                                void *workspace, size_t workspace_bytes, void *out,
+                                                lia_stream_t stream) {
+    static const uint32_t dummy = 0;
+    if (!c) return LIA_E_ARG;
+    if (c->kv_dtype != LIA_FP8_E4M3) return LIA_E_UNSUPPORTED;
+    if (!new_k || !new_v || !slot_mapping) return LIA_E_ARG;
+    if (((uintptr_t)new_k | (uintptr_t)new_v) & 15) return LIA_E_ALIGN;
+    // every check of both launches before either is issued
+    int st = run_stages(kPartial, c, n_seqs, n_rows, &dummy, &dummy, nullptr, pages, q, kc, vc,
+                        k_scales, v_scales, workspace, workspace_bytes, out, stream, nullptr, false);
+    if (st) return st;
+    const lia_kv_layout layout{c->num_kv_heads, c->head_dim, c->page_size, c->pool_pages, LIA_FP8_E4M3};
+    st = lia_kv_append(&layout, n_rows, nullptr, nullptr, nullptr, 0, slot_mapping, LIA_BF16, new_k,
+                       new_v, kc, vc, k_scales, v_scales, stream);
+    if (st) return st;
+    return run_stages(kPartial, c, n_seqs, n_rows, &dummy, &dummy, nullptr, pages, q, kc, vc,
+                      k_scales, v_scales, workspace, workspace_bytes, out, stream);
 }
 
 extern "C" int lia_attention_merge(const lia_attention_config *c, uint32_t n_seqs, uint32_t n_rows,

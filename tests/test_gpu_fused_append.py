@@ -206,3 +206,71 @@ def test_config3_full_step_with_shared_prefix_pages(lia, wl, O):
     print(f"[case] cfg3 step: max_abs={mx:.3e} mean_abs={mean:.3e}", flush=True)
     assert np.all(np.isfinite(got))
     assert mx < 2e-2 and mean < 2e-3
+
+
+@pytest.mark.parametrize("case_name", ["decode_mtp_prefill", "config5_head"])
+def test_fused_fp8_append(lia, wl, O, case_name):
+    """lia_attention_partial_append_fp8: the step's bf16 rows are quantised into the FP8 pool
+    exactly as lia_kv_append(src bf16) stores them - bytes and per-(page, head) scales, fresh
+    pages (scale 0) taking scale 1 - and attended with those quantised values (float64
+    oracle over the pool after the append, FP8 tolerance)."""
+    if case_name == "config5_head":
+        b5 = wl.config5(seed=0)
+        keep = 8
+        ctx, q_len = b5.ctx[:keep], b5.q_len[:keep]
+        g = b5.geom
+    else:
+        # decode rows at and past page boundaries (fresh pages), MTP rows crossing a page,
+        # a prefill chunk of 40 rows after 16 cached keys
+        ctx, q_len = [17, 33, 100, 16 + 3, 16 + 40, 900], [1, 1, 1, 3, 40, 2]
+        g = wl.Geometry(kv_dtype=FP8)
+    b = wl.custom(ctx, q_len, geom=g, seed=71)
+    P, W = g.page_size, g.hkv * g.d
+    rng = np.random.default_rng(71)
+    tokens = b.pool_pages * P
+    layout = O.KVLayout(g.hkv, g.d, P, b.pool_pages, FP8)
+    kc = np.zeros(tokens * W, np.uint8)
+    vc = np.zeros_like(kc)
+    ks = np.zeros(b.pool_pages * g.hkv, np.float32)
+    vs = np.zeros_like(ks)
+    kf = rng.standard_normal((b.pool_pages, P, g.hkv, g.d)).astype(np.float32)
+    vf = rng.standard_normal((b.pool_pages, P, g.hkv, g.d)).astype(np.float32)
+    # quantise the pages holding cached keys; pages holding only new rows stay fresh (scale 0)
+    cached_pages = set()
+    for s, t in enumerate(b.tables):
+        for lp in range(-(-int(b.cached[s]) // P)):
+            cached_pages.add(int(t[lp]))
+    ids = np.array(sorted(cached_pages), np.uint32)
+    O.kv_quantize_pages(layout, ids, kf[ids], vf[ids], kc, vc, ks, vs)
+    newk = O.from_f32(rng.standard_normal((b.n_rows, W)).astype(np.float32) * 2, BF16)
+    newv = O.from_f32(rng.standard_normal((b.n_rows, W)).astype(np.float32), BF16)
+    # expected pool after the step
+    kexp, vexp, ksx, vsx = kc.copy(), vc.copy(), ks.copy(), vs.copy()
+    O.kv_append(layout, b.positions(), b.sequences(), b.flat_table(), b.stride, newk, newv, kexp,
+                vexp, src_dtype=BF16, k_scales=ksx, v_scales=vsx)
+    assert (ksx != ks).any(), "some page was fresh"
+    dkc, dvc = G.to_dev(kc, torch.uint8), G.to_dev(vc, torch.uint8)
+    dks, dvs = G.to_dev(ks), G.to_dev(vs)
+    qf = O.from_f32(rng.standard_normal((b.n_rows, g.hq, g.d)).astype(np.float32), BF16)
+    cfg = lia.AttentionConfig(g.hq, g.hkv, g.d, P, b.pool_pages, b.stride, g.q_dtype, g.kv_dtype,
+                              g.out_dtype, g.scale, b.n_seqs, b.n_rows, int(b.ctx.max()))
+    ws = torch.zeros(lia.workspace_bytes(cfg), dtype=torch.uint8, device="cuda")
+    out = torch.full((b.n_rows, g.hq, g.d), float("nan"), dtype=torch.bfloat16, device="cuda")
+    flat = G.u32_dev(b.flat_table())
+    print(f"[case] fused fp8 {case_name}: seqs={b.n_seqs} rows={b.n_rows}", flush=True)
+    lia.attention_plan(cfg, b.n_seqs, b.n_rows, G.u32_dev(b.cu_seqlens()), G.u32_dev(b.positions()),
+                       G.u32_dev(b.sequences()), ws, pages=flat)
+    lia.attention_partial_append_fp8(cfg, b.n_seqs, flat, G.u32_dev(b.slot_mapping()),
+                                     G.to_dev(qf, torch.bfloat16), G.to_dev(newk, torch.bfloat16),
+                                     G.to_dev(newv, torch.bfloat16), dkc, dvc, dks, dvs, out, ws)
+    lia.attention_merge(cfg, b.n_seqs, b.n_rows, out, ws)
+    torch.cuda.synchronize()
+    assert np.array_equal(dks.cpu().numpy(), ksx) and np.array_equal(dvs.cpu().numpy(), vsx)
+    assert np.array_equal(dkc.cpu().numpy(), kexp) and np.array_equal(dvc.cpu().numpy(), vexp)
+    geom = O.geom(g.hq, g.hkv, g.d, P, b.stride, FP8, g.scale)
+    ref = O.attention_f64(geom, b.positions(), b.sequences(), b.flat_table(), O.to_f32(qf, BF16),
+                          kexp, vexp, ksx, vsx)
+    got = out.float().cpu().numpy()
+    mx, mean = G.errors(got, ref)
+    print(f"[case] fused fp8 {case_name}: max_abs={mx:.3e} mean_abs={mean:.3e}", flush=True)
+    assert np.all(np.isfinite(got)) and mx < 5e-2 and mean < 5e-3

@@ -180,3 +180,19 @@ def test_scale_must_be_positive_and_finite(lia, scale):
     positive scale (the reference's is 1/sqrt(head_dim))."""
     cfg = _cfg(lia, scale=scale)
     assert _paged(lia, cfg, _args(lia, cfg)) == E_ARG
+
+
+def test_fp8_partial_append_validates_both_launches_first(lia):
+    """lia_attention_partial_append_fp8 checks the append's and the attention's arguments
+    before it issues either launch."""
+    def call(cfg, new_k=A, ws_bytes=None, ks=A):
+        p = lambda x: None if x is None else C.c_void_p(x)
+        return lia.lib().lia_attention_partial_append_fp8(
+            C.byref(cfg), 2, 2, p(A), p(A), p(A), p(new_k), p(A), p(A), p(A), p(ks), p(A), p(A),
+            lia.workspace_bytes(cfg) if ws_bytes is None else ws_bytes, p(A), None)
+    assert call(_cfg(lia, kv_dtype=BF16)) == E_UNSUPPORTED
+    fp8 = _cfg(lia, kv_dtype=FP8)
+    assert call(fp8, new_k=None) == E_ARG
+    assert call(fp8, new_k=ODD16) == E_ALIGN
+    assert call(fp8, ks=None) == E_ARG
+    assert call(fp8, ws_bytes=1) == E_WORKSPACE
