@@ -384,12 +384,16 @@ int lia_paged_attention_static(const lia_attention_config *config, uint32_t n_se
                                void *out, lia_stream_t stream);
 size_t lia_static_workspace_bytes(void);
 
-/* Number of compute units the library schedules decode work for (device 0 unless
- * lia_init selected another).  0 on failure. */
+/* Number of compute units of the calling thread's current device, which the library
+ * schedules decode work for (cached per device).  0 on failure. */
 uint32_t lia_device_cus(void);
 
-/* Optional: select the device, cache its properties and look up its static workspace
- * (lia_paged_attention_static).  Returns LIA_OK. */
+/* Optional set-up of one device, the counterpart of loading the kernels' module once
+ * (src/gpu/llama_attention.rs:24,163 take the loaded `module`): makes `device` current,
+ * caches its compute-unit count, looks up its static workspace (lia_paged_attention_static)
+ * and resolves every kernel of the library's gfx950 code object on it (hipGetFuncBySymbol).
+ * Every launch goes through hipModuleLaunchKernel on those functions; a device not set up
+ * here resolves each function on its first launch instead.  LIA_OK, or LIA_E_HIP. */
 int lia_init(int device);
 
 /*

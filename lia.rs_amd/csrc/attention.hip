@@ -32,6 +32,7 @@
 #include <mutex>
 
 #include "common.hpp"
+#include "launch.hpp"
 
 namespace lia {
 
@@ -1824,10 +1825,11 @@ static inline uint32_t nt_for(uint32_t n_rows, uint32_t n_seqs, uint32_t group, 
 }
 
 template <int D, int NT, int REC>
-static void launch_combine(uint32_t split, dim3 grid, const AttnParams &p, hipStream_t s) {
-    if (split == 4) hipLaunchKernelGGL((combine_kernel<D, NT, 4, REC>), grid, dim3(kCombineThreads), 0, s, p);
-    else if (split == 2) hipLaunchKernelGGL((combine_kernel<D, NT, 2, REC>), grid, dim3(kCombineThreads), 0, s, p);
-    else hipLaunchKernelGGL((combine_kernel<D, NT, 1, REC>), grid, dim3(kCombineThreads), 0, s, p);
+static hipError_t launch_combine(uint32_t split, dim3 grid, const AttnParams &p, hipStream_t s) {
+    const dim3 block(kCombineThreads);
+    if (split == 4) return launch<combine_kernel<D, NT, 4, REC>>(grid, block, 0, s, p);
+    if (split == 2) return launch<combine_kernel<D, NT, 2, REC>>(grid, block, 0, s, p);
+    return launch<combine_kernel<D, NT, 1, REC>>(grid, block, 0, s, p);
 }
 
 static Layout layout_for(const lia_attention_config *c, uint32_t n_wg) {
@@ -1858,8 +1860,6 @@ static Layout layout_for(const lia_attention_config *c, uint32_t n_wg) {
 
 using namespace lia;
 
-static int g_device = 0;
-static uint32_t g_cus = 0;
 
 // Workspace of lia_paged_attention_static: a file-scope device array, so that entry point
 // allocates nothing.  Each device the library runs on holds its own copy until the process
@@ -1889,25 +1889,17 @@ static int scratch_of_current_device(void **out) {
 }
 
 extern "C" int lia_init(int device) {
-    if (hipSetDevice(device) != hipSuccess) return LIA_E_HIP;
-    void *ws = nullptr;
-    if (scratch_of_current_device(&ws) != LIA_OK) return LIA_E_HIP;
-    int cus = 0;
-    if (hipDeviceGetAttribute(&cus, hipDeviceAttributeMultiprocessorCount, device) != hipSuccess)
+    if (hipSetDevice(device) != hipSuccess) {
+        (void)hipGetLastError(); // leave no pending error for the caller's next runtime call
         return LIA_E_HIP;
-    g_device = device;
-    g_cus = (uint32_t)cus;
-    return LIA_OK;
+    }
+    void *ws = nullptr;
+    if (const int e = scratch_of_current_device(&ws)) return e;
+    if (!device_cus()) return LIA_E_HIP;
+    return resolve_kernels();
 }
 
-extern "C" uint32_t lia_device_cus(void) {
-    if (!g_cus) {
-        int dev = 0;
-        if (hipGetDevice(&dev) != hipSuccess) return 0;
-        if (lia_init(dev) != LIA_OK) return 0;
-    }
-    return g_cus;
-}
+extern "C" uint32_t lia_device_cus(void) { return device_cus(); }
 
 // Prefill kernel: resident 8-wave workgroups per CU at most.  Decode kernel: at most this
 // many waves per CU (three 2-wave workgroups measured best on 16-bit pools at head_dim 128,
@@ -2013,22 +2005,22 @@ static int validate(const lia_attention_config *c) {
 }
 
 template <int D, int NT, int KVT>
-static void launch_partial(const AttnParams &p, uint32_t n_wg, hipStream_t s) {
-    hipLaunchKernelGGL((attention_kernel<D, NT, KVT>), dim3(n_wg), dim3(Cfg<D, KVT>::THREADS), 0, s, p);
+static hipError_t launch_partial(const AttnParams &p, uint32_t n_wg, hipStream_t s) {
+    return launch<attention_kernel<D, NT, KVT>>(dim3(n_wg), dim3(Cfg<D, KVT>::THREADS), 0, s, p);
 }
 
 template <int D>
-static void launch_wide(int kv, const AttnParams &p, uint32_t n_wg, hipStream_t s) {
+static hipError_t launch_wide(int kv, const AttnParams &p, uint32_t n_wg, hipStream_t s) {
     const dim3 block(WCfg<D>::THREADS);
-    if (kv == LIA_BF16) hipLaunchKernelGGL((wide_kernel<D, LIA_BF16>), dim3(n_wg), block, 0, s, p);
-    else hipLaunchKernelGGL((wide_kernel<D, LIA_F16>), dim3(n_wg), block, 0, s, p);
+    if (kv == LIA_BF16) return launch<wide_kernel<D, LIA_BF16>>(dim3(n_wg), block, 0, s, p);
+    return launch<wide_kernel<D, LIA_F16>>(dim3(n_wg), block, 0, s, p);
 }
 
 template <int D, int NT>
-static void launch_partial_kv(int kv, const AttnParams &p, uint32_t n_wg, hipStream_t s) {
-    if (kv == LIA_BF16) launch_partial<D, NT, LIA_BF16>(p, n_wg, s);
-    else if (kv == LIA_F16) launch_partial<D, NT, LIA_F16>(p, n_wg, s);
-    else launch_partial<D, NT, LIA_FP8_E4M3>(p, n_wg, s);
+static hipError_t launch_partial_kv(int kv, const AttnParams &p, uint32_t n_wg, hipStream_t s) {
+    if (kv == LIA_BF16) return launch_partial<D, NT, LIA_BF16>(p, n_wg, s);
+    if (kv == LIA_F16) return launch_partial<D, NT, LIA_F16>(p, n_wg, s);
+    return launch_partial<D, NT, LIA_FP8_E4M3>(p, n_wg, s);
 }
 
 enum Stage { kPlan = 1, kPartial = 2, kMerge = 4 };
@@ -2044,7 +2036,7 @@ static int run_stages(int stages, const lia_attention_config *c, uint32_t n_seqs
                       const uint32_t *sequences, const uint32_t *pages, const void *q,
                       const void *kc, const void *vc, const float *k_scales,
                       const float *v_scales, void *workspace, size_t workspace_bytes, void *out,
-                      lia_stream_t stream, const FusedAppend *fa = nullptr, bool launch = true) {
+                      lia_stream_t stream, const FusedAppend *fa = nullptr, bool enqueue = true) {
     int st = validate(c);
     if (st) return st;
     if (n_seqs == 0 || n_seqs > c->max_seqs || n_rows == 0 || n_rows > c->max_rows) return LIA_E_ARG;
@@ -2071,7 +2063,7 @@ static int run_stages(int stages, const lia_attention_config *c, uint32_t n_seqs
     Layout L = layout_for(c, max_workgroups(c));
     if (workspace_bytes < L.total) return LIA_E_WORKSPACE;
     if ((uintptr_t)workspace & 255) return LIA_E_ALIGN;
-    if (!launch) return LIA_OK; // validation only
+    if (!enqueue) return LIA_OK; // validation only
     const uint32_t group = c->num_q_heads / c->num_kv_heads;
     const uint32_t NT = nt_for(n_rows, n_seqs, group, c->kv_dtype);
     const uint32_t n_wg = workgroups_for(c, NT);
@@ -2106,23 +2098,24 @@ static int run_stages(int stages, const lia_attention_config *c, uint32_t n_seqs
     p.vc_w = const_cast<void *>(vc);
     p.n_rows = n_rows;
     hipStream_t s = (hipStream_t)stream;
+    hipError_t e = hipSuccess;
     if (stages & kPlan)
-        hipLaunchKernelGGL(plan_kernel, dim3(1), dim3(256), 0, s, n_seqs, cu_seqlens, positions,
-                           sequences, pages, c->stride, p.page_shift, rpc, c->num_kv_heads,
-                           L.max_units, n_wg, (UnitDesc *)(ws + L.units), (WorkDesc *)(ws + L.work),
-                           (MergeDesc *)(ws + L.merge), (uint32_t *)(ws + L.header));
-    if (stages & kPartial) {
+        e = launch<plan_kernel>(dim3(1), dim3(256), 0, s, n_seqs, cu_seqlens, positions, sequences,
+                                pages, c->stride, p.page_shift, rpc, c->num_kv_heads, L.max_units,
+                                n_wg, (UnitDesc *)(ws + L.units), (WorkDesc *)(ws + L.work),
+                                (MergeDesc *)(ws + L.merge), (uint32_t *)(ws + L.header));
+    if (e == hipSuccess && (stages & kPartial)) {
         if (c->head_dim == 128) {
-            if (NT == 1) launch_partial_kv<128, 1>(c->kv_dtype, p, n_wg, s);
-            else if (NT == 2) launch_partial_kv<128, 2>(c->kv_dtype, p, n_wg, s);
-            else launch_wide<128>(c->kv_dtype, p, n_wg, s);
+            if (NT == 1) e = launch_partial_kv<128, 1>(c->kv_dtype, p, n_wg, s);
+            else if (NT == 2) e = launch_partial_kv<128, 2>(c->kv_dtype, p, n_wg, s);
+            else e = launch_wide<128>(c->kv_dtype, p, n_wg, s);
         } else {
-            if (NT == 1) launch_partial_kv<64, 1>(c->kv_dtype, p, n_wg, s);
-            else if (NT == 2) launch_partial_kv<64, 2>(c->kv_dtype, p, n_wg, s);
-            else launch_wide<64>(c->kv_dtype, p, n_wg, s);
+            if (NT == 1) e = launch_partial_kv<64, 1>(c->kv_dtype, p, n_wg, s);
+            else if (NT == 2) e = launch_partial_kv<64, 2>(c->kv_dtype, p, n_wg, s);
+            else e = launch_wide<64>(c->kv_dtype, p, n_wg, s);
         }
     }
-    if (stages & kMerge) {
+    if (e == hipSuccess && (stages & kMerge)) {
         // units this NT can produce: rows in blocks of rpc per sequence and KV head
         // (sum over sequences of ceil(rows / rpc) <= n_rows / rpc + n_seqs)
         uint32_t units_nt = (n_rows / (rpc ? rpc : 1) + n_seqs + 1) * c->num_kv_heads;
@@ -2145,27 +2138,27 @@ static int run_stages(int stages, const lia_attention_config *c, uint32_t n_seqs
         grid.z = split;
 #define LIA_COMBINE(DD, NN)                                                                      \
     do {                                                                                         \
-        if (rec == 1) launch_combine<DD, NN, 1>(split, grid, p, s);                               \
-        else if (rec == 2) launch_combine<DD, NN, 2>(split, grid, p, s);                          \
-        else launch_combine<DD, NN, 0>(split, grid, p, s);                                        \
+        if (rec == 1) e = launch_combine<DD, NN, 1>(split, grid, p, s);                           \
+        else if (rec == 2) e = launch_combine<DD, NN, 2>(split, grid, p, s);                      \
+        else e = launch_combine<DD, NN, 0>(split, grid, p, s);                                    \
     } while (0)
         const dim3 wgrid(grid.x, 16 * kWideNT / (4 * kWideCombineCols));
         if (c->head_dim == 128) {
             if (NT == 1) LIA_COMBINE(128, 1);
             else if (NT == 2) LIA_COMBINE(128, 2);
-            else if (rec == 0) hipLaunchKernelGGL((combine_wide_kernel<128, 0>), wgrid, dim3(256), 0, s, p);
-            else if (rec == 2) hipLaunchKernelGGL((combine_wide_kernel<128, 2>), wgrid, dim3(256), 0, s, p);
-            else hipLaunchKernelGGL((combine_wide_kernel<128, 1>), wgrid, dim3(256), 0, s, p);
+            else if (rec == 0) e = launch<combine_wide_kernel<128, 0>>(wgrid, dim3(256), 0, s, p);
+            else if (rec == 2) e = launch<combine_wide_kernel<128, 2>>(wgrid, dim3(256), 0, s, p);
+            else e = launch<combine_wide_kernel<128, 1>>(wgrid, dim3(256), 0, s, p);
         } else {
             if (NT == 1) LIA_COMBINE(64, 1);
             else if (NT == 2) LIA_COMBINE(64, 2);
-            else if (rec == 0) hipLaunchKernelGGL((combine_wide_kernel<64, 0>), wgrid, dim3(256), 0, s, p);
-            else if (rec == 2) hipLaunchKernelGGL((combine_wide_kernel<64, 2>), wgrid, dim3(256), 0, s, p);
-            else hipLaunchKernelGGL((combine_wide_kernel<64, 1>), wgrid, dim3(256), 0, s, p);
+            else if (rec == 0) e = launch<combine_wide_kernel<64, 0>>(wgrid, dim3(256), 0, s, p);
+            else if (rec == 2) e = launch<combine_wide_kernel<64, 2>>(wgrid, dim3(256), 0, s, p);
+            else e = launch<combine_wide_kernel<64, 1>>(wgrid, dim3(256), 0, s, p);
         }
 #undef LIA_COMBINE
     }
-    return hipGetLastError() == hipSuccess ? LIA_OK : LIA_E_HIP;
+    return e == hipSuccess ? LIA_OK : LIA_E_HIP;
 }
 
 extern "C" int lia_paged_attention(const lia_attention_config *c, uint32_t n_seqs, uint32_t n_rows,

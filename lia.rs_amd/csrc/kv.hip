@@ -1,5 +1,6 @@
 // Packing, slot mapping and KV-append scatter for the paged KV pool (gfx950).
 #include "common.hpp"
+#include "launch.hpp"
 
 namespace lia {
 
@@ -572,9 +573,10 @@ extern "C" int lia_gather_rows(uint32_t count, uint32_t width, const uint32_t *i
     const bool vec = width % 4 == 0 && (((uintptr_t)src | (uintptr_t)dst) & 15) == 0;
     const uint32_t n = count * (vec ? width / 4 : width);
     hipStream_t s = (hipStream_t)stream;
-    if (vec) hipLaunchKernelGGL(gather_kernel<true>, dim3((n + 255) / 256), dim3(256), 0, s, count, width, indices, src, dst);
-    else hipLaunchKernelGGL(gather_kernel<false>, dim3((n + 255) / 256), dim3(256), 0, s, count, width, indices, src, dst);
-    return hipGetLastError() == hipSuccess ? LIA_OK : LIA_E_HIP;
+    const dim3 grid((n + 255) / 256);
+    const hipError_t e = vec ? launch<gather_kernel<true>>(grid, dim3(256), 0, s, count, width, indices, src, dst)
+                             : launch<gather_kernel<false>>(grid, dim3(256), 0, s, count, width, indices, src, dst);
+    return e == hipSuccess ? LIA_OK : LIA_E_HIP;
 }
 
 extern "C" int lia_rope_coefficients(uint32_t rows, uint32_t head_dim, float base,
@@ -585,9 +587,10 @@ extern "C" int lia_rope_coefficients(uint32_t rows, uint32_t head_dim, float bas
     if (((uintptr_t)coefficients & 7) != 0) return LIA_E_ALIGN;
     if (rows == 0) return LIA_OK;
     const uint32_t n = rows * (head_dim / 2);
-    hipLaunchKernelGGL(rope_coefficients_kernel, dim3((n + 255) / 256), dim3(256), 0,
-                       (hipStream_t)stream, rows, head_dim, base, positions, coefficients);
-    return hipGetLastError() == hipSuccess ? LIA_OK : LIA_E_HIP;
+    const hipError_t e = launch<rope_coefficients_kernel>(dim3((n + 255) / 256), dim3(256), 0,
+                                                          (hipStream_t)stream, rows, head_dim, base,
+                                                          positions, coefficients);
+    return e == hipSuccess ? LIA_OK : LIA_E_HIP;
 }
 
 extern "C" int lia_rope_kv_append(const lia_kv_layout *L, uint32_t num_q_heads, uint32_t rows,
@@ -612,10 +615,12 @@ extern "C" int lia_rope_kv_append(const lia_kv_layout *L, uint32_t num_q_heads, 
     const uint32_t shift = (uint32_t)__builtin_ctz(L->page_size);
     hipStream_t s = (hipStream_t)stream;
     const int qb = query_dtype == LIA_BF16;
+    hipError_t e;
 #define LIA_ROPE(KVT)                                                                              \
-    hipLaunchKernelGGL(rope_append_kernel<KVT>, grid, dim3(256), 0, s, rows, num_q_heads,          \
-                       L->num_kv_heads, L->head_dim, positions, sequences, pages, stride, shift,   \
-                       L->pool_pages, slot_mapping, coefficients, input, query, qb, kc, vc, k_scales, v_scales)
+    e = launch<rope_append_kernel<KVT>>(grid, dim3(256), 0, s, rows, num_q_heads, L->num_kv_heads, \
+                                        L->head_dim, positions, sequences, pages, stride, shift,   \
+                                        L->pool_pages, slot_mapping, coefficients, input, query,   \
+                                        qb, kc, vc, k_scales, v_scales)
     switch (L->dtype) {
     case LIA_F16: LIA_ROPE(LIA_F16); break;
     case LIA_BF16: LIA_ROPE(LIA_BF16); break;
@@ -623,7 +628,7 @@ extern "C" int lia_rope_kv_append(const lia_kv_layout *L, uint32_t num_q_heads, 
     default: return LIA_E_UNSUPPORTED;
     }
 #undef LIA_ROPE
-    return hipGetLastError() == hipSuccess ? LIA_OK : LIA_E_HIP;
+    return e == hipSuccess ? LIA_OK : LIA_E_HIP;
 }
 
 static int src_kind_of(int32_t dtype) {
@@ -640,14 +645,17 @@ extern "C" int lia_pack_device(uint32_t n_seqs, const uint32_t *seq_slots, const
         !sequences || !slot_mapping || !status || stride == 0)
         return LIA_E_ARG;
     if (page_size == 0 || (page_size & (page_size - 1))) return LIA_E_ARG;
-    hipLaunchKernelGGL(pack_kernel, dim3(1), dim3(1024), 0, (hipStream_t)stream, n_seqs, seq_slots,
-                       q_lens, cached, pages, stride, (uint32_t)__builtin_ctz(page_size), pool_pages,
-                       context, max_rows, cu_seqlens, positions, sequences, slot_mapping, status);
-    hipLaunchKernelGGL(table_check_kernel, dim3(kCheckGroups), dim3(kCheckThreads), 0,
-                       (hipStream_t)stream, n_seqs, seq_slots, q_lens, cached, pages, stride,
-                       (uint32_t)__builtin_ctz(page_size), pool_pages, context, max_rows, cu_seqlens,
-                       slot_mapping, status);
-    return hipGetLastError() == hipSuccess ? LIA_OK : LIA_E_HIP;
+    hipStream_t s = (hipStream_t)stream;
+    const uint32_t shift = (uint32_t)__builtin_ctz(page_size);
+    if (launch<pack_kernel>(dim3(1), dim3(1024), 0, s, n_seqs, seq_slots, q_lens, cached, pages,
+                            stride, shift, pool_pages, context, max_rows, cu_seqlens, positions,
+                            sequences, slot_mapping, status) != hipSuccess)
+        return LIA_E_HIP;
+    const hipError_t e = launch<table_check_kernel>(dim3(kCheckGroups), dim3(kCheckThreads), 0, s,
+                                                    n_seqs, seq_slots, q_lens, cached, pages, stride,
+                                                    shift, pool_pages, context, max_rows, cu_seqlens,
+                                                    slot_mapping, status);
+    return e == hipSuccess ? LIA_OK : LIA_E_HIP;
 }
 
 extern "C" int lia_kv_append(const lia_kv_layout *L, uint32_t rows, const uint32_t *positions,
@@ -668,26 +676,20 @@ extern "C" int lia_kv_append(const lia_kv_layout *L, uint32_t rows, const uint32
     dim3 grid((uint32_t)((threads + 255) / 256));
     uint32_t shift = (uint32_t)__builtin_ctz(L->page_size);
     hipStream_t s = (hipStream_t)stream;
+    hipError_t e;
+#define LIA_APPEND(KVT)                                                                            \
+    e = launch<append_kernel<KVT>>(grid, dim3(256), 0, s, rows, width, L->head_dim,                \
+                                   L->num_kv_heads, positions, sequences, pages, stride, shift,    \
+                                   L->pool_pages, slot_mapping, kind, k, v, kc, vc, k_scales,      \
+                                   v_scales)
     switch (L->dtype) {
-    case LIA_F16:
-        hipLaunchKernelGGL(append_kernel<LIA_F16>, grid, dim3(256), 0, s, rows, width, L->head_dim,
-                           L->num_kv_heads, positions, sequences, pages, stride, shift, L->pool_pages,
-                           slot_mapping, kind, k, v, kc, vc, k_scales, v_scales);
-        break;
-    case LIA_BF16:
-        hipLaunchKernelGGL(append_kernel<LIA_BF16>, grid, dim3(256), 0, s, rows, width, L->head_dim,
-                           L->num_kv_heads, positions, sequences, pages, stride, shift, L->pool_pages,
-                           slot_mapping, kind, k, v, kc, vc, k_scales, v_scales);
-        break;
-    case LIA_FP8_E4M3:
-        hipLaunchKernelGGL(append_kernel<LIA_FP8_E4M3>, grid, dim3(256), 0, s, rows, width,
-                           L->head_dim, L->num_kv_heads, positions, sequences, pages, stride, shift,
-                           L->pool_pages, slot_mapping, kind, k, v, kc, vc, k_scales, v_scales);
-        break;
-    default:
-        return LIA_E_UNSUPPORTED;
+    case LIA_F16: LIA_APPEND(LIA_F16); break;
+    case LIA_BF16: LIA_APPEND(LIA_BF16); break;
+    case LIA_FP8_E4M3: LIA_APPEND(LIA_FP8_E4M3); break;
+    default: return LIA_E_UNSUPPORTED;
     }
-    return hipGetLastError() == hipSuccess ? LIA_OK : LIA_E_HIP;
+#undef LIA_APPEND
+    return e == hipSuccess ? LIA_OK : LIA_E_HIP;
 }
 
 extern "C" int lia_kv_quantize_pages(const lia_kv_layout *L, uint32_t n_pages,
@@ -699,8 +701,9 @@ extern "C" int lia_kv_quantize_pages(const lia_kv_layout *L, uint32_t n_pages,
     if (n_pages == 0) return LIA_OK;
     int kind = src_kind_of(src_dtype);
     if (kind < 0) return LIA_E_UNSUPPORTED;
-    hipLaunchKernelGGL(quantize_kernel, dim3(n_pages, L->num_kv_heads, 2), dim3(256), 0,
-                       (hipStream_t)stream, L->page_size, L->num_kv_heads, L->head_dim, page_ids,
-                       kind, k, v, kc, vc, k_scales, v_scales);
-    return hipGetLastError() == hipSuccess ? LIA_OK : LIA_E_HIP;
+    const hipError_t e = launch<quantize_kernel>(dim3(n_pages, L->num_kv_heads, 2), dim3(256), 0,
+                                                 (hipStream_t)stream, L->page_size, L->num_kv_heads,
+                                                 L->head_dim, page_ids, kind, k, v, kc, vc, k_scales,
+                                                 v_scales);
+    return e == hipSuccess ? LIA_OK : LIA_E_HIP;
 }

@@ -16,6 +16,7 @@
 #include <vector>
 
 #include "common.hpp"
+#include "launch.hpp"
 
 // Every product and sum below is rounded on its own, as in the reference (no FMA contraction).
 #pragma clang fp contract(off)
@@ -463,10 +464,10 @@ extern "C" int lia_nucleus_candidates(uint32_t vocab, uint32_t rows, const doubl
     if (rows == 0) return LIA_OK;
     const uint64_t groups = (uint64_t)rows * nucleus_parts(vocab);
     if (groups > 0x3FFFFFFFu || (uint64_t)rows * vocab > 0xFFFFFFFFull) return LIA_E_ARG;
-    hipLaunchKernelGGL(nucleus_candidates_kernel, dim3((uint32_t)((groups + 3) / 4)), dim3(256), 0,
-                       (hipStream_t)stream, vocab, nucleus_parts(vocab), (uint32_t)groups,
-                       temperatures, logits, candidates, normalizers);
-    return hipGetLastError() == hipSuccess ? LIA_OK : LIA_E_HIP;
+    const hipError_t e = launch<nucleus_candidates_kernel>(
+        dim3((uint32_t)((groups + 3) / 4)), dim3(256), 0, (hipStream_t)stream, vocab,
+        nucleus_parts(vocab), (uint32_t)groups, temperatures, logits, candidates, normalizers);
+    return e == hipSuccess ? LIA_OK : LIA_E_HIP;
 }
 
 // Workspace::read's reduction and the per-row sampling of forward_paged_sampled, on host

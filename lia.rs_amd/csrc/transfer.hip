@@ -15,6 +15,7 @@
 #include <map>
 
 #include "common.hpp"
+#include "launch.hpp"
 
 namespace lia {
 
@@ -175,9 +176,9 @@ extern "C" int lia_kv_write_pages(const lia_kv_layout *layout, const lia_kv_plan
                            hipMemcpyHostToDevice, s) != hipSuccess)
             return finish(s, LIA_E_HIP);
     }
-    hipLaunchKernelGGL(kv_pages_kernel<true>, dim3(pages_grid(g, n_pages)), dim3(256), 0, s,
-                       n_pages, g, (uint8_t *)staging_device);
-    return finish(s, hipGetLastError() == hipSuccess ? LIA_OK : LIA_E_HIP);
+    const hipError_t e = launch<kv_pages_kernel<true>>(dim3(pages_grid(g, n_pages)), dim3(256), 0, s,
+                                                       n_pages, g, (uint8_t *)staging_device);
+    return finish(s, e == hipSuccess ? LIA_OK : LIA_E_HIP);
 }
 
 extern "C" int lia_kv_read_pages(const lia_kv_layout *layout, const lia_kv_planes *planes,
@@ -192,9 +193,9 @@ extern "C" int lia_kv_read_pages(const lia_kv_layout *layout, const lia_kv_plane
     hipStream_t s = (hipStream_t)stream;
     if (hipMemcpyAsync(staging_device, staging_host, g.header, hipMemcpyHostToDevice, s) != hipSuccess)
         return finish(s, LIA_E_HIP);
-    hipLaunchKernelGGL(kv_pages_kernel<false>, dim3(pages_grid(g, n_pages)), dim3(256), 0, s,
-                       n_pages, g, (uint8_t *)staging_device);
-    if (hipGetLastError() != hipSuccess) return finish(s, LIA_E_HIP);
+    if (launch<kv_pages_kernel<false>>(dim3(pages_grid(g, n_pages)), dim3(256), 0, s, n_pages, g,
+                                       (uint8_t *)staging_device) != hipSuccess)
+        return finish(s, LIA_E_HIP);
     // One device-to-host copy and one event per page: page i is copied out to the caller
     // while page i + 1 is still in flight.
     hipEvent_t *ev = page_events();
