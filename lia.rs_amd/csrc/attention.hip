@@ -1181,28 +1181,82 @@ __device__ __forceinline__ uint32_t swz_v(uint32_t t) {
     return D == 128 ? 2 * (t & 7) : 2 * ((t >> 1) & 1);
 }
 
-// This wave's quarter of chunk t of K and V (from the pool or the step's rows) into LDS.
+// Page data of a window of up to 64 logical pages for the wide kernel, one page per lane, so
+// that a chunk's tile costs three v_readlane: lane i holds the byte offset of logical page
+// base + i in its plane (64-bit) and the bytes of it that are live keys of the range (0 for a
+// page wholly past the range end, and for a table entry outside the pool: no load is based
+// outside the pool).
+struct WideWindow {
+    uint32_t base;          // first logical page covered (wave-uniform)
+    uint32_t off_lo, off_hi; // per lane
+    uint32_t bytes;         // per lane
+};
+
+// The 16-token tile a load reads: its page's byte offset and live bytes (0: the loads move
+// no data and return zeros).
+struct WideTile {
+    uint64_t off;
+    uint32_t bytes;
+};
+
+__device__ __forceinline__ void wide_window(const AttnParams &p, WideWindow &w,
+                                            const uint32_t *table, uint32_t first,
+                                            uint32_t limit, uint32_t tlim, uint32_t row_bytes) {
+    const uint32_t shift = p.page_shift, P = 1u << shift;
+    const uint32_t idx = first + lane_id();
+    uint32_t page = idx;
+    bool in_pool = true;
+    if (table) {
+        page = (uint32_t)__builtin_amdgcn_raw_buffer_load_b32(make_rsrc(table, limit * 4), (int)(idx * 4), 0, 0);
+        in_pool = page < p.pool_pages;
+    }
+    const uint32_t pstart = idx << shift;
+    const uint64_t off = (uint64_t)page * ((uint64_t)P * row_bytes);
+    w.base = first;
+    w.off_lo = (uint32_t)off;
+    w.off_hi = (uint32_t)(off >> 32);
+    w.bytes = in_pool && tlim > pstart ? min(tlim - pstart, P) * row_bytes : 0u;
+}
+
+// Tile at key t0 of a window whose range ends at tlim (t0 past it: no live keys; before it
+// the tile's page lies inside the window).
+__device__ __forceinline__ WideTile wide_tile(const WideWindow &w, uint32_t t0, uint32_t shift,
+                                              uint32_t tlim) {
+    const int rel = (int)(((t0 >> shift) - w.base) & 63);
+    WideTile r;
+    const uint32_t lo = (uint32_t)__builtin_amdgcn_readlane((int)w.off_lo, rel);
+    const uint32_t hi = (uint32_t)__builtin_amdgcn_readlane((int)w.off_hi, rel);
+    r.off = ((uint64_t)hi << 32) | lo;
+    r.bytes = t0 < tlim ? (uint32_t)__builtin_amdgcn_readlane((int)w.bytes, rel) : 0u;
+    return r;
+}
+
+// The tile of chunk t that this wave loads (each wave loads RPI consecutive tokens of one
+// 16-token tile).
 template <int D>
-__device__ __forceinline__ void wide_load(const AttnParams &p, uint32_t t, const TilePages &tp,
+__device__ __forceinline__ uint32_t wide_tile_key(uint32_t t, uint32_t wave) {
+    return t + 16 * ((wave * WCfg<D>::RPI) / 16);
+}
+
+// This wave's quarter of chunk t of K and V (from the pool or the step's rows) into LDS, from
+// the wave's tile (wide_tile_key).
+template <int D>
+__device__ __forceinline__ void wide_load(const AttnParams &p, uint32_t t, const WideTile &tile,
                                           const uint8_t *kbase, const uint8_t *vbase, uint32_t hk,
                                           uint32_t wave, uint16_t *kst, uint16_t *vst) {
     using W = WCfg<D>;
+    static_assert(W::PER == 1, "one direct-to-LDS instruction per wave and plane");
     const uint32_t lane = lane_id(), P = 1u << p.page_shift;
     const uint32_t row_bytes = p.hkv * W::ROWB;
     __builtin_amdgcn_s_waitcnt(0xC07F); // lgkmcnt(0): this wave's reads of the stage are done
-#pragma unroll
-    for (int s = 0; s < W::PER; s++) {
-        const uint32_t q = wave + s * W::WAVES;        // instruction: tokens q*RPI .. +RPI-1
-        if (W::NI % W::WAVES && q >= W::NI) break;     // waves past the last instruction
+    const uint32_t q = wave;                       // instruction: tokens q*RPI .. +RPI-1
+    if (W::NI % W::WAVES == 0 || q < W::NI) {      // waves past the last instruction load nothing
         const uint32_t tl = q * W::RPI + lane / W::CH; // token within the chunk
         const uint32_t pos = lane % W::CH;
-        const uint32_t j = (q * W::RPI) / 16;          // 16-token tile (one page)
         const uint32_t rowoff = ((t + tl) & (P - 1)) * row_bytes + hk * W::ROWB;
         const uint32_t base_k = (pos ^ swz_k<D>(tl)) * 16, base_v = (pos ^ swz_v<D>(tl)) * 16;
-        // select, not index: a runtime index into tp would put it in scratch memory
-        const uint32_t page = j ? tp.page[1] : tp.page[0], live = j ? tp.live[1] : tp.live[0];
-        const __amdgpu_buffer_rsrc_t rk = make_rsrc(kbase + (size_t)page * P * row_bytes, live * row_bytes);
-        const __amdgpu_buffer_rsrc_t rv = make_rsrc(vbase + (size_t)page * P * row_bytes, live * row_bytes);
+        const __amdgpu_buffer_rsrc_t rk = make_rsrc(kbase + tile.off, tile.bytes);
+        const __amdgpu_buffer_rsrc_t rv = make_rsrc(vbase + tile.off, tile.bytes);
         __builtin_amdgcn_raw_ptr_buffer_load_lds(
             rk, (__attribute__((address_space(3))) void *)(kst + q * 512), 16, rowoff + base_k, 0, 0, 0);
         __builtin_amdgcn_raw_ptr_buffer_load_lds(
@@ -1385,7 +1439,7 @@ constexpr int kWideStages = 3;
 // Chunk t needs the causal / range mask unless [t, t + 32) lies in [free_lo, free_hi), the
 // keys live for every valid column of the unit.
 template <int D, int KVT>
-__device__ __forceinline__ void wide_step(const AttnParams &p, uint32_t tn, const TilePages &tpn,
+__device__ __forceinline__ void wide_step(const AttnParams &p, uint32_t tn, const WideTile &tpn,
                                           uint16_t *__restrict__ kn, uint16_t *__restrict__ vn,
                                           uint32_t tc, const uint16_t *__restrict__ kc,
                                           const uint16_t *__restrict__ vc, const uint8_t *kbase,
@@ -1410,18 +1464,23 @@ __device__ __forceinline__ void wide_range(const AttnParams &p, const uint8_t *k
                                            uint32_t free_lo, uint32_t free_hi) {
     const uint32_t shift = p.page_shift;
     const uint32_t page_limit = (s_hi + (1u << shift) - 1) >> shift;
+    const uint32_t row_bytes = p.hkv * WCfg<D>::ROWB;
+    const uint32_t dt = wide_tile_key<D>(0, wave); // the wave's tile within a chunk
     for (uint32_t wbeg = s_lo & ~31u; wbeg < s_hi;) {
         const uint32_t wend = min(s_hi, ((wbeg >> shift) + 64) << shift);
-        PageWindow win;
-        window_load<false>(p, win, table, wbeg >> shift, page_limit, hk);
-        TilePages tp0, tp1;
-        if (use_pre) {
-            tp0 = tile_pages_pre(pre, wbeg >> shift, wbeg, shift, wend, p.pool_pages);
-            tp1 = tile_pages_pre(pre, wbeg >> shift, wbeg + 32, shift, wend, p.pool_pages);
+        WideWindow win;
+        wide_window(p, win, table, wbeg >> shift, page_limit, wend, row_bytes);
+        WideTile tp0, tp1;
+        if (use_pre) { // the plan's first pages: no wait for the table load
+            const TilePages a = tile_pages_pre(pre, wbeg >> shift, wbeg + dt, shift, wend, p.pool_pages);
+            const TilePages b = tile_pages_pre(pre, wbeg >> shift, wbeg + 32 + dt, shift, wend, p.pool_pages);
+            const uint64_t pb = (uint64_t)(1u << shift) * row_bytes;
+            tp0 = WideTile{a.page[0] * pb, a.live[0] * row_bytes};
+            tp1 = WideTile{b.page[0] * pb, b.live[0] * row_bytes};
             use_pre = false;
         } else {
-            tp0 = tile_pages<false>(win, wbeg, shift, wend);
-            tp1 = tile_pages<false>(win, wbeg + 32, shift, wend);
+            tp0 = wide_tile(win, wbeg + dt, shift, wend);
+            tp1 = wide_tile(win, wbeg + 32 + dt, shift, wend);
         }
         // every wave finished the previous window's chunks before their stages are refilled
         lds_barrier();
@@ -1429,13 +1488,13 @@ __device__ __forceinline__ void wide_range(const AttnParams &p, const uint8_t *k
         wide_load<D>(p, wbeg + 32, tp1, kbase, vbase, hk, wave, k1, v1);
         for (uint32_t t = wbeg;; t += 96) {
             // loads past wend carry no traffic
-            wide_step<D, KVT>(p, t + 64, tile_pages<false>(win, t + 64, shift, wend), k2, v2, t, k0,
+            wide_step<D, KVT>(p, t + 64, wide_tile(win, t + 64 + dt, shift, wend), k2, v2, t, k0,
                               v0, kbase, vbase, hk, wave, active, st, free_lo, free_hi);
             if (t + 32 >= wend) break;
-            wide_step<D, KVT>(p, t + 96, tile_pages<false>(win, t + 96, shift, wend), k0, v0, t + 32,
+            wide_step<D, KVT>(p, t + 96, wide_tile(win, t + 96 + dt, shift, wend), k0, v0, t + 32,
                               k1, v1, kbase, vbase, hk, wave, active, st, free_lo, free_hi);
             if (t + 64 >= wend) break;
-            wide_step<D, KVT>(p, t + 128, tile_pages<false>(win, t + 128, shift, wend), k1, v1, t + 64,
+            wide_step<D, KVT>(p, t + 128, wide_tile(win, t + 128 + dt, shift, wend), k1, v1, t + 64,
                               k2, v2, kbase, vbase, hk, wave, active, st, free_lo, free_hi);
             if (t + 96 >= wend) break;
         }
