@@ -168,9 +168,11 @@ __device__ void plan_lds(uint32_t n_seqs, const uint32_t *cu, const uint32_t *po
     __shared__ uint32_t s_u0[kPlanSeqs + 1], s_b0[kPlanSeqs + 1];
     __shared__ uint32_t s_units[256], s_blocks[256];
     __shared__ uint32_t carry_units, carry_blocks;
+    // Threads exchange only LDS data (nothing written to global memory is read back), so the
+    // barriers need not wait for the descriptor stores in flight.
     const uint32_t t = threadIdx.x;
     if (t == 0) { carry_units = 0; carry_blocks = 0; }
-    __syncthreads();
+    lds_barrier();
     for (uint32_t base = 0; base < n_seqs; base += 256) {
         const uint32_t b = base + t;
         uint32_t nu = 0, nb = 0, r0 = 0, nr = 0, p0 = 0, trow = 0;
@@ -188,21 +190,21 @@ __device__ void plan_lds(uint32_t n_seqs, const uint32_t *cu, const uint32_t *po
         }
         s_units[t] = nu;
         s_blocks[t] = nb;
-        __syncthreads();
+        lds_barrier();
         for (uint32_t off = 1; off < 256; off <<= 1) { // inclusive Hillis-Steele scan
             uint32_t a = t >= off ? s_units[t - off] : 0, c = t >= off ? s_blocks[t - off] : 0;
-            __syncthreads();
+            lds_barrier();
             s_units[t] += a;
             s_blocks[t] += c;
-            __syncthreads();
+            lds_barrier();
         }
         if (b < n_seqs) {
             s_u0[b] = carry_units + s_units[t] - nu;
             s_b0[b] = carry_blocks + s_blocks[t] - nb;
         }
-        __syncthreads();
+        lds_barrier();
         if (t == 255) { carry_units += s_units[255]; carry_blocks += s_blocks[255]; }
-        __syncthreads();
+        lds_barrier();
     }
     const bool overflow = carry_units > max_units;
     const uint32_t U = overflow ? 0 : carry_units, B = overflow ? 0 : carry_blocks;
@@ -216,7 +218,7 @@ __device__ void plan_lds(uint32_t n_seqs, const uint32_t *cu, const uint32_t *po
         header[2] = N;
         header[3] = overflow;
     }
-    __syncthreads();
+    lds_barrier();
     // last sequence b with arr[b] <= v (empty sequences share their offset with the next
     // one, so this is the sequence that owns v)
     auto seq_of = [&](const uint32_t *arr, uint32_t v) {
@@ -1361,6 +1363,23 @@ __device__ __forceinline__ void wide_compute(const AttnParams &p, uint32_t t, WS
 #pragma unroll
         for (int nt = 0; nt < NTW; nt++) acc[j][nt] = mfma16x16x32<MB>(ka[i & 1], st.qr[nt][ks], acc[j][nt]);
     }
+    // O^T += V^T P^T: V^T rows 16n .. 16n+15, k slots = tokens {4g..4g+3, 16+4g..16+4g+3}.
+    // The transpose read of row r0 = 4g + li/4, chunk 2n + b at position (2n + b) ^ swz_v(r0),
+    // is at vb ^ 32 n (row r0 + 16 swizzles like r0).
+    const uint32_t r0 = 4 * g + li / 4;
+    const uint32_t vb = r0 * 2 * D + 16 * ((li & 3) >> 1) + 8 * (li & 1) + 16 * swz_v<D>(r0);
+    auto vread = [&](int n) {
+        const uint8_t *a0p = (const uint8_t *)vst + (vb ^ (32 * n));
+        const uint8_t *a1p = a0p + 32 * D; // row r0 + 16
+        const s16x4 a0 = __builtin_amdgcn_ds_read_tr16_b64_v4i16((__attribute__((address_space(3))) s16x4 *)(a0p));
+        const s16x4 a1 = __builtin_amdgcn_ds_read_tr16_b64_v4i16((__attribute__((address_space(3))) s16x4 *)(a1p));
+        const u32x2 b0 = __builtin_bit_cast(u32x2, a0), b1 = __builtin_bit_cast(u32x2, a1);
+        return u32x4{b0.x, b0.y, b1.x, b1.y};
+    };
+    // the first V operand is read before the softmax: its LDS latency passes under it
+    u32x4 vt[3];
+    vt[0] = vread(0);
+    vt[1] = vread(1);
     if (masked) {
 #pragma unroll
         for (int j = 0; j < 2; j++)
@@ -1403,26 +1422,11 @@ __device__ __forceinline__ void wide_compute(const AttnParams &p, uint32_t t, WS
         pb[nt] = u32x4{pack2<MB>(pr[0][0], pr[0][1]), pack2<MB>(pr[0][2], pr[0][3]),
                        pack2<MB>(pr[1][0], pr[1][1]), pack2<MB>(pr[1][2], pr[1][3])};
     }
-    // O^T += V^T P^T: V^T rows 16n .. 16n+15, k slots = tokens {4g..4g+3, 16+4g..16+4g+3}.
-    // The transpose read of row r0 = 4g + li/4, chunk 2n + b at position (2n + b) ^ swz_v(r0),
-    // is at vb ^ 32 n (row r0 + 16 swizzles like r0).
-    const uint32_t r0 = 4 * g + li / 4;
-    const uint32_t vb = r0 * 2 * D + 16 * ((li & 3) >> 1) + 8 * (li & 1) + 16 * swz_v<D>(r0);
-    auto vread = [&](int n) {
-        const uint8_t *a0p = (const uint8_t *)vst + (vb ^ (32 * n));
-        const uint8_t *a1p = a0p + 32 * D; // row r0 + 16
-        const s16x4 a0 = __builtin_amdgcn_ds_read_tr16_b64_v4i16((__attribute__((address_space(3))) s16x4 *)(a0p));
-        const s16x4 a1 = __builtin_amdgcn_ds_read_tr16_b64_v4i16((__attribute__((address_space(3))) s16x4 *)(a1p));
-        const u32x2 b0 = __builtin_bit_cast(u32x2, a0), b1 = __builtin_bit_cast(u32x2, a1);
-        return u32x4{b0.x, b0.y, b1.x, b1.y};
-    };
-    u32x4 vt[2];
-    vt[0] = vread(0);
 #pragma unroll
     for (int n = 0; n < W::DT; n++) {
-        if (n + 1 < W::DT) vt[(n + 1) & 1] = vread(n + 1);
+        if (n + 2 < W::DT) vt[(n + 2) % 3] = vread(n + 2);
 #pragma unroll
-        for (int nt = 0; nt < NTW; nt++) st.o[nt][n] = mfma16x16x32<MB>(vt[n & 1], pb[nt], st.o[nt][n]);
+        for (int nt = 0; nt < NTW; nt++) st.o[nt][n] = mfma16x16x32<MB>(vt[n % 3], pb[nt], st.o[nt][n]);
     }
     // the mass: every row of the ones tile is the column's sum of this chunk's weights
     constexpr uint32_t one2 = MB ? 0x3F803F80u : 0x3C003C00u;

@@ -32,7 +32,14 @@ __device__ __forceinline__ float append_scale(float *scales, size_t at) {
 constexpr uint32_t kPackHash = 8192;  // LDS slot hash (open addressing, load <= 1/2 per pass)
 constexpr uint32_t kPackPass = kPackHash / 2;
 
-__device__ __forceinline__ uint32_t slot_hash(uint32_t s) { return (s * 2654435761u) >> 19; } // 13 bits
+// Home bucket of a slot: the 16 slots of an aligned 16-slot group (the consecutive rows of a
+// page) take the 16 buckets of one bucket group, chosen by a multiplicative hash of the group
+// index, so they never collide with each other and their LDS accesses hit distinct banks.  A
+// probe steps 17 buckets - the next group, the next offset - which visits every bucket.
+__device__ __forceinline__ uint32_t slot_hash(uint32_t s) {
+    return ((((s >> 4) * 2654435761u) >> 23) << 4) | (s & 15u); // 13 bits
+}
+constexpr uint32_t kPackProbe = 17;
 
 // K independent upper-bound searches over arr[0 .. n) (n <= 1024, ascending): out[k] = the
 // smallest index whose value exceeds v[k].  Branchless and with a fixed step count, so the K
@@ -66,7 +73,7 @@ __device__ __forceinline__ void block_scan2(uint32_t &a, uint32_t &b, uint32_t *
         if (lane >= (uint32_t)off) { a += x; b += y; }
     }
     if (lane == 63) { wa[w] = a; wb[w] = b; }
-    __syncthreads();
+    lds_barrier();
     uint32_t pa = 0, pb = 0;
     for (uint32_t i = 0; i < w; i++) { pa += wa[i]; pb += wb[i]; }
     a += pa;
@@ -86,9 +93,10 @@ __global__ __launch_bounds__(1024) void pack_kernel(uint32_t n_seqs, const uint3
     __shared__ uint32_t w_a[16], w_b[16];
     // error: (row << 4) | code of the failing row with the lowest index, so the status is the
     // first failure in row order whatever the thread timing (codes are below 16)
-    __shared__ uint32_t carry, error;
+    // dup: some insert found its slot already present (only then can a row fail the check)
+    __shared__ uint32_t carry, error, dup;
     const uint32_t t = threadIdx.x;
-    if (t == 0) { carry = 0; error = 0xFFFFFFFFu; }
+    if (t == 0) { carry = 0; error = 0xFFFFFFFFu; dup = 0; }
     for (uint32_t i = t; i < kPackHash; i += 1024) { h_key[i] = kNone; h_row[i] = kNone; }
     const uint32_t P = 1u << page_shift;
     auto upper = [&](const uint32_t *arr, uint32_t n, uint32_t v) { // smallest b with arr[b] > v
@@ -113,10 +121,9 @@ __global__ __launch_bounds__(1024) void pack_kernel(uint32_t n_seqs, const uint3
             cu[b] = start;
             if (b == n_seqs - 1) cu[n_seqs] = start + n;
         }
-        __syncthreads();
-        __syncthreads();
+        lds_barrier();
         if (t == 1023) carry += scan[1023];
-        __syncthreads();
+        lds_barrier();
     }
     const uint32_t total = carry;
     // rejects the batch: no sequence has rows, no row has a slot (all max_rows slots, so a
@@ -127,6 +134,7 @@ __global__ __launch_bounds__(1024) void pack_kernel(uint32_t n_seqs, const uint3
         if (t == 0) *status = code;
     };
     if (total > max_rows) {
+        __syncthreads(); // the cu stores above land before the rejection overwrites them
         reject((uint32_t)(-LIA_E_ROWS));
         return;
     }
@@ -139,8 +147,9 @@ __global__ __launch_bounds__(1024) void pack_kernel(uint32_t n_seqs, const uint3
         uint32_t h = slot_hash(s), probes = 0;
         for (; probes < kPackHash; probes++) {
             const uint32_t k = atomicCAS(&h_key[h], kNone, s);
+            if (k == s) dup = 1;
             if (k == kNone || k == s) { atomicMin(&h_row[h], r); break; }
-            h = (h + 1) & (kPackHash - 1);
+            h = (h + kPackProbe) & (kPackHash - 1);
         }
         if (probes == kPackHash) { // table full (a pathological slot pattern): scan the rows
             for (uint32_t q = 0; q < r; q++)
@@ -156,7 +165,7 @@ __global__ __launch_bounds__(1024) void pack_kernel(uint32_t n_seqs, const uint3
                 return;
             }
             if (k == kNone) return;
-            h = (h + 1) & (kPackHash - 1);
+            h = (h + kPackProbe) & (kPackHash - 1);
         }
     };
     // the row's slot from its page (loaded by the caller), with the row checks
@@ -202,10 +211,12 @@ __global__ __launch_bounds__(1024) void pack_kernel(uint32_t n_seqs, const uint3
                 if (mine[k] != kNone) insert(mine[k], r);
             }
         }
-        __syncthreads();
+        lds_barrier(); // the hash (LDS); the rows' global stores need not have landed
+        if (dup) { // uniform; with no slot inserted twice no row can fail
 #pragma unroll
-        for (uint32_t k = 0; k < RPT; k++)
-            if (mine[k] != kNone) lookup(mine[k], t + k * 1024);
+            for (uint32_t k = 0; k < RPT; k++)
+                if (mine[k] != kNone) lookup(mine[k], t + k * 1024);
+        }
     } else {
         if (n_seqs <= 1024) {
             for (uint32_t r = t; r < total; r += 1024) {
@@ -233,17 +244,25 @@ __global__ __launch_bounds__(1024) void pack_kernel(uint32_t n_seqs, const uint3
                 if (s != kNone && s % passes == pass) insert(s, r);
             }
             __syncthreads();
-            for (uint32_t r = t; r < total; r += 1024) {
-                const uint32_t s = slot_mapping[r];
-                if (s != kNone && s % passes == pass) lookup(s, r);
+            if (dup) { // uniform
+                for (uint32_t r = t; r < total; r += 1024) {
+                    const uint32_t s = slot_mapping[r];
+                    if (s != kNone && s % passes == pass) lookup(s, r);
+                }
             }
             __syncthreads();
         }
     }
-    __syncthreads();
-    const uint32_t code = error == 0xFFFFFFFFu ? 0u : (error & 15u);
-    if (code) reject(code); // nothing downstream may run on a rejected batch
-    else if (t == 0) *status = 0;
+    lds_barrier();
+    const uint32_t code = error == 0xFFFFFFFFu ? 0u : (error & 15u); // uniform
+    if (code) {
+        // nothing downstream may run on a rejected batch; every row store of the workgroup
+        // lands before the rejection overwrites it
+        __syncthreads();
+        reject(code);
+    } else if (t == 0) {
+        *status = 0;
+    }
 }
 
 // Table checks of a packed step, launched right after pack_kernel.  The reference checks the
