@@ -66,9 +66,9 @@ def load_traffic(path, kernel_us, layer_bytes):
 def side_config(args):
     """One layer of BASELINE config 3 (mixed prefill + decode, MFMA-bound), 4 (MTP verify) or
     5 (FP8 decode) on resident synthetic data, timed as a step of its own: device packing,
-    the plan, the KV append of the step's rows fused into the attention launch (quantised on
-    FP8 pools), split attention and the combine,
-    replayed from a graph.  Prints a JSON line with the step time and the roofline of the
+    the plan, the KV append of the step's rows (fused into the attention launch on 16-bit
+    pools; on FP8 pools quantised by the append launch of the same call, just before the
+    attention launch), split attention and the combine, replayed from a graph.  Prints a JSON line with the step time and the roofline of the
     layer's algorithmic work."""
     import torch
     from __graft_entry__ import package
