@@ -449,9 +449,10 @@ __global__ __launch_bounds__(256) void plan_kernel(uint32_t n_seqs, const uint32
 // therefore split evenly whatever the segment lengths, and no end-of-segment merge is
 // needed: each wave writes its own slice of the output or of the split record.
 
-// Cache policy of the K/V loads per pool type: 2 (non-temporal) on 16-bit pools, where
-// each wave reads whole 128-byte lines of a token, 0 on FP8 pools, whose 64-byte slices
-// share a line between two waves.
+// Cache policy of the K/V loads: 2 (non-temporal) wherever a wave reads whole 128-byte lines
+// of a token - K and V on 16-bit pools, V on FP8 pools - and 0 for the K loads of FP8 pools,
+// whose 64-byte slices share a line between two waves (measured on config 5: V non-temporal
+// 197.3 -> 183.5 us per step; non-temporal on the shared K lines costs 5 %).
 
 template <int D, int KVT>
 struct Cfg {
@@ -463,7 +464,7 @@ struct Cfg {
     // contiguous bytes of a token per 16-token tile and load (its A-operand k slots), so
     // every load instruction reads 16 tokens x 64 bytes.
     static constexpr int SW = 64;
-    static constexpr int AUX = FP8 ? 0 : 2; // cache policy of the K/V loads
+    static constexpr int AUX = FP8 ? 0 : 2; // cache policy of the K loads (and 16-bit V)
     static constexpr int WAVES = D / SW;            // one wave per slice
     static constexpr int KS = SW / 32;              // k-steps of S^T = K Q^T per tile
     static constexpr int DTW = SW / 16;             // 16-dim tiles of O per wave
@@ -474,6 +475,9 @@ struct Cfg {
     static constexpr int CPR = SW / 8;              // 16-byte chunks of a staged V row
     static constexpr int VRPI = 64 / CPR;           // staged V rows per direct-to-LDS load
     static constexpr int NV = FP8 ? 2 : 32 / VRPI;  // V loads per chunk
+    static constexpr int CPT = D * EB / 16;         // FP8: 16-byte chunks of a head's row
+    static constexpr int TPI = 64 / CPT;            // FP8: tokens per V load (whole rows)
+    static_assert(!FP8 || TPI * WAVES == 16, "the waves' V loads cover a 16-token tile");
 };
 
 // Staged V rows hold 64 16-bit values (8 chunks of 16 bytes); chunk c of row r sits in slot
@@ -623,15 +627,17 @@ __device__ __forceinline__ void load_chunk(const AttnParams &p, Chunk<D, KVT> &c
         }
     }
     if constexpr (C::FP8) {
-        // V slice into registers: lane l of tile j reads token 16j + l/4, bytes 16(l%4) ..
-        // +15 of the slice (16 dims), through a descriptor over the V plane bounded like K's.
+        // V into registers as whole head rows: wave w reads tokens TPI*w .. +TPI-1 of each
+        // tile (lane l: token TPI*w + l/CPT, bytes 16(l%CPT) .. +15 of the head's row), so every
+        // load reads whole lines; each wave stages both halves of its rows for the wave that
+        // owns those dims.  Bounded like K.
 #pragma unroll
         for (int j = 0; j < 2; j++) {
             const __amdgpu_buffer_rsrc_t vr =
                 make_rsrc(vbase + (size_t)tp.page[j] * P * row_bytes, tp.live[j] * row_bytes);
-            const uint32_t off = (((t + 16 * j) & (P - 1)) + (lane >> 2)) * row_bytes + slice_off +
-                                 16 * (lane & 3);
-            c.v[j] = buffer_load16_p<C::AUX>(vr, off);
+            const uint32_t off = (((t + 16 * j) & (P - 1)) + C::TPI * wave + lane / C::CPT) * row_bytes +
+                                 hk * D * C::EB + 16 * (lane % C::CPT);
+            c.v[j] = buffer_load16_p<2>(vr, off); // whole lines, read once: non-temporal
         }
     } else {
         // V slice goes straight to this wave's LDS stage: load s fills rows VRPI*s ..
@@ -716,17 +722,20 @@ __device__ __forceinline__ void compute_chunk(const AttnParams &p, const Chunk<D
     using C = Cfg<D, KVT>;
     const uint32_t lane = lane_id(), g = lane >> 4, li = lane & 15;
     if constexpr (C::FP8) {
-        // convert the wave's FP8 V slice (16 values per lane and tile) to f16 and stage it:
-        // lane l of tile j holds dims 16(l%4) .. +15 of token 16j + l/4 = 8-value chunks
-        // 2(l%4) and 2(l%4) + 1 of that row
+        // convert this lane's FP8 V (16 values per tile) to f16 and stage it: lane l of tile j
+        // holds dims 16(l%CPT) .. +15 of token 16j + TPI*w + l/CPT, i.e. 8-value chunks c0 and
+        // c0 + 1 (c0 = 2(l%CPT)) of the head's row, which belong to the stage of the wave owning
+        // dims 64(c0/8) .. (staging is double-buffered by chunk and read after the barrier)
+        uint16_t *base = stage - wave * C::STAGE;
 #pragma unroll
         for (int j = 0; j < 2; j++) {
-            const uint32_t row = 16 * j + (lane >> 2), c0 = 2 * (lane & 3);
+            const uint32_t row = 16 * j + C::TPI * wave + lane / C::CPT, c0 = 2 * (lane % C::CPT);
             const u32x2 a = e4m3x4_to_f16x4_scaled(c.v[j].x), b = e4m3x4_to_f16x4_scaled(c.v[j].y);
             const u32x2 e = e4m3x4_to_f16x4_scaled(c.v[j].z), f = e4m3x4_to_f16x4_scaled(c.v[j].w);
-            uint16_t *dst = stage + row * C::SW;
-            *(u32x4 *)(dst + ((c0 ^ vswz(row)) * 8)) = u32x4{a.x, a.y, b.x, b.y};
-            *(u32x4 *)(dst + (((c0 + 1) ^ vswz(row)) * 8)) = u32x4{e.x, e.y, f.x, f.y};
+            uint16_t *dst = base + (c0 / 8) * C::STAGE + row * C::SW;
+            const uint32_t cc = c0 % 8;
+            *(u32x4 *)(dst + ((cc ^ vswz(row)) * 8)) = u32x4{a.x, a.y, b.x, b.y};
+            *(u32x4 *)(dst + (((cc + 1) ^ vswz(row)) * 8)) = u32x4{e.x, e.y, f.x, f.y};
         }
     } else {
         wait_vmcnt<VW>(); // this chunk's V is in LDS (VW = memory ops issued after its loads)
