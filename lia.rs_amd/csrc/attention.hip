@@ -449,10 +449,11 @@ __global__ __launch_bounds__(256) void plan_kernel(uint32_t n_seqs, const uint32
 // therefore split evenly whatever the segment lengths, and no end-of-segment merge is
 // needed: each wave writes its own slice of the output or of the split record.
 
-// Cache policy of the K/V loads: 2 (non-temporal) wherever a wave reads whole 128-byte lines
-// of a token - K and V on 16-bit pools, V on FP8 pools - and 0 for the K loads of FP8 pools,
-// whose 64-byte slices share a line between two waves (measured on config 5: V non-temporal
-// 197.3 -> 183.5 us per step; non-temporal on the shared K lines costs 5 %).
+// Cache policy of the K/V loads: 2 (non-temporal; every key is read once).  On FP8 pools the V
+// loads read whole 128-byte head rows per wave; the K loads of the two waves share each line
+// (64-byte slices).  Measured on config 5 (one-layer step): V as whole rows with the default
+// policy 197.3 -> 196.6 us, non-temporal 183.5 us, and non-temporal K as well 179.1 us (with V
+// still in 64-byte slices the non-temporal policy had cost 5 %).
 
 template <int D, int KVT>
 struct Cfg {
@@ -464,7 +465,7 @@ struct Cfg {
     // contiguous bytes of a token per 16-token tile and load (its A-operand k slots), so
     // every load instruction reads 16 tokens x 64 bytes.
     static constexpr int SW = 64;
-    static constexpr int AUX = FP8 ? 0 : 2; // cache policy of the K loads (and 16-bit V)
+    static constexpr int AUX = 2;           // cache policy of the K/V loads
     static constexpr int WAVES = D / SW;            // one wave per slice
     static constexpr int KS = SW / 32;              // k-steps of S^T = K Q^T per tile
     static constexpr int DTW = SW / 16;             // 16-dim tiles of O per wave
@@ -637,7 +638,7 @@ __device__ __forceinline__ void load_chunk(const AttnParams &p, Chunk<D, KVT> &c
                 make_rsrc(vbase + (size_t)tp.page[j] * P * row_bytes, tp.live[j] * row_bytes);
             const uint32_t off = (((t + 16 * j) & (P - 1)) + C::TPI * wave + lane / C::CPT) * row_bytes +
                                  hk * D * C::EB + 16 * (lane % C::CPT);
-            c.v[j] = buffer_load16_p<2>(vr, off); // whole lines, read once: non-temporal
+            c.v[j] = buffer_load16_p<C::AUX>(vr, off);
         }
     } else {
         // V slice goes straight to this wave's LDS stage: load s fills rows VRPI*s ..
@@ -652,10 +653,8 @@ __device__ __forceinline__ void load_chunk(const AttnParams &p, Chunk<D, KVT> &c
             const uint32_t chunk = (lane % C::CPR) ^ vswz(row);
             const uint32_t off = (((t + 16 * j) & (P - 1)) + (row & 15)) * row_bytes + slice_off + 16 * chunk;
             auto *dst = (__attribute__((address_space(3))) void *)(stage + s * 512);
-            if constexpr (C::AUX == 2)
-                __builtin_amdgcn_raw_ptr_buffer_load_lds(vr, dst, 16, off, 0, 0, 2);
-            else
-                __builtin_amdgcn_raw_ptr_buffer_load_lds(vr, dst, 16, off, 0, 0, 0);
+            static_assert(C::AUX == 2, "the direct-to-LDS V loads are non-temporal");
+            __builtin_amdgcn_raw_ptr_buffer_load_lds(vr, dst, 16, off, 0, 0, 2);
         }
     }
     __builtin_amdgcn_sched_barrier(0);
