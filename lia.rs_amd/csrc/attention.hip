@@ -153,10 +153,11 @@ __device__ __forceinline__ uint32_t new_blocks_before(uint32_t m, uint32_t rpc) 
     return (uint32_t)floor_sum(m, 32, rpc, rpc + 31);
 }
 
-constexpr uint32_t kPlanSeqs = 1024; // sequences the plan keeps in LDS
+constexpr uint32_t kPlanSeqs = 1024; // sequences the plan keeps in LDS (one per thread)
+constexpr uint32_t kPlanThreads = 1024;
 
-// The plan for up to kPlanSeqs sequences: per-sequence extents in LDS and every unit in
-// closed form (unit (h, cb) of sequence b starts at block b0 + h*nbh + cb*cblocks +
+// The plan for up to kPlanSeqs sequences, one thread each (kPlanThreads): per-sequence extents
+// in LDS (a shuffle scan with one barrier) and every unit in closed form (unit (h, cb) of sequence b starts at block b0 + h*nbh + cb*cblocks +
 // new_blocks_before(cb)), so units, merge descriptors and the work list are each written
 // in parallel with no serial per-sequence loop and no reads of the units just written.
 __device__ void plan_lds(uint32_t n_seqs, const uint32_t *cu, const uint32_t *positions,
@@ -166,15 +167,14 @@ __device__ void plan_lds(uint32_t n_seqs, const uint32_t *cu, const uint32_t *po
                          uint32_t *header) {
     __shared__ uint32_t s_r0[kPlanSeqs], s_nr[kPlanSeqs], s_p0[kPlanSeqs], s_trow[kPlanSeqs];
     __shared__ uint32_t s_u0[kPlanSeqs + 1], s_b0[kPlanSeqs + 1];
-    __shared__ uint32_t s_units[256], s_blocks[256];
+    __shared__ uint32_t w_a[kPlanThreads / 64], w_b[kPlanThreads / 64];
     __shared__ uint32_t carry_units, carry_blocks;
     // Threads exchange only LDS data (nothing written to global memory is read back), so the
     // barriers need not wait for the descriptor stores in flight.
+    constexpr uint32_t T = kPlanThreads;
     const uint32_t t = threadIdx.x;
-    if (t == 0) { carry_units = 0; carry_blocks = 0; }
-    lds_barrier();
-    for (uint32_t base = 0; base < n_seqs; base += 256) {
-        const uint32_t b = base + t;
+    {
+        const uint32_t b = t;
         uint32_t nu = 0, nb = 0, r0 = 0, nr = 0, p0 = 0, trow = 0;
         if (b < n_seqs) {
             r0 = cu[b];
@@ -188,22 +188,13 @@ __device__ void plan_lds(uint32_t n_seqs, const uint32_t *cu, const uint32_t *po
             }
             s_r0[b] = r0; s_nr[b] = nr; s_p0[b] = p0; s_trow[b] = trow;
         }
-        s_units[t] = nu;
-        s_blocks[t] = nb;
-        lds_barrier();
-        for (uint32_t off = 1; off < 256; off <<= 1) { // inclusive Hillis-Steele scan
-            uint32_t a = t >= off ? s_units[t - off] : 0, c = t >= off ? s_blocks[t - off] : 0;
-            lds_barrier();
-            s_units[t] += a;
-            s_blocks[t] += c;
-            lds_barrier();
-        }
+        uint32_t su = nu, sb = nb;
+        block_scan2(su, sb, w_a, w_b); // inclusive
         if (b < n_seqs) {
-            s_u0[b] = carry_units + s_units[t] - nu;
-            s_b0[b] = carry_blocks + s_blocks[t] - nb;
+            s_u0[b] = su - nu;
+            s_b0[b] = sb - nb;
         }
-        lds_barrier();
-        if (t == 255) { carry_units += s_units[255]; carry_blocks += s_blocks[255]; }
+        if (t == T - 1) { carry_units = su; carry_blocks = sb; }
         lds_barrier();
     }
     const bool overflow = carry_units > max_units;
@@ -241,13 +232,13 @@ __device__ void plan_lds(uint32_t n_seqs, const uint32_t *cu, const uint32_t *po
         const uint32_t b = seq_of(s_u0, u), ncb = (s_nr[b] + rpc - 1) / rpc, i = u - s_u0[b];
         return make_unit(b, i / ncb, i % ncb);
     };
-    for (uint32_t u = t; u < U; u += 256) units[u] = unit_by_index(u);
+    for (uint32_t u = t; u < U; u += T) units[u] = unit_by_index(u);
     const uint32_t P = 1u << page_shift;
-    for (uint32_t w = N + t; w < n_wg; w += 256) { // launched workgroups without work
+    for (uint32_t w = N + t; w < n_wg; w += T) { // launched workgroups without work
         WorkDesc d = {};
         work[w] = d;
     }
-    for (uint32_t u = t; u < max_units; u += 256) {
+    for (uint32_t u = t; u < max_units; u += T) {
         MergeDesc m = {0, 0, 0, 0};
         if (u < U) {
             const UnitDesc ud = unit_by_index(u);
@@ -260,14 +251,14 @@ __device__ void plan_lds(uint32_t n_seqs, const uint32_t *cu, const uint32_t *po
     auto range_lo = [&](uint32_t w) { return (uint32_t)((uint64_t)w * B / N); };
     const bool xcd_major = N == n_wg && N % 8 == 0;
     const uint32_t per = N / 8;
-    // Work descriptors four at a time, so the page-table reads of all four are in flight
-    // together (unconditional loads: an entry not needed reads cu[0] and is replaced by 0).
-    for (uint32_t w0 = t; w0 < N; w0 += 4 * 256) {
-        WorkDesc d[4];
-        uint32_t v[4][kPrePages];
+    // One work descriptor per thread and pass (unconditional page-table loads: an entry not
+    // needed reads cu[0] and is replaced by 0).
+    for (uint32_t w0 = t; w0 < N; w0 += T) {
+        WorkDesc d[1];
+        uint32_t v[1][kPrePages];
 #pragma unroll
-        for (int k = 0; k < 4; k++) {
-            const uint32_t w = min(w0 + k * 256, N - 1); // past N: a copy of the last, not stored
+        for (int k = 0; k < 1; k++) {
+            const uint32_t w = w0;
             const uint32_t r = xcd_major ? (w % 8) * per + w / 8 : w;
             const uint32_t lo = range_lo(r), hi = range_lo(r + 1);
             // the unit holding block lo: its sequence, KV head, then column block
@@ -299,14 +290,22 @@ __device__ void plan_lds(uint32_t n_seqs, const uint32_t *cu, const uint32_t *po
             }
             if (pre) d[k].flags |= 1;
         }
-#pragma unroll
-        for (int k = 0; k < 4; k++) {
-            d[k].pre = make_uint4(v[k][0], v[k][1], v[k][2], v[k][3]);
-            if (w0 + k * 256 < N) work[w0 + k * 256] = d[k];
-        }
+        d[0].pre = make_uint4(v[0][0], v[0][1], v[0][2], v[0][3]);
+        work[w0] = d[0];
     }
 }
 
+__global__ __launch_bounds__(kPlanThreads) void plan_lds_kernel(
+    uint32_t n_seqs, const uint32_t *cu, const uint32_t *positions, const uint32_t *sequences,
+    const uint32_t *pages, uint32_t stride, uint32_t page_shift, uint32_t rpc, uint32_t hkv,
+    uint32_t max_units, uint32_t n_wg, UnitDesc *units, WorkDesc *work, MergeDesc *merge,
+    uint32_t *header) {
+    plan_lds(n_seqs, cu, positions, sequences, pages, stride, page_shift, rpc, hkv, max_units, n_wg,
+             units, work, merge, header);
+}
+
+// The plan for more sequences than plan_lds_kernel holds: units written by a serial walk of
+// each thread's sequences.
 __global__ __launch_bounds__(256) void plan_kernel(uint32_t n_seqs, const uint32_t *cu,
                                                    const uint32_t *positions,
                                                    const uint32_t *sequences, const uint32_t *pages,
@@ -314,11 +313,6 @@ __global__ __launch_bounds__(256) void plan_kernel(uint32_t n_seqs, const uint32
                                                    uint32_t hkv, uint32_t max_units,
                                                    uint32_t n_wg, UnitDesc *units, WorkDesc *work,
                                                    MergeDesc *merge, uint32_t *header) {
-    if (n_seqs <= kPlanSeqs) {
-        plan_lds(n_seqs, cu, positions, sequences, pages, stride, page_shift, rpc, hkv, max_units, n_wg,
-                 units, work, merge, header);
-        return;
-    }
     __shared__ uint32_t s_units[256], s_blocks[256];
     __shared__ uint32_t carry_units, carry_blocks, overflow;
     const uint32_t t = threadIdx.x;
@@ -2170,11 +2164,20 @@ static int run_stages(int stages, const lia_attention_config *c, uint32_t n_seqs
     p.n_rows = n_rows;
     hipStream_t s = (hipStream_t)stream;
     hipError_t e = hipSuccess;
-    if (stages & kPlan)
-        e = launch<plan_kernel>(dim3(1), dim3(256), 0, s, n_seqs, cu_seqlens, positions, sequences,
-                                pages, c->stride, p.page_shift, rpc, c->num_kv_heads, L.max_units,
-                                n_wg, (UnitDesc *)(ws + L.units), (WorkDesc *)(ws + L.work),
-                                (MergeDesc *)(ws + L.merge), (uint32_t *)(ws + L.header));
+    if (stages & kPlan) {
+        UnitDesc *units = (UnitDesc *)(ws + L.units);
+        WorkDesc *work = (WorkDesc *)(ws + L.work);
+        MergeDesc *merge = (MergeDesc *)(ws + L.merge);
+        uint32_t *header = (uint32_t *)(ws + L.header);
+        if (n_seqs <= kPlanSeqs)
+            e = launch<plan_lds_kernel>(dim3(1), dim3(kPlanThreads), 0, s, n_seqs, cu_seqlens,
+                                        positions, sequences, pages, c->stride, p.page_shift, rpc,
+                                        c->num_kv_heads, L.max_units, n_wg, units, work, merge, header);
+        else
+            e = launch<plan_kernel>(dim3(1), dim3(256), 0, s, n_seqs, cu_seqlens, positions,
+                                    sequences, pages, c->stride, p.page_shift, rpc, c->num_kv_heads,
+                                    L.max_units, n_wg, units, work, merge, header);
+    }
     if (e == hipSuccess && (stages & kPartial)) {
         if (c->head_dim == 128) {
             if (NT == 1) e = launch_partial_kv<128, 1>(c->kv_dtype, p, n_wg, s);

@@ -163,6 +163,24 @@ __device__ __forceinline__ void lds_barrier() {
     asm volatile("s_waitcnt lgkmcnt(0)\n\ts_barrier" ::: "memory");
 }
 
+// Inclusive scan of two values over the threads of a workgroup (wa / wb hold one value per
+// wave): shuffle scans within each wave, then the wave totals through LDS (one barrier; wa /
+// wb must not be rewritten until every thread has passed the next barrier).
+__device__ __forceinline__ void block_scan2(uint32_t &a, uint32_t &b, uint32_t *wa, uint32_t *wb) {
+    const uint32_t lane = threadIdx.x & 63, w = threadIdx.x >> 6;
+#pragma unroll
+    for (int off = 1; off < 64; off <<= 1) {
+        const uint32_t x = __shfl_up(a, off), y = __shfl_up(b, off);
+        if (lane >= (uint32_t)off) { a += x; b += y; }
+    }
+    if (lane == 63) { wa[w] = a; wb[w] = b; }
+    lds_barrier();
+    uint32_t pa = 0, pb = 0;
+    for (uint32_t i = 0; i < w; i++) { pa += wa[i]; pb += wb[i]; }
+    a += pa;
+    b += pb;
+}
+
 // Raw buffer resource over [base, base + bytes): loads at or past `bytes` return zeros and
 // touch no memory, which lets a loop issue every load unconditionally.
 constexpr int kBufferConfig = 0x00020000; // gfx9 raw buffer, 32-bit data format

@@ -62,24 +62,6 @@ __device__ __forceinline__ void upper_many(const uint32_t *arr, uint32_t n, cons
     }
 }
 
-// Inclusive scan of two values over the 1024 threads of a workgroup: shuffle scans within
-// each wave, then the wave totals through LDS (one barrier; wa / wb must not be rewritten
-// until every thread has passed the next barrier).
-__device__ __forceinline__ void block_scan2(uint32_t &a, uint32_t &b, uint32_t *wa, uint32_t *wb) {
-    const uint32_t lane = threadIdx.x & 63, w = threadIdx.x >> 6;
-#pragma unroll
-    for (int off = 1; off < 64; off <<= 1) {
-        const uint32_t x = __shfl_up(a, off), y = __shfl_up(b, off);
-        if (lane >= (uint32_t)off) { a += x; b += y; }
-    }
-    if (lane == 63) { wa[w] = a; wb[w] = b; }
-    lds_barrier();
-    uint32_t pa = 0, pb = 0;
-    for (uint32_t i = 0; i < w; i++) { pa += wa[i]; pb += wb[i]; }
-    a += pa;
-    b += pb;
-}
-
 __global__ __launch_bounds__(1024) void pack_kernel(uint32_t n_seqs, const uint32_t *seq_slots,
                                                     const uint32_t *q_lens, const uint32_t *cached,
                                                     const uint32_t *pages, uint32_t stride,
