@@ -155,18 +155,25 @@ __device__ __forceinline__ uint32_t new_blocks_before(uint32_t m, uint32_t rpc) 
 
 constexpr uint32_t kPlanSeqs = 1024; // sequences the plan keeps in LDS (one per thread)
 constexpr uint32_t kPlanThreads = 1024;
+// Cost of starting a unit, in 32-key blocks, that the balanced partition charges each unit: a
+// range crossing into a unit loads its queries, unit descriptor and page window before its first
+// keys.  Measured best: 8 for the prefill kernel (config 3 step 303 -> 246 us against no charge),
+// 4 for the decode kernel (config 2 8,320 -> 8,540 tokens/s; configs 4 and 5 lose beyond 4).
+constexpr uint32_t kUnitCostWide = 8, kUnitCostDecode = 4;
 
 // The plan for up to kPlanSeqs sequences, one thread each (kPlanThreads): per-sequence extents
-// in LDS (a shuffle scan with one barrier) and every unit in closed form (unit (h, cb) of sequence b starts at block b0 + h*nbh + cb*cblocks +
-// new_blocks_before(cb)), so units, merge descriptors and the work list are each written
-// in parallel with no serial per-sequence loop and no reads of the units just written.
+// in LDS (a shuffle scan with one barrier) and every unit in closed form (unit (h, cb) of
+// sequence b starts at block b0 + h*nbh + cb*cblocks + new_blocks_before(cb)), so units, merge
+// descriptors and the work list are each written in parallel with no serial per-sequence loop
+// and no reads of the units just written.  Workgroups get equal shares of cost: the blocks plus
+// unit_cost per unit (its start).
 __device__ void plan_lds(uint32_t n_seqs, const uint32_t *cu, const uint32_t *positions,
                          const uint32_t *sequences, const uint32_t *pages, uint32_t stride,
                          uint32_t page_shift, uint32_t rpc, uint32_t hkv, uint32_t max_units,
-                         uint32_t n_wg, UnitDesc *units, WorkDesc *work, MergeDesc *merge,
-                         uint32_t *header) {
+                         uint32_t n_wg, uint32_t unit_cost, UnitDesc *units, WorkDesc *work,
+                         MergeDesc *merge, uint32_t *header) {
     __shared__ uint32_t s_r0[kPlanSeqs], s_nr[kPlanSeqs], s_p0[kPlanSeqs], s_trow[kPlanSeqs];
-    __shared__ uint32_t s_u0[kPlanSeqs + 1], s_b0[kPlanSeqs + 1];
+    __shared__ uint32_t s_u0[kPlanSeqs + 1], s_b0[kPlanSeqs + 1], s_c0[kPlanSeqs + 1];
     __shared__ uint32_t w_a[kPlanThreads / 64], w_b[kPlanThreads / 64];
     __shared__ uint32_t carry_units, carry_blocks;
     // Threads exchange only LDS data (nothing written to global memory is read back), so the
@@ -193,6 +200,7 @@ __device__ void plan_lds(uint32_t n_seqs, const uint32_t *cu, const uint32_t *po
         if (b < n_seqs) {
             s_u0[b] = su - nu;
             s_b0[b] = sb - nb;
+            s_c0[b] = sb - nb + unit_cost * (su - nu);
         }
         if (t == T - 1) { carry_units = su; carry_blocks = sb; }
         lds_barrier();
@@ -203,6 +211,7 @@ __device__ void plan_lds(uint32_t n_seqs, const uint32_t *cu, const uint32_t *po
     if (t == 0) {
         s_u0[n_seqs] = carry_units;
         s_b0[n_seqs] = carry_blocks;
+        s_c0[n_seqs] = carry_blocks + unit_cost * carry_units;
         units[U] = UnitDesc{B, 0, 0, 0, 0, 0, 0, 0};
         header[0] = U;
         header[1] = B;
@@ -238,17 +247,43 @@ __device__ void plan_lds(uint32_t n_seqs, const uint32_t *cu, const uint32_t *po
         WorkDesc d = {};
         work[w] = d;
     }
+    // Work is split in cost: each unit's blocks are preceded by unit_cost virtual blocks (the
+    // cost of starting a unit), so a range that crosses into a unit is shorter by that much and a
+    // boundary falling in a unit's lead-in moves to the unit's start.
+    const uint64_t TC = (uint64_t)B + (uint64_t)unit_cost * U;
     for (uint32_t u = t; u < max_units; u += T) {
         MergeDesc m = {0, 0, 0, 0};
         if (u < U) {
             const UnitDesc ud = unit_by_index(u);
-            const uint32_t wf = (uint32_t)((((uint64_t)ud.block_start + 1) * N - 1) / B);
-            const uint32_t wl = (uint32_t)((((uint64_t)ud.block_start + ud.nblocks) * N - 1) / B);
+            const uint64_t cu0 = (uint64_t)ud.block_start + unit_cost * (u + 1); // cost of its first block
+            const uint32_t wf = (uint32_t)(((cu0 + 1) * N - 1) / TC);
+            const uint32_t wl = (uint32_t)(((cu0 + ud.nblocks) * N - 1) / TC);
             if (wf != wl) m = MergeDesc{wf + u, wl - wf + 1, ud.rowbeg, ud.nrows_hk};
         }
         merge[u] = m;
     }
-    auto range_lo = [&](uint32_t w) { return (uint32_t)((uint64_t)w * B / N); };
+    // The block at cost c, and its unit (sequence ub, KV head uh, column block ucb): in cost,
+    // sequence b starts at s_c0[b], a KV head's units span nbh + unit_cost * ncb, and a unit's
+    // blocks follow its unit_cost lead-in; a cost inside a lead-in maps to the unit's first block.
+    auto block_of_cost = [&](uint64_t c, uint32_t &ub, uint32_t &uh, uint32_t &ucb) {
+        if (c >= TC) { ub = n_seqs; return B; }
+        const uint32_t cc = (uint32_t)c;
+        const uint32_t b = seq_of(s_c0, cc);
+        const uint32_t ncb = (s_nr[b] + rpc - 1) / rpc, cblocks = (s_p0[b] + 31) / 32;
+        const uint32_t nbh = (s_b0[b + 1] - s_b0[b]) / hkv;
+        const uint32_t hsp = nbh + unit_cost * ncb, co = cc - s_c0[b];
+        const uint32_t h = co / hsp, co2 = co - h * hsp;
+        uint32_t cb = 0, e = ncb; // last cb whose cost start <= co2
+        while (cb + 1 < e) {
+            const uint32_t mid = (cb + e) >> 1;
+            if (mid * cblocks + new_blocks_before(mid, rpc) + unit_cost * mid <= co2) cb = mid; else e = mid;
+        }
+        const uint32_t ustart = cb * cblocks + new_blocks_before(cb, rpc);
+        const uint32_t off = co2 - (ustart + unit_cost * cb);
+        ub = b; uh = h; ucb = cb;
+        return s_b0[b] + h * nbh + ustart + (off < unit_cost ? 0u : off - unit_cost);
+    };
+    auto range_lo = [&](uint32_t w) { return (uint64_t)w * TC / N; };
     const bool xcd_major = N == n_wg && N % 8 == 0;
     const uint32_t per = N / 8;
     // One work descriptor per thread and pass (unconditional page-table loads: an entry not
@@ -256,21 +291,15 @@ __device__ void plan_lds(uint32_t n_seqs, const uint32_t *cu, const uint32_t *po
     for (uint32_t w0 = t; w0 < N; w0 += T) {
         WorkDesc d[1];
         uint32_t v[1][kPrePages];
-#pragma unroll
-        for (int k = 0; k < 1; k++) {
+        {
+            constexpr int k = 0;
             const uint32_t w = w0;
             const uint32_t r = xcd_major ? (w % 8) * per + w / 8 : w;
-            const uint32_t lo = range_lo(r), hi = range_lo(r + 1);
-            // the unit holding block lo: its sequence, KV head, then column block
-            const uint32_t b = seq_of(s_b0, lo);
-            const uint32_t ncb = (s_nr[b] + rpc - 1) / rpc, cblocks = (s_p0[b] + 31) / 32;
-            const uint32_t nbh = (s_b0[b + 1] - s_b0[b]) / hkv, off = lo - s_b0[b];
-            const uint32_t h = off / nbh, rem = off - h * nbh;
-            uint32_t c = 0, e = ncb; // last cb whose first block <= rem
-            while (c + 1 < e) {
-                const uint32_t mid = (c + e) >> 1;
-                if (mid * cblocks + new_blocks_before(mid, rpc) <= rem) c = mid; else e = mid;
-            }
+            uint32_t b, h, c, b2, h2, c2;
+            const uint32_t lo = block_of_cost(range_lo(r), b, h, c);
+            const uint32_t hi = block_of_cost(range_lo(r + 1), b2, h2, c2);
+            if (b >= n_seqs) { b = 0; h = 0; c = 0; } // empty range at the end
+            const uint32_t ncb = (s_nr[b] + rpc - 1) / rpc;
             d[k].unit = s_u0[b] + h * ncb + c;
             d[k].first = make_unit(b, h, c);
             d[k].flags = r << 8;
@@ -298,10 +327,10 @@ __device__ void plan_lds(uint32_t n_seqs, const uint32_t *cu, const uint32_t *po
 __global__ __launch_bounds__(kPlanThreads) void plan_lds_kernel(
     uint32_t n_seqs, const uint32_t *cu, const uint32_t *positions, const uint32_t *sequences,
     const uint32_t *pages, uint32_t stride, uint32_t page_shift, uint32_t rpc, uint32_t hkv,
-    uint32_t max_units, uint32_t n_wg, UnitDesc *units, WorkDesc *work, MergeDesc *merge,
-    uint32_t *header) {
+    uint32_t max_units, uint32_t n_wg, uint32_t unit_cost, UnitDesc *units, WorkDesc *work,
+    MergeDesc *merge, uint32_t *header) {
     plan_lds(n_seqs, cu, positions, sequences, pages, stride, page_shift, rpc, hkv, max_units, n_wg,
-             units, work, merge, header);
+             unit_cost, units, work, merge, header);
 }
 
 // The plan for more sequences than plan_lds_kernel holds: units written by a serial walk of
@@ -2172,7 +2201,9 @@ static int run_stages(int stages, const lia_attention_config *c, uint32_t n_seqs
         if (n_seqs <= kPlanSeqs)
             e = launch<plan_lds_kernel>(dim3(1), dim3(kPlanThreads), 0, s, n_seqs, cu_seqlens,
                                         positions, sequences, pages, c->stride, p.page_shift, rpc,
-                                        c->num_kv_heads, L.max_units, n_wg, units, work, merge, header);
+                                        c->num_kv_heads, L.max_units, n_wg,
+                                        NT == kWideNT ? kUnitCostWide : kUnitCostDecode, units,
+                                        work, merge, header);
         else
             e = launch<plan_kernel>(dim3(1), dim3(256), 0, s, n_seqs, cu_seqlens, positions,
                                     sequences, pages, c->stride, p.page_shift, rpc, c->num_kv_heads,
