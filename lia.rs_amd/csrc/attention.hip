@@ -1177,10 +1177,12 @@ __global__ __launch_bounds__(D / 32 * 64, kMinWavesPerEU<KVT>) void attention_ke
 // rows, so the decode kernel's split over head_dim - every wave reading its own slice of K
 // and V, 16-32 columns per workgroup - would re-read the K/V of a prefix once per 4 rows.
 // Here a workgroup covers 128 columns ((row, query head) pairs of one KV head: 16 rows x 8
-// heads at GQA 8) and each of its 8 waves owns one 16-column tile over the full head_dim
-// (measured: 8 x 16 beats 4 x 32 - more waves per SIMD hide the LDS -> MFMA -> softmax
-// chain - and 16 x 16).  Every 32-token chunk of K and V is staged once in LDS with
-// direct-to-LDS loads (spread over the waves) and read by all of them: K as the A operand of S^T = K Q^T (one
+// heads at GQA 8) and each of its 4 waves owns two 16-column tiles over the full head_dim.
+// Each K and V operand read from LDS then feeds two MFMAs: LDS reads are the kernel's largest
+// single cost, and 4 x 32 at 2 waves per SIMD (199 VGPRs) beats 8 x 16 at 4 (measured 3 %
+// on a mixed prefill step; 4 x 32 held to 3 waves per SIMD spills and is 8 % slower).  Every
+// 32-token chunk of K and V is staged once in LDS with direct-to-LDS loads (spread over the
+// waves) and read by all of them: K as the A operand of S^T = K Q^T (one
 // 16-byte read per lane per 16 tokens x 32 dims; chunk positions XOR-swizzled by token so
 // the 16 rows of a read hit distinct banks), V through transpose reads as the A operand of
 // O^T += V^T P^T (swizzled so the 4 rows of a transpose read hit distinct banks).  Three
@@ -1190,8 +1192,8 @@ __global__ __launch_bounds__(D / 32 * 64, kMinWavesPerEU<KVT>) void attention_ke
 // kernel's; records hold 128 columns.
 template <int D>
 struct WCfg {
-    static constexpr int WAVES = 8;
-    static constexpr int NTW = 1;               // 16-column tiles per wave
+    static constexpr int WAVES = 4;
+    static constexpr int NTW = 2;               // 16-column tiles per wave
     static constexpr int THREADS = 64 * WAVES;
     static constexpr int COLS = 16 * NTW * WAVES;
     static constexpr int ROWB = 2 * D;          // bytes of one token's head (16-bit KV)
@@ -1264,38 +1266,50 @@ __device__ __forceinline__ WideTile wide_tile(const WideWindow &w, uint32_t t0, 
     return r;
 }
 
-// The tile of chunk t that this wave loads (each wave loads RPI consecutive tokens of one
-// 16-token tile).
+// The tile of chunk t that this wave's k-th load reads (each load reads RPI consecutive
+// tokens of one 16-token tile).
 template <int D>
-__device__ __forceinline__ uint32_t wide_tile_key(uint32_t t, uint32_t wave) {
-    return t + 16 * ((wave * WCfg<D>::RPI) / 16);
+__device__ __forceinline__ uint32_t wide_tile_key(uint32_t t, uint32_t wave, int k) {
+    return t + 16 * (((wave + k * WCfg<D>::WAVES) * WCfg<D>::RPI) / 16);
 }
 
 // This wave's quarter of chunk t of K and V (from the pool or the step's rows) into LDS, from
 // the wave's tile (wide_tile_key).
 template <int D>
-__device__ __forceinline__ void wide_load(const AttnParams &p, uint32_t t, const WideTile &tile,
-                                          const uint8_t *kbase, const uint8_t *vbase, uint32_t hk,
-                                          uint32_t wave, uint16_t *kst, uint16_t *vst) {
+__device__ __forceinline__ void wide_load(const AttnParams &p, uint32_t t,
+                                          const WideTile (&tile)[WCfg<D>::PER], const uint8_t *kbase,
+                                          const uint8_t *vbase, uint32_t hk, uint32_t wave,
+                                          uint16_t *kst, uint16_t *vst) {
     using W = WCfg<D>;
-    static_assert(W::PER == 1, "one direct-to-LDS instruction per wave and plane");
     const uint32_t lane = lane_id(), P = 1u << p.page_shift;
     const uint32_t row_bytes = p.hkv * W::ROWB;
     __builtin_amdgcn_s_waitcnt(0xC07F); // lgkmcnt(0): this wave's reads of the stage are done
-    const uint32_t q = wave;                       // instruction: tokens q*RPI .. +RPI-1
-    if (W::NI % W::WAVES == 0 || q < W::NI) {      // waves past the last instruction load nothing
-        const uint32_t tl = q * W::RPI + lane / W::CH; // token within the chunk
-        const uint32_t pos = lane % W::CH;
-        const uint32_t rowoff = ((t + tl) & (P - 1)) * row_bytes + hk * W::ROWB;
-        const uint32_t base_k = (pos ^ swz_k<D>(tl)) * 16, base_v = (pos ^ swz_v<D>(tl)) * 16;
-        const __amdgpu_buffer_rsrc_t rk = make_rsrc(kbase + tile.off, tile.bytes);
-        const __amdgpu_buffer_rsrc_t rv = make_rsrc(vbase + tile.off, tile.bytes);
-        __builtin_amdgcn_raw_ptr_buffer_load_lds(
-            rk, (__attribute__((address_space(3))) void *)(kst + q * 512), 16, rowoff + base_k, 0, 0, 0);
-        __builtin_amdgcn_raw_ptr_buffer_load_lds(
-            rv, (__attribute__((address_space(3))) void *)(vst + q * 512), 16, rowoff + base_v, 0, 0, 0);
+#pragma unroll
+    for (int k = 0; k < W::PER; k++) {
+        const uint32_t q = wave + k * W::WAVES;        // instruction: tokens q*RPI .. +RPI-1
+        if (W::NI % W::WAVES == 0 || q < W::NI) {      // waves past the last instruction load nothing
+            const uint32_t tl = q * W::RPI + lane / W::CH; // token within the chunk
+            const uint32_t pos = lane % W::CH;
+            const uint32_t rowoff = ((t + tl) & (P - 1)) * row_bytes + hk * W::ROWB;
+            const uint32_t base_k = (pos ^ swz_k<D>(tl)) * 16, base_v = (pos ^ swz_v<D>(tl)) * 16;
+            const __amdgpu_buffer_rsrc_t rk = make_rsrc(kbase + tile[k].off, tile[k].bytes);
+            const __amdgpu_buffer_rsrc_t rv = make_rsrc(vbase + tile[k].off, tile[k].bytes);
+            __builtin_amdgcn_raw_ptr_buffer_load_lds(
+                rk, (__attribute__((address_space(3))) void *)(kst + q * 512), 16, rowoff + base_k, 0, 0, 0);
+            __builtin_amdgcn_raw_ptr_buffer_load_lds(
+                rv, (__attribute__((address_space(3))) void *)(vst + q * 512), 16, rowoff + base_v, 0, 0, 0);
+        }
     }
     __builtin_amdgcn_sched_barrier(0);
+}
+
+// The tiles of chunk t that this wave's loads read.
+template <int D>
+__device__ __forceinline__ void wide_tiles(const WideWindow &w, uint32_t t, uint32_t wave,
+                                           uint32_t shift, uint32_t tlim,
+                                           WideTile (&out)[WCfg<D>::PER]) {
+#pragma unroll
+    for (int k = 0; k < WCfg<D>::PER; k++) out[k] = wide_tile(w, wide_tile_key<D>(t, wave, k), shift, tlim);
 }
 
 template <int D>
@@ -1348,7 +1362,7 @@ __device__ __forceinline__ void load_q_full(const AttnParams &p, uint32_t row, u
     }
 }
 
-// One chunk (32 tokens at t) for this wave's 16 columns, from stages kst / vst.  `masked`: some
+// One chunk (32 tokens at t) for this wave's 16 * NTW columns, from stages kst / vst.  `masked`: some
 // key of the chunk is outside some column's live range (the range's unaligned start, the
 // causal diagonal, the range end); only then are the scores masked, in a branch of their
 // own.  Otherwise every key is live for every valid column (padding columns attend zero
@@ -1469,12 +1483,14 @@ __device__ __forceinline__ void wide_compute(const AttnParams &p, uint32_t t, WS
 // One step: wait for chunk i (this wave's loads; the next chunk's loads stay in flight),
 // the barrier, the loads of chunk i + 2 into the stage chunk i - 1 used, then chunk i.
 // Restrict stages: the compiler may keep the new loads in flight across the reads.
+// Three stages (measured: four are 1 % slower on a mixed prefill step).
 constexpr int kWideStages = 3;
 
 // Chunk t needs the causal / range mask unless [t, t + 32) lies in [free_lo, free_hi), the
 // keys live for every valid column of the unit.
 template <int D, int KVT>
-__device__ __forceinline__ void wide_step(const AttnParams &p, uint32_t tn, const WideTile &tpn,
+__device__ __forceinline__ void wide_step(const AttnParams &p, uint32_t tn,
+                                          const WideTile (&tpn)[WCfg<D>::PER],
                                           uint16_t *__restrict__ kn, uint16_t *__restrict__ vn,
                                           uint32_t tc, const uint16_t *__restrict__ kc,
                                           const uint16_t *__restrict__ vc, const uint8_t *kbase,
@@ -1488,62 +1504,77 @@ __device__ __forceinline__ void wide_step(const AttnParams &p, uint32_t tn, cons
 }
 
 // Keys [s_lo, s_hi) of one source into the running state (windows of at most 64 pages), through
-// three LDS stages (measured: a ring of four or five is slower).
+// a ring of kWideStages LDS stages (st_k / st_v).
 template <int D, int KVT>
 __device__ __forceinline__ void wide_range(const AttnParams &p, const uint8_t *kbase,
                                            const uint8_t *vbase, const uint32_t *table,
                                            uint32_t s_lo, uint32_t s_hi, bool use_pre, uint4 pre,
                                            uint32_t hk, uint32_t wave, bool active,
-                                           WState<D, KVT> &st, uint16_t *k0, uint16_t *k1,
-                                           uint16_t *k2, uint16_t *v0, uint16_t *v1, uint16_t *v2,
-                                           uint32_t free_lo, uint32_t free_hi) {
+                                           WState<D, KVT> &st, uint16_t *const (&st_k)[4],
+                                           uint16_t *const (&st_v)[4], uint32_t free_lo,
+                                           uint32_t free_hi) {
+    constexpr int NS = kWideStages;
     const uint32_t shift = p.page_shift;
     const uint32_t page_limit = (s_hi + (1u << shift) - 1) >> shift;
     const uint32_t row_bytes = p.hkv * WCfg<D>::ROWB;
-    const uint32_t dt = wide_tile_key<D>(0, wave); // the wave's tile within a chunk
+    using W = WCfg<D>;
     for (uint32_t wbeg = s_lo & ~31u; wbeg < s_hi;) {
         const uint32_t wend = min(s_hi, ((wbeg >> shift) + 64) << shift);
         WideWindow win;
         wide_window(p, win, table, wbeg >> shift, page_limit, wend, row_bytes);
-        WideTile tp0, tp1;
-        if (use_pre) { // the plan's first pages: no wait for the table load
-            const TilePages a = tile_pages_pre(pre, wbeg >> shift, wbeg + dt, shift, wend, p.pool_pages);
-            const TilePages b = tile_pages_pre(pre, wbeg >> shift, wbeg + 32 + dt, shift, wend, p.pool_pages);
-            const uint64_t pb = (uint64_t)(1u << shift) * row_bytes;
-            tp0 = WideTile{a.page[0] * pb, a.live[0] * row_bytes};
-            tp1 = WideTile{b.page[0] * pb, b.live[0] * row_bytes};
-            use_pre = false;
-        } else {
-            tp0 = wide_tile(win, wbeg + dt, shift, wend);
-            tp1 = wide_tile(win, wbeg + 32 + dt, shift, wend);
+        WideTile tp[NS - 1][W::PER], tpn[W::PER];
+        // the first two chunks from the plan's first pages when it preloaded them (no wait for
+        // the table load; they cover the kPrePages pages of two chunks at the smallest page size)
+#pragma unroll
+        for (int c = 0; c < NS - 1; c++) {
+            if (use_pre && c < 2) {
+                const uint64_t pb = (uint64_t)(1u << shift) * row_bytes;
+#pragma unroll
+                for (int k = 0; k < W::PER; k++) {
+                    const TilePages a = tile_pages_pre(pre, wbeg >> shift,
+                                                       wide_tile_key<D>(wbeg + 32 * c, wave, k), shift,
+                                                       wend, p.pool_pages);
+                    tp[c][k] = WideTile{a.page[0] * pb, a.live[0] * row_bytes};
+                }
+            } else {
+                wide_tiles<D>(win, wbeg + 32 * c, wave, shift, wend, tp[c]);
+            }
         }
+        use_pre = false;
         // every wave finished the previous window's chunks before their stages are refilled
         lds_barrier();
-        wide_load<D>(p, wbeg, tp0, kbase, vbase, hk, wave, k0, v0);
-        wide_load<D>(p, wbeg + 32, tp1, kbase, vbase, hk, wave, k1, v1);
-        for (uint32_t t = wbeg;; t += 96) {
+#pragma unroll
+        for (int c = 0; c < NS - 1; c++) wide_load<D>(p, wbeg + 32 * c, tp[c], kbase, vbase, hk, wave, st_k[c], st_v[c]);
+        for (uint32_t t = wbeg;; t += 32 * NS) {
             // loads past wend carry no traffic
-            wide_step<D, KVT>(p, t + 64, wide_tile(win, t + 64 + dt, shift, wend), k2, v2, t, k0,
-                              v0, kbase, vbase, hk, wave, active, st, free_lo, free_hi);
-            if (t + 32 >= wend) break;
-            wide_step<D, KVT>(p, t + 96, wide_tile(win, t + 96 + dt, shift, wend), k0, v0, t + 32,
-                              k1, v1, kbase, vbase, hk, wave, active, st, free_lo, free_hi);
-            if (t + 64 >= wend) break;
-            wide_step<D, KVT>(p, t + 128, wide_tile(win, t + 128 + dt, shift, wend), k1, v1, t + 64,
-                              k2, v2, kbase, vbase, hk, wave, active, st, free_lo, free_hi);
-            if (t + 96 >= wend) break;
+#pragma unroll
+            for (int c = 0; c < NS; c++) {
+                const uint32_t tn = t + 32 * (c + NS - 1);
+                wide_tiles<D>(win, tn, wave, shift, wend, tpn);
+                wide_step<D, KVT>(p, tn, tpn, st_k[(c + NS - 1) % NS], st_v[(c + NS - 1) % NS],
+                                  t + 32 * c, st_k[c], st_v[c], kbase, vbase, hk, wave, active, st,
+                                  free_lo, free_hi);
+                if (t + 32 * (c + 1) >= wend) goto window_done;
+            }
         }
+    window_done:
         wait_vmcnt<0>(); // the trailing (empty) loads target stages about to be reused
         wbeg = wend;
     }
 }
 
 template <int D, int KVT>
-__global__ __launch_bounds__(512, 4) void wide_kernel(AttnParams p) {
+__global__ __launch_bounds__(WCfg<D>::THREADS, 2) void wide_kernel(AttnParams p) {
     using W = WCfg<D>;
     constexpr uint32_t COLS = W::COLS;
-    __shared__ __attribute__((aligned(16))) uint16_t k0[W::STAGE], k1[W::STAGE], k2[W::STAGE];
-    __shared__ __attribute__((aligned(16))) uint16_t v0[W::STAGE], v1[W::STAGE], v2[W::STAGE];
+    // one object per stage, so that the compiler sees a stage's reads and the loads in flight
+    // into the other stages as independent (with one array and variable offsets into it, it
+    // waits for every load before each read)
+    static_assert(kWideStages == 3 || kWideStages == 4, "three or four stages");
+    constexpr int S4 = kWideStages == 4 ? W::STAGE : 1;
+    __shared__ __attribute__((aligned(16))) uint16_t k0[W::STAGE], k1[W::STAGE], k2[W::STAGE], k3[S4];
+    __shared__ __attribute__((aligned(16))) uint16_t v0[W::STAGE], v1[W::STAGE], v2[W::STAGE], v3[S4];
+    uint16_t *const st_k[4] = {k0, k1, k2, k3}, *const st_v[4] = {v0, v1, v2, v3};
     const uint32_t wg = blockIdx.x;
     const WorkDesc wd = p.work[wg];
     const uint32_t tid = threadIdx.x, lane = tid & 63;
@@ -1607,13 +1638,13 @@ __global__ __launch_bounds__(512, 4) void wide_kernel(AttnParams p) {
             const uint32_t r_lo = key_of(a), r_hi = min(key_of(e), kend);
             set_limits(r_lo, r_hi, 0);
             wide_range<D, KVT>(p, kpool, vpool, table, r_lo, r_hi, use_pre, wd.pre, hk, wave, active,
-                               st, k0, k1, k2, v0, v1, v2, r_lo, free_hi);
+                               st, st_k, st_v, r_lo, free_hi);
         } else {
             if (a < cb) {
                 const uint32_t r_lo = 32 * a, r_hi = min(32 * min(e, cb), kcache);
                 set_limits(r_lo, r_hi, 0);
                 wide_range<D, KVT>(p, kpool, vpool, table, r_lo, r_hi, use_pre, wd.pre, hk, wave,
-                                   active, st, k0, k1, k2, v0, v1, v2, r_lo, free_hi);
+                                   active, st, st_k, st_v, r_lo, free_hi);
             }
             if (e > cb) {
                 const uint32_t r0 = ud.rowbeg - (pos0 - kcache);
@@ -1621,7 +1652,7 @@ __global__ __launch_bounds__(512, 4) void wide_kernel(AttnParams p) {
                 set_limits(r_lo, r_hi, kcache);
                 wide_range<D, KVT>(p, (const uint8_t *)p.newk + (size_t)r0 * row_bytes,
                                    (const uint8_t *)p.newv + (size_t)r0 * row_bytes, nullptr, r_lo,
-                                   r_hi, false, wd.pre, hk, wave, active, st, k0, k1, k2, v0, v1, v2,
+                                   r_hi, false, wd.pre, hk, wave, active, st, st_k, st_v,
                                    r_lo, free_hi);
             }
         }
@@ -1687,7 +1718,7 @@ __global__ __launch_bounds__(512, 4) void wide_kernel(AttnParams p) {
 // the record groups are summed through LDS at the end.
 constexpr uint32_t kCombineThreads = 256;
 constexpr uint32_t kCombinePasses = 8;
-constexpr uint32_t kWideNTDev = 8; // column tiles of a prefill unit (one per wave)
+constexpr uint32_t kWideNTDev = 8; // 16-column tiles of a prefill unit
 
 __device__ __forceinline__ float wave_max(float v) {
 #pragma unroll
