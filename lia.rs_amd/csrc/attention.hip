@@ -160,22 +160,29 @@ constexpr uint32_t kPlanThreads = 1024;
 // keys.  Measured best: 8 for the prefill kernel (config 3 step 303 -> 246 us against no charge),
 // 4 for the decode kernel (config 2 8,320 -> 8,540 tokens/s; configs 4 and 5 lose beyond 4).
 constexpr uint32_t kUnitCostWide = 8, kUnitCostDecode = 4;
+// Weight lag (of 256) of the workgroups that share a CU with an older one.  Measured per
+// workgroup on the prefill kernel (two per CU): with equal shares the CU's first workgroup
+// finished in 183 us and the second in 216 us, the older waves being issued first.  Lag 56
+// (22 %) gave the best step (lags 24-96 measured); the decode kernels lose with any lag
+// (HBM-bound: the order of issue does not change their rate).
+constexpr uint32_t kLagWide = 56, kLagDecode = 0;
 
 // The plan for up to kPlanSeqs sequences, one thread each (kPlanThreads): per-sequence extents
 // in LDS (a shuffle scan with one barrier) and every unit in closed form (unit (h, cb) of
 // sequence b starts at block b0 + h*nbh + cb*cblocks + new_blocks_before(cb)), so units, merge
 // descriptors and the work list are each written in parallel with no serial per-sequence loop
-// and no reads of the units just written.  Workgroups get equal shares of cost: the blocks plus
-// unit_cost per unit (its start).
+// and no reads of the units just written.  Workgroups get shares of cost - the blocks plus
+// unit_cost per unit (its start) - equal, or weighted by dispatch round (round_wg, lag).
 __device__ void plan_lds(uint32_t n_seqs, const uint32_t *cu, const uint32_t *positions,
                          const uint32_t *sequences, const uint32_t *pages, uint32_t stride,
                          uint32_t page_shift, uint32_t rpc, uint32_t hkv, uint32_t max_units,
-                         uint32_t n_wg, uint32_t unit_cost, UnitDesc *units, WorkDesc *work,
-                         MergeDesc *merge, uint32_t *header) {
+                         uint32_t n_wg, uint32_t unit_cost, uint32_t round_wg, uint32_t lag,
+                         UnitDesc *units, WorkDesc *work, MergeDesc *merge, uint32_t *header) {
     __shared__ uint32_t s_r0[kPlanSeqs], s_nr[kPlanSeqs], s_p0[kPlanSeqs], s_trow[kPlanSeqs];
     __shared__ uint32_t s_u0[kPlanSeqs + 1], s_b0[kPlanSeqs + 1], s_c0[kPlanSeqs + 1];
     __shared__ uint32_t w_a[kPlanThreads / 64], w_b[kPlanThreads / 64];
     __shared__ uint32_t carry_units, carry_blocks;
+    __shared__ uint64_t s_rlo[kPlanThreads + 1];
     // Threads exchange only LDS data (nothing written to global memory is read back), so the
     // barriers need not wait for the descriptor stores in flight.
     constexpr uint32_t T = kPlanThreads;
@@ -251,13 +258,53 @@ __device__ void plan_lds(uint32_t n_seqs, const uint32_t *cu, const uint32_t *po
     // cost of starting a unit), so a range that crosses into a unit is shorter by that much and a
     // boundary falling in a unit's lead-in moves to the unit's start.
     const uint64_t TC = (uint64_t)B + (uint64_t)unit_cost * U;
+    const bool xcd_major = N == n_wg && N % 8 == 0;
+    const uint32_t per = N / 8;
+    // Ranges in cost order r = 0 .. N-1 run on workgroup w(r) (XCD-major when the grid allows).
+    // A workgroup dispatched after the first round_wg shares its CU with an older one, which the
+    // hardware issues first, so its range is weighted (256 - lag) / 256 against 1 for the first
+    // round (lag 0: equal shares).  F(r) = sum of the weights of ranges before r, times 256.
+    const bool skew = lag && round_wg && round_wg < N;
+    auto weight_before = [&](uint32_t r) -> uint64_t {
+        uint32_t late = 0; // ranges before r on workgroups w >= round_wg
+        if (skew) {
+            if (xcd_major) {
+                const uint32_t X = r / per, I = r % per;
+                for (uint32_t x = 0; x <= X && x < 8; x++) {
+                    const uint32_t cx = round_wg > x ? min(per, (round_wg - x + 7) / 8) : 0u;
+                    late += x < X ? per - cx : (I > cx ? I - cx : 0u);
+                }
+            } else {
+                late = r > round_wg ? r - round_wg : 0u;
+            }
+        }
+        return 256ull * r - (uint64_t)lag * late;
+    };
+    // Equal weights: range r starts at cost r*TC/N, and cost c lies in range ((c+1)*N-1)/TC.
+    // Weighted: the start cost of every range is tabulated once (one division per range) and
+    // searched.
+    if (skew) {
+        const uint64_t FN = weight_before(N);
+        for (uint32_t r = t; r <= N; r += T) s_rlo[r] = weight_before(r) * TC / FN;
+        lds_barrier();
+    }
+    auto range_lo = [&](uint32_t r) { return skew ? s_rlo[r] : (uint64_t)r * TC / N; };
+    // the last range starting at or before cost c
+    auto range_of = [&](uint64_t c) {
+        if (!skew) return (uint32_t)(((c + 1) * N - 1) / TC);
+        uint32_t a = 0, e = N;
+        while (a + 1 < e) {
+            const uint32_t mid = (a + e) >> 1;
+            if (s_rlo[mid] <= c) a = mid; else e = mid;
+        }
+        return a;
+    };
     for (uint32_t u = t; u < max_units; u += T) {
         MergeDesc m = {0, 0, 0, 0};
         if (u < U) {
             const UnitDesc ud = unit_by_index(u);
             const uint64_t cu0 = (uint64_t)ud.block_start + unit_cost * (u + 1); // cost of its first block
-            const uint32_t wf = (uint32_t)(((cu0 + 1) * N - 1) / TC);
-            const uint32_t wl = (uint32_t)(((cu0 + ud.nblocks) * N - 1) / TC);
+            const uint32_t wf = range_of(cu0), wl = range_of(cu0 + ud.nblocks - 1);
             if (wf != wl) m = MergeDesc{wf + u, wl - wf + 1, ud.rowbeg, ud.nrows_hk};
         }
         merge[u] = m;
@@ -283,9 +330,6 @@ __device__ void plan_lds(uint32_t n_seqs, const uint32_t *cu, const uint32_t *po
         ub = b; uh = h; ucb = cb;
         return s_b0[b] + h * nbh + ustart + (off < unit_cost ? 0u : off - unit_cost);
     };
-    auto range_lo = [&](uint32_t w) { return (uint64_t)w * TC / N; };
-    const bool xcd_major = N == n_wg && N % 8 == 0;
-    const uint32_t per = N / 8;
     // One work descriptor per thread and pass (unconditional page-table loads: an entry not
     // needed reads cu[0] and is replaced by 0).
     for (uint32_t w0 = t; w0 < N; w0 += T) {
@@ -327,10 +371,10 @@ __device__ void plan_lds(uint32_t n_seqs, const uint32_t *cu, const uint32_t *po
 __global__ __launch_bounds__(kPlanThreads) void plan_lds_kernel(
     uint32_t n_seqs, const uint32_t *cu, const uint32_t *positions, const uint32_t *sequences,
     const uint32_t *pages, uint32_t stride, uint32_t page_shift, uint32_t rpc, uint32_t hkv,
-    uint32_t max_units, uint32_t n_wg, uint32_t unit_cost, UnitDesc *units, WorkDesc *work,
-    MergeDesc *merge, uint32_t *header) {
+    uint32_t max_units, uint32_t n_wg, uint32_t unit_cost, uint32_t round_wg, uint32_t lag,
+    UnitDesc *units, WorkDesc *work, MergeDesc *merge, uint32_t *header) {
     plan_lds(n_seqs, cu, positions, sequences, pages, stride, page_shift, rpc, hkv, max_units, n_wg,
-             unit_cost, units, work, merge, header);
+             unit_cost, round_wg, lag, units, work, merge, header);
 }
 
 // The plan for more sequences than plan_lds_kernel holds: units written by a serial walk of
@@ -1389,25 +1433,11 @@ __device__ __forceinline__ void wide_compute(const AttnParams &p, uint32_t t, WS
     // XOR form keeps one address register per operand and the stage base an immediate.
     const uint32_t sk = swz_k<D>(li);
     const uint32_t kb = li * 2 * D + 64 * (sk >> 2) + 16 * (g ^ (sk & 3));
-    // operand reads one step ahead of their MFMAs (two buffers), so a read's LDS latency
-    // overlaps the previous MFMA instead of stalling the wave
+    // every operand of the chunk is read from LDS at its start (K first, then V), so the
+    // reads' latency passes under the S^T MFMAs and the softmax instead of stalling the wave
     auto kread = [&](int i) { // i = 2 ks + j: the two token tiles' chains alternate
         return *(const u32x4 *)((const uint8_t *)kst + (kb ^ (64 * (i / 2))) + (i % 2) * 32 * D);
     };
-    f32x4 acc[2][NTW];
-#pragma unroll
-    for (int j = 0; j < 2; j++)
-#pragma unroll
-        for (int nt = 0; nt < NTW; nt++) acc[j][nt] = f32x4{0.0f, 0.0f, 0.0f, 0.0f};
-    u32x4 ka[2];
-    ka[0] = kread(0);
-#pragma unroll
-    for (int i = 0; i < 2 * W::KT; i++) {
-        if (i + 1 < 2 * W::KT) ka[(i + 1) & 1] = kread(i + 1);
-        const int j = i % 2, ks = i / 2;
-#pragma unroll
-        for (int nt = 0; nt < NTW; nt++) acc[j][nt] = mfma16x16x32<MB>(ka[i & 1], st.qr[nt][ks], acc[j][nt]);
-    }
     // O^T += V^T P^T: V^T rows 16n .. 16n+15, k slots = tokens {4g..4g+3, 16+4g..16+4g+3}.
     // The transpose read of row r0 = 4g + li/4, chunk 2n + b at position (2n + b) ^ swz_v(r0),
     // is at vb ^ 32 n (row r0 + 16 swizzles like r0).
@@ -1421,10 +1451,22 @@ __device__ __forceinline__ void wide_compute(const AttnParams &p, uint32_t t, WS
         const u32x2 b0 = __builtin_bit_cast(u32x2, a0), b1 = __builtin_bit_cast(u32x2, a1);
         return u32x4{b0.x, b0.y, b1.x, b1.y};
     };
-    // the first V operand is read before the softmax: its LDS latency passes under it
-    u32x4 vt[3];
-    vt[0] = vread(0);
-    vt[1] = vread(1);
+    u32x4 ka[2 * W::KT], vt[W::DT];
+#pragma unroll
+    for (int i = 0; i < 2 * W::KT; i++) ka[i] = kread(i);
+#pragma unroll
+    for (int n = 0; n < W::DT; n++) vt[n] = vread(n);
+    f32x4 acc[2][NTW];
+#pragma unroll
+    for (int j = 0; j < 2; j++)
+#pragma unroll
+        for (int nt = 0; nt < NTW; nt++) acc[j][nt] = f32x4{0.0f, 0.0f, 0.0f, 0.0f};
+#pragma unroll
+    for (int i = 0; i < 2 * W::KT; i++) {
+        const int j = i % 2, ks = i / 2;
+#pragma unroll
+        for (int nt = 0; nt < NTW; nt++) acc[j][nt] = mfma16x16x32<MB>(ka[i], st.qr[nt][ks], acc[j][nt]);
+    }
     if (masked) {
 #pragma unroll
         for (int j = 0; j < 2; j++)
@@ -1468,11 +1510,9 @@ __device__ __forceinline__ void wide_compute(const AttnParams &p, uint32_t t, WS
                        pack2<MB>(pr[1][0], pr[1][1]), pack2<MB>(pr[1][2], pr[1][3])};
     }
 #pragma unroll
-    for (int n = 0; n < W::DT; n++) {
-        if (n + 2 < W::DT) vt[(n + 2) % 3] = vread(n + 2);
+    for (int n = 0; n < W::DT; n++)
 #pragma unroll
-        for (int nt = 0; nt < NTW; nt++) st.o[nt][n] = mfma16x16x32<MB>(vt[n % 3], pb[nt], st.o[nt][n]);
-    }
+        for (int nt = 0; nt < NTW; nt++) st.o[nt][n] = mfma16x16x32<MB>(vt[n], pb[nt], st.o[nt][n]);
     // the mass: every row of the ones tile is the column's sum of this chunk's weights
     constexpr uint32_t one2 = MB ? 0x3F803F80u : 0x3C003C00u;
     const u32x4 ones = u32x4{one2, one2, one2, one2};
@@ -2229,12 +2269,13 @@ static int run_stages(int stages, const lia_attention_config *c, uint32_t n_seqs
         WorkDesc *work = (WorkDesc *)(ws + L.work);
         MergeDesc *merge = (MergeDesc *)(ws + L.merge);
         uint32_t *header = (uint32_t *)(ws + L.header);
-        if (n_seqs <= kPlanSeqs)
+        if (n_seqs <= kPlanSeqs && n_wg <= kPlanThreads)
             e = launch<plan_lds_kernel>(dim3(1), dim3(kPlanThreads), 0, s, n_seqs, cu_seqlens,
                                         positions, sequences, pages, c->stride, p.page_shift, rpc,
                                         c->num_kv_heads, L.max_units, n_wg,
-                                        NT == kWideNT ? kUnitCostWide : kUnitCostDecode, units,
-                                        work, merge, header);
+                                        NT == kWideNT ? kUnitCostWide : kUnitCostDecode,
+                                        lia_device_cus(), NT == kWideNT ? kLagWide : kLagDecode,
+                                        units, work, merge, header);
         else
             e = launch<plan_kernel>(dim3(1), dim3(256), 0, s, n_seqs, cu_seqlens, positions,
                                     sequences, pages, c->stride, p.page_shift, rpc, c->num_kv_heads,
