@@ -118,6 +118,7 @@ class Case:
                             dev["pages"], dev["q"], dev["kc"], dev["vc"], out, ws,
                             dev["k_scales"], dev["v_scales"])
         torch.cuda.synchronize()
+        self.last_ws = ws  # the plan's header (units, blocks, ranges, overflow) is its first 16 bytes
         return out.float().cpu().numpy()
 
 

@@ -280,6 +280,21 @@ def test_single_sequence_small_merge(lia, wl, d, q):
     _check(G.Case(b, seed=32), lia, f"single sequence d={d} rows={q}")
 
 
+def test_prefill_weighted_ranges_in_launch_order(lia, wl):
+    """A 64-row chunk after 1,536 cached keys: 8 prefill units of about 50 blocks each, about 400
+    blocks in all.  That is fewer blocks than the launch's prefill workgroups (two per CU), so
+    ranges run on workgroups in launch order rather than XCD-major, and more ranges than CUs, so
+    the ranges of workgroups past the first dispatch round get the plan's smaller weight."""
+    b = wl.custom([1536 + 64], [64], seed=33)
+    case = G.Case(b, seed=33)
+    _check(case, lia, "weighted ranges in launch order")
+    units, blocks, ranges, overflow = case.last_ws[:16].view(torch.int32).cpu().tolist()
+    cus = lia.lib().lia_device_cus()
+    print(f"[case] units={units} blocks={blocks} ranges={ranges} cus={cus}", flush=True)
+    assert overflow == 0 and units == 8 and ranges == blocks
+    assert cus < ranges < 2 * cus
+
+
 def test_repeat_calls_are_identical(lia, wl):
     b = wl.custom([5000, 17, 900], [1, 1, 3], seed=8)
     case = G.Case(b, seed=8)
