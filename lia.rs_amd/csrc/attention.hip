@@ -1317,31 +1317,57 @@ __device__ __forceinline__ uint32_t wide_tile_key(uint32_t t, uint32_t wave, int
     return t + 16 * (((wave + k * WCfg<D>::WAVES) * WCfg<D>::RPI) / 16);
 }
 
+// Per-lane byte offsets of this wave's direct-to-LDS loads within the 16-token tile each load
+// reads (constant over a range: the tile's position in its page goes into the scalar base).
+template <int D>
+struct WideLanes {
+    uint32_t k[WCfg<D>::PER], v[WCfg<D>::PER];
+};
+
+template <int D>
+__device__ __forceinline__ WideLanes<D> wide_lanes(uint32_t wave, uint32_t hk, uint32_t row_bytes) {
+    using W = WCfg<D>;
+    const uint32_t lane = lane_id();
+    WideLanes<D> r;
+#pragma unroll
+    for (int k = 0; k < W::PER; k++) {
+        const uint32_t q = wave + k * W::WAVES;            // instruction: tokens q*RPI .. +RPI-1
+        const uint32_t tl = q * W::RPI + lane / W::CH;      // token within the chunk
+        const uint32_t tt = (q * W::RPI) % 16 + lane / W::CH; // token within its 16-token tile
+        const uint32_t pos = lane % W::CH;
+        const uint32_t rowoff = tt * row_bytes + hk * W::ROWB;
+        r.k[k] = rowoff + (pos ^ swz_k<D>(tl)) * 16;
+        r.v[k] = rowoff + (pos ^ swz_v<D>(tl)) * 16;
+    }
+    return r;
+}
+
 // This wave's quarter of chunk t of K and V (from the pool or the step's rows) into LDS, from
-// the wave's tile (wide_tile_key).
+// the wave's tile (wide_tile_key).  The tile's first token lies (ts mod P) tokens into its
+// page: the descriptor starts there and keeps the page's remaining live bytes, so the lane
+// offsets stay constant and the per-chunk address arithmetic is scalar.
 template <int D>
 __device__ __forceinline__ void wide_load(const AttnParams &p, uint32_t t,
                                           const WideTile (&tile)[WCfg<D>::PER], const uint8_t *kbase,
-                                          const uint8_t *vbase, uint32_t hk, uint32_t wave,
+                                          const uint8_t *vbase, const WideLanes<D> &ln, uint32_t wave,
                                           uint16_t *kst, uint16_t *vst) {
     using W = WCfg<D>;
-    const uint32_t lane = lane_id(), P = 1u << p.page_shift;
+    const uint32_t P = 1u << p.page_shift;
     const uint32_t row_bytes = p.hkv * W::ROWB;
     __builtin_amdgcn_s_waitcnt(0xC07F); // lgkmcnt(0): this wave's reads of the stage are done
 #pragma unroll
     for (int k = 0; k < W::PER; k++) {
         const uint32_t q = wave + k * W::WAVES;        // instruction: tokens q*RPI .. +RPI-1
         if (W::NI % W::WAVES == 0 || q < W::NI) {      // waves past the last instruction load nothing
-            const uint32_t tl = q * W::RPI + lane / W::CH; // token within the chunk
-            const uint32_t pos = lane % W::CH;
-            const uint32_t rowoff = ((t + tl) & (P - 1)) * row_bytes + hk * W::ROWB;
-            const uint32_t base_k = (pos ^ swz_k<D>(tl)) * 16, base_v = (pos ^ swz_v<D>(tl)) * 16;
-            const __amdgpu_buffer_rsrc_t rk = make_rsrc(kbase + tile[k].off, tile[k].bytes);
-            const __amdgpu_buffer_rsrc_t rv = make_rsrc(vbase + tile[k].off, tile[k].bytes);
+            const uint32_t sh = (wide_tile_key<D>(t, wave, k) & (P - 1)) * row_bytes;
+            // a tile with live bytes starts before the range end, so they exceed sh
+            const uint32_t nb = tile[k].bytes ? tile[k].bytes - sh : 0u;
+            const __amdgpu_buffer_rsrc_t rk = make_rsrc(kbase + tile[k].off + sh, nb);
+            const __amdgpu_buffer_rsrc_t rv = make_rsrc(vbase + tile[k].off + sh, nb);
             __builtin_amdgcn_raw_ptr_buffer_load_lds(
-                rk, (__attribute__((address_space(3))) void *)(kst + q * 512), 16, rowoff + base_k, 0, 0, 0);
+                rk, (__attribute__((address_space(3))) void *)(kst + q * 512), 16, (int)ln.k[k], 0, 0, 0);
             __builtin_amdgcn_raw_ptr_buffer_load_lds(
-                rv, (__attribute__((address_space(3))) void *)(vst + q * 512), 16, rowoff + base_v, 0, 0, 0);
+                rv, (__attribute__((address_space(3))) void *)(vst + q * 512), 16, (int)ln.v[k], 0, 0, 0);
         }
     }
     __builtin_amdgcn_sched_barrier(0);
@@ -1534,12 +1560,12 @@ __device__ __forceinline__ void wide_step(const AttnParams &p, uint32_t tn,
                                           uint16_t *__restrict__ kn, uint16_t *__restrict__ vn,
                                           uint32_t tc, const uint16_t *__restrict__ kc,
                                           const uint16_t *__restrict__ vc, const uint8_t *kbase,
-                                          const uint8_t *vbase, uint32_t hk, uint32_t wave,
+                                          const uint8_t *vbase, const WideLanes<D> &ln, uint32_t wave,
                                           bool active, WState<D, KVT> &st, uint32_t free_lo,
                                           uint32_t free_hi) {
     wait_vmcnt<(kWideStages - 2) * kWideLoads<D>>(); // the later chunks' loads stay in flight
     lds_barrier();
-    wide_load<D>(p, tn, tpn, kbase, vbase, hk, wave, kn, vn);
+    wide_load<D>(p, tn, tpn, kbase, vbase, ln, wave, kn, vn);
     if (active) wide_compute<D, KVT>(p, tc, st, kc, vc, !(tc >= free_lo && tc + 32 <= free_hi));
 }
 
@@ -1558,6 +1584,10 @@ __device__ __forceinline__ void wide_range(const AttnParams &p, const uint8_t *k
     const uint32_t page_limit = (s_hi + (1u << shift) - 1) >> shift;
     const uint32_t row_bytes = p.hkv * WCfg<D>::ROWB;
     using W = WCfg<D>;
+    const WideLanes<D> ln = wide_lanes<D>(wave, hk, row_bytes);
+    // wave-uniform bases, so the descriptors are built by scalar instructions
+    kbase = uniform_ptr(kbase);
+    vbase = uniform_ptr(vbase);
     for (uint32_t wbeg = s_lo & ~31u; wbeg < s_hi;) {
         const uint32_t wend = min(s_hi, ((wbeg >> shift) + 64) << shift);
         WideWindow win;
@@ -1571,10 +1601,10 @@ __device__ __forceinline__ void wide_range(const AttnParams &p, const uint8_t *k
                 const uint64_t pb = (uint64_t)(1u << shift) * row_bytes;
 #pragma unroll
                 for (int k = 0; k < W::PER; k++) {
-                    const TilePages a = tile_pages_pre(pre, wbeg >> shift,
-                                                       wide_tile_key<D>(wbeg + 32 * c, wave, k), shift,
-                                                       wend, p.pool_pages);
-                    tp[c][k] = WideTile{a.page[0] * pb, a.live[0] * row_bytes};
+                    const uint32_t key = wide_tile_key<D>(wbeg + 32 * c, wave, k);
+                    const TilePages a = tile_pages_pre(pre, wbeg >> shift, key, shift, wend, p.pool_pages);
+                    // no live bytes for a tile at or past the range end (wide_load relies on it)
+                    tp[c][k] = WideTile{a.page[0] * pb, key < wend ? a.live[0] * row_bytes : 0u};
                 }
             } else {
                 wide_tiles<D>(win, wbeg + 32 * c, wave, shift, wend, tp[c]);
@@ -1584,7 +1614,7 @@ __device__ __forceinline__ void wide_range(const AttnParams &p, const uint8_t *k
         // every wave finished the previous window's chunks before their stages are refilled
         lds_barrier();
 #pragma unroll
-        for (int c = 0; c < NS - 1; c++) wide_load<D>(p, wbeg + 32 * c, tp[c], kbase, vbase, hk, wave, st_k[c], st_v[c]);
+        for (int c = 0; c < NS - 1; c++) wide_load<D>(p, wbeg + 32 * c, tp[c], kbase, vbase, ln, wave, st_k[c], st_v[c]);
         for (uint32_t t = wbeg;; t += 32 * NS) {
             // loads past wend carry no traffic
 #pragma unroll
@@ -1592,7 +1622,7 @@ __device__ __forceinline__ void wide_range(const AttnParams &p, const uint8_t *k
                 const uint32_t tn = t + 32 * (c + NS - 1);
                 wide_tiles<D>(win, tn, wave, shift, wend, tpn);
                 wide_step<D, KVT>(p, tn, tpn, st_k[(c + NS - 1) % NS], st_v[(c + NS - 1) % NS],
-                                  t + 32 * c, st_k[c], st_v[c], kbase, vbase, hk, wave, active, st,
+                                  t + 32 * c, st_k[c], st_v[c], kbase, vbase, ln, wave, active, st,
                                   free_lo, free_hi);
                 if (t + 32 * (c + 1) >= wend) goto window_done;
             }

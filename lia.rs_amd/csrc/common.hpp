@@ -125,6 +125,15 @@ __device__ __forceinline__ T uniform(T v) {
     return __builtin_bit_cast(T, __builtin_amdgcn_readfirstlane(__builtin_bit_cast(int, v)));
 }
 
+// The same for a pointer (two readfirstlanes).
+template <typename T>
+__device__ __forceinline__ T *uniform_ptr(T *v) {
+    const uint64_t a = (uint64_t)(uintptr_t)v;
+    const uint32_t lo = (uint32_t)__builtin_amdgcn_readfirstlane((int)(uint32_t)a);
+    const uint32_t hi = (uint32_t)__builtin_amdgcn_readfirstlane((int)(uint32_t)(a >> 32));
+    return (T *)(uintptr_t)(((uint64_t)hi << 32) | lo);
+}
+
 // MFMA 16x16x32 with f32 accumulation; operands are raw 16-byte register quads.
 // A[m][k]: lane l holds row m = l%16, k = 8*(l/16) .. +7.  B[k][n]: lane l holds column
 // n = l%16, the same k.  D[m][n]: lane l holds rows 4*(l/16) .. +3 of column l%16.
