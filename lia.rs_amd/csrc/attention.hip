@@ -616,7 +616,7 @@ __device__ __forceinline__ TilePages tile_pages(const PageWindow &w, uint32_t t,
         const uint32_t rel = (t0 >> shift) - w.base;
         tp.page[j] = (uint32_t)__builtin_amdgcn_readlane((int)w.page, (int)(rel & 63));
         const uint32_t pstart = t0 & ~(P - 1);
-        tp.live[j] = (rel < 64 && tlim > pstart && tp.page[j] < w.valid) ? min(tlim - pstart, P) : 0u;
+        tp.live[j] = (rel < 64 && tlim > t0 && tp.page[j] < w.valid) ? min(tlim - pstart, P) : 0u;
         if constexpr (FP8) {
             tp.ks[j] = __builtin_bit_cast(float, __builtin_amdgcn_readlane(__builtin_bit_cast(int, w.ks), (int)(rel & 63)));
             tp.vs[j] = __builtin_bit_cast(float, __builtin_amdgcn_readlane(__builtin_bit_cast(int, w.vs), (int)(rel & 63)));
@@ -639,7 +639,7 @@ __device__ __forceinline__ TilePages tile_pages_pre(uint4 pre, uint32_t lp0, uin
         const uint32_t rel = (t0 >> shift) - lp0;
         const uint32_t pstart = t0 & ~(P - 1);
         tp.page[j] = rel == 0 ? pre.x : rel == 1 ? pre.y : rel == 2 ? pre.z : pre.w;
-        tp.live[j] = (rel < kPrePages && tlim > pstart && tp.page[j] < valid) ? min(tlim - pstart, P) : 0u;
+        tp.live[j] = (rel < kPrePages && tlim > t0 && tp.page[j] < valid) ? min(tlim - pstart, P) : 0u;
         tp.ks[j] = tp.vs[j] = 1.0f;
     }
     return tp;
@@ -656,72 +656,108 @@ __device__ __forceinline__ void wait_vmcnt() {
 template <int D, int KVT>
 constexpr int kLoadsPerChunk = 2 * Cfg<D, KVT>::KL + Cfg<D, KVT>::NV; // K loads + V loads
 
+// Per-lane byte offsets of the chunk loads within their 16-token tile (constant over a key
+// range; the tile's position in its page goes into the scalar buffer base).
+template <int D, int KVT>
+struct DecLanes {
+    uint32_t k[Cfg<D, KVT>::KL];                     // K: tile row li, this lane's 16 bytes
+    uint32_t v[Cfg<D, KVT>::FP8 ? 1 : Cfg<D, KVT>::NV]; // V: FP8 whole-row load, or each staged load
+};
+
+template <int D, int KVT>
+__device__ __forceinline__ DecLanes<D, KVT> dec_lanes(uint32_t hk, uint32_t wave, uint32_t row_bytes) {
+    using C = Cfg<D, KVT>;
+    const uint32_t lane = lane_id(), g = lane >> 4, li = lane & 15;
+    const uint32_t slice_off = (hk * D + C::SW * wave) * C::EB;
+    DecLanes<D, KVT> r;
+    // K: lane (g, li) of a tile reads token li, bytes 16g .. 16g+15 of the wave's slice (the
+    // four groups of a token cover its 64-byte slice contiguously): dims 32w + 8g .. +7 of a
+    // 16-bit pool, dims 64w + 16g .. +15 of an FP8 pool (k slots 8g..8g+7 of k-step s hold
+    // dims 64w + 16g + 8s .. +7, and Q is loaded to match).  A 16-bit slice of 64 dims takes
+    // two loads per tile, bytes 64q + 16g (dims 32q + 8g .. +7 = k-step q), so each load
+    // instruction still reads 64 contiguous bytes of a token.
+#pragma unroll
+    for (int q = 0; q < C::KL; q++) r.k[q] = li * row_bytes + slice_off + 64 * q + 16 * g;
+    if constexpr (C::FP8) {
+        // V as whole head rows: wave w reads tokens TPI*w .. +TPI-1 of each tile (lane l:
+        // token TPI*w + l/CPT, bytes 16(l%CPT) .. +15 of the head's row)
+        r.v[0] = (C::TPI * wave + lane / C::CPT) * row_bytes + hk * D * C::EB + 16 * (lane % C::CPT);
+    } else {
+        // staged V: load s fills rows VRPI*s .. +VRPI-1, lane l writes slot l%CPR of row
+        // VRPI*s + l/CPR with the swizzled chunk
+#pragma unroll
+        for (int s = 0; s < C::NV; s++) {
+            const uint32_t row = C::VRPI * s + lane / C::CPR;
+            const uint32_t chunk = (lane % C::CPR) ^ vswz(row);
+            r.v[s] = (row & 15) * row_bytes + slice_off + 16 * chunk;
+        }
+    }
+    return r;
+}
+
+// Byte span of 16-token tile j of chunk t within a plane: it starts at the tile's first
+// token and holds the live tokens from there (a tile with live tokens starts before the
+// range end, tile_pages), so loads past them read zeros without touching memory.  Scalar
+// arithmetic only; the K and V descriptors of the tile share it.
+struct TileSpan {
+    uint64_t off;
+    uint32_t bytes;
+};
+
+__device__ __forceinline__ TileSpan tile_span(const TilePages &tp, int j, uint32_t t, uint32_t shift,
+                                              uint32_t row_bytes) {
+    const uint32_t P = 1u << shift;
+    const uint32_t pb = P * row_bytes; // bytes of a page (all KV heads)
+    const uint32_t pg = tp.page[j];
+    const uint32_t sh = ((t + 16 * j) & (P - 1)) * row_bytes;
+    const uint32_t live = tp.live[j] * row_bytes;
+    TileSpan r;
+    r.off = (((uint64_t)__umulhi(pg, pb) << 32) | (uint32_t)(pg * pb)) + sh;
+    r.bytes = live ? live - sh : 0u;
+    return r;
+}
+
 // Loads chunk t (32 tokens, t a multiple of 32) of this wave's d slice from the planes at
-// kbase / vbase (the pool, or the step's new rows).  Buffer loads are bounded to each
-// tile's live tokens: rows past them read as zeros without touching memory, so every load
-// is issued unconditionally and masked V rows are zero.
+// kbase / vbase (the pool, or the step's new rows).  Every load is issued unconditionally:
+// tiles past the live keys have empty descriptors, and masked V rows are zero.
 template <int D, int KVT>
 __device__ __forceinline__ void load_chunk(const AttnParams &p, Chunk<D, KVT> &c, uint32_t t,
                                            const TilePages &tp, const uint8_t *kbase,
-                                           const uint8_t *vbase, uint32_t hk, uint32_t wave,
+                                           const uint8_t *vbase, const DecLanes<D, KVT> &ln,
                                            uint16_t *stage) {
     using C = Cfg<D, KVT>;
-    const uint32_t lane = lane_id(), g = lane >> 4, li = lane & 15;
-    const uint32_t P = 1u << p.page_shift;
     const uint32_t row_bytes = p.hkv * D * C::EB; // bytes per slot (all KV heads)
-    const uint32_t slice_off = (hk * D + C::SW * wave) * C::EB;
-    __amdgpu_buffer_rsrc_t r[2];
+    TileSpan sp[2];
 #pragma unroll
     for (int j = 0; j < 2; j++) {
-        r[j] = make_rsrc(kbase + (size_t)tp.page[j] * P * row_bytes, tp.live[j] * row_bytes);
+        sp[j] = tile_span(tp, j, t, p.page_shift, row_bytes);
         if constexpr (C::FP8) {
             c.ks[j] = tp.ks[j];
             c.vs[j] = tp.vs[j];
         }
-    }
-    // K: lane (g, li) of tile j reads token 16j+li, bytes 16g .. 16g+15 of the wave's slice
-    // (the four groups of a token cover its 64-byte slice contiguously): dims 32w + 8g .. +7
-    // of a 16-bit pool, dims 64w + 16g .. +15 of an FP8 pool (k slots 8g..8g+7 of k-step s
-    // hold dims 64w + 16g + 8s .. +7, and Q is loaded to match).
-    // A 16-bit slice of 64 dims takes two loads per tile, bytes 64q + 16g (dims 32q + 8g ..
-    // +7 = k-step q), so each load instruction still reads 64 contiguous bytes of a token.
-#pragma unroll
-    for (int j = 0; j < 2; j++) {
+        const __amdgpu_buffer_rsrc_t r = make_rsrc(kbase + sp[j].off, sp[j].bytes);
 #pragma unroll
         for (int q = 0; q < C::KL; q++) {
-            const uint32_t off = (((t + 16 * j) & (P - 1)) + li) * row_bytes + slice_off + 64 * q + 16 * g;
-            u32x4 x = buffer_load16_p<C::AUX>(r[j], off);
+            u32x4 x = buffer_load16_p<C::AUX>(r, (uint32_t)ln.k[q]);
             c.k[j][4 * q] = x.x; c.k[j][4 * q + 1] = x.y; c.k[j][4 * q + 2] = x.z; c.k[j][4 * q + 3] = x.w;
         }
     }
     if constexpr (C::FP8) {
-        // V into registers as whole head rows: wave w reads tokens TPI*w .. +TPI-1 of each
-        // tile (lane l: token TPI*w + l/CPT, bytes 16(l%CPT) .. +15 of the head's row), so every
-        // load reads whole lines; each wave stages both halves of its rows for the wave that
-        // owns those dims.  Bounded like K.
+        // V into registers as whole head rows, so every load reads whole lines; each wave
+        // stages both halves of its rows for the wave that owns those dims
 #pragma unroll
-        for (int j = 0; j < 2; j++) {
-            const __amdgpu_buffer_rsrc_t vr =
-                make_rsrc(vbase + (size_t)tp.page[j] * P * row_bytes, tp.live[j] * row_bytes);
-            const uint32_t off = (((t + 16 * j) & (P - 1)) + C::TPI * wave + lane / C::CPT) * row_bytes +
-                                 hk * D * C::EB + 16 * (lane % C::CPT);
-            c.v[j] = buffer_load16_p<C::AUX>(vr, off);
-        }
+        for (int j = 0; j < 2; j++)
+            c.v[j] = buffer_load16_p<C::AUX>(make_rsrc(vbase + sp[j].off, sp[j].bytes), (uint32_t)ln.v[0]);
     } else {
-        // V slice goes straight to this wave's LDS stage: load s fills rows VRPI*s ..
-        // +VRPI-1, lane l writes slot l%CPR of row VRPI*s + l/CPR with the swizzled chunk.
+        // V slice straight to this wave's LDS stage
         __builtin_amdgcn_s_waitcnt(0xC07F); // lgkmcnt(0): earlier reads of this stage are done
 #pragma unroll
         for (int s = 0; s < C::NV; s++) {
-            const uint32_t j = (C::VRPI * s) / 16; // the load's 16-token tile
-            const __amdgpu_buffer_rsrc_t vr =
-                make_rsrc(vbase + (size_t)tp.page[j] * P * row_bytes, tp.live[j] * row_bytes);
-            const uint32_t row = C::VRPI * s + lane / C::CPR;
-            const uint32_t chunk = (lane % C::CPR) ^ vswz(row);
-            const uint32_t off = (((t + 16 * j) & (P - 1)) + (row & 15)) * row_bytes + slice_off + 16 * chunk;
+            const int j = (C::VRPI * s) / 16; // the load's 16-token tile
+            const __amdgpu_buffer_rsrc_t vr = make_rsrc(vbase + sp[j].off, sp[j].bytes);
             auto *dst = (__attribute__((address_space(3))) void *)(stage + s * 512);
             static_assert(C::AUX == 2, "the direct-to-LDS V loads are non-temporal");
-            __builtin_amdgcn_raw_ptr_buffer_load_lds(vr, dst, 16, off, 0, 0, 2);
+            __builtin_amdgcn_raw_ptr_buffer_load_lds(vr, dst, 16, (int)ln.v[s], 0, 0, 2);
         }
     }
     __builtin_amdgcn_sched_barrier(0);
@@ -934,9 +970,9 @@ __device__ __forceinline__ void pipeline_step(const AttnParams &p, Chunk<D, KVT>
                                               const TilePages &tpn, uint16_t *__restrict__ sn,
                                               const Chunk<D, KVT> &cc, uint32_t tc,
                                               uint16_t *__restrict__ sc, const uint8_t *kbase,
-                                              const uint8_t *vbase, uint32_t hk, uint32_t wave,
-                                              State<D, NT, KVT> &st, f32x4 *sx) {
-    load_chunk<D, KVT>(p, cn, tn, tpn, kbase, vbase, hk, wave, sn);
+                                              const uint8_t *vbase, const DecLanes<D, KVT> &ln,
+                                              uint32_t wave, State<D, NT, KVT> &st, f32x4 *sx) {
+    load_chunk<D, KVT>(p, cn, tn, tpn, kbase, vbase, ln, sn);
     compute_chunk<D, NT, KVT>(p, cc, tc, st, sc, sx, wave);
 }
 
@@ -954,6 +990,10 @@ __device__ __forceinline__ void run_range(const AttnParams &p, const uint8_t *kb
     constexpr uint32_t SX = C::WAVES * NT * 2 * 64;
     const uint32_t shift = p.page_shift;
     const uint32_t page_limit = (s_hi + (1u << shift) - 1) >> shift;
+    const DecLanes<D, KVT> ln = dec_lanes<D, KVT>(hk, wave, p.hkv * D * C::EB);
+    // wave-uniform bases, so the descriptors are built by scalar instructions
+    kbase = uniform_ptr(kbase);
+    vbase = uniform_ptr(vbase);
     for (uint32_t wbeg = s_lo & ~31u; wbeg < s_hi;) {
         const uint32_t wend = min(s_hi, ((wbeg >> shift) + 64) << shift);
         PageWindow win;
@@ -969,20 +1009,20 @@ __device__ __forceinline__ void run_range(const AttnParams &p, const uint8_t *kb
             tp0 = tile_pages<C::FP8>(win, wbeg, shift, wend);
             tp1 = tile_pages<C::FP8>(win, wbeg + 32, shift, wend);
         }
-        load_chunk<D, KVT>(p, c0, wbeg, tp0, kbase, vbase, hk, wave, stage0);
-        pipeline_step<D, NT, KVT>(p, c1, wbeg + 32, tp1, stage1, c0, wbeg, stage0, kbase, vbase, hk,
+        load_chunk<D, KVT>(p, c0, wbeg, tp0, kbase, vbase, ln, stage0);
+        pipeline_step<D, NT, KVT>(p, c1, wbeg + 32, tp1, stage1, c0, wbeg, stage0, kbase, vbase, ln,
                                   wave, st, sxb + parity * SX);
         parity ^= 1;
         if (wbeg + 32 < wend) {
             for (uint32_t t = wbeg + 32;; t += 64) {
                 // loads past wend carry no traffic
                 pipeline_step<D, NT, KVT>(p, c0, t + 32, tile_pages<C::FP8>(win, t + 32, shift, wend),
-                                          stage0, c1, t, stage1, kbase, vbase, hk, wave, st,
+                                          stage0, c1, t, stage1, kbase, vbase, ln, wave, st,
                                           sxb + parity * SX);
                 parity ^= 1;
                 if (t + 32 >= wend) break;
                 pipeline_step<D, NT, KVT>(p, c1, t + 64, tile_pages<C::FP8>(win, t + 64, shift, wend),
-                                          stage1, c0, t + 32, stage0, kbase, vbase, hk, wave, st,
+                                          stage1, c0, t + 32, stage0, kbase, vbase, ln, wave, st,
                                           sxb + parity * SX);
                 parity ^= 1;
                 if (t + 64 >= wend) break;
