@@ -1824,8 +1824,9 @@ __global__ __launch_bounds__(WCfg<D>::THREADS, 2) void wide_kernel(AttnParams p)
 // row (SPLIT = 2, blockIdx.z): D/4/SPLIT lanes cover the workgroup's share of a record's row
 // as float4 quads, so 256 threads hold 1024*SPLIT/D records per pass, and a batch of
 // kCombinePasses passes is loaded at once (every load independent of the weights).  Each
-// batch raises the running reference maximum to the batch's, rescaling what came before;
-// the record groups are summed through LDS at the end.
+// thread merges its records against its own running reference maximum; the record groups
+// sharing a quad are then merged pairwise (max, rescale both, add) by lane shuffles within
+// a wave and through LDS across the waves, with one barrier.
 constexpr uint32_t kCombineThreads = 256;
 constexpr uint32_t kCombinePasses = 8;
 constexpr uint32_t kWideNTDev = 8; // 16-column tiles of a prefill unit
@@ -1844,9 +1845,10 @@ __global__ __launch_bounds__(kCombineThreads) void combine_kernel(AttnParams p) 
     const uint32_t qoff = blockIdx.z * Q;
     constexpr uint32_t RPP = kCombineThreads / Q;  // records per pass
     constexpr uint32_t COLS = 16 * NT;
-    __shared__ float4 s_num[RPP][Q];
-    __shared__ float s_den[RPP][Q];
-    __shared__ float s_max[2][kCombineThreads / 64];
+    constexpr uint32_t WAVES = kCombineThreads / 64;
+    static_assert(Q <= 64 && 64 % Q == 0, "a wave holds whole record rows");
+    __shared__ float4 s_num[WAVES][Q];
+    __shared__ float s_den[WAVES][Q], s_m[WAVES][Q];
     const uint32_t u = blockIdx.x, col = blockIdx.y, t = threadIdx.x;
     const MergeDesc md = p.merge[u];
     if (md.n == 0) return; // written directly by its only workgroup, or no such unit
@@ -1854,9 +1856,9 @@ __global__ __launch_bounds__(kCombineThreads) void combine_kernel(AttnParams p) 
     const uint32_t n = md.n, rec0 = md.rec0;
     const uint32_t q = t % Q, rg = t / Q;
     const float4 *po = (const float4 *)p.part_o;
+    // per thread: its records merged against its own reference maximum M
     float M = -INFINITY, den = 0.0f;
     float4 num = make_float4(0.0f, 0.0f, 0.0f, 0.0f);
-    uint32_t parity = 0;
     for (uint32_t base = 0; base < n; base += RPP * kCombinePasses) {
         float4 o[kCombinePasses];
         float m[kCombinePasses], l[kCombinePasses];
@@ -1881,22 +1883,15 @@ __global__ __launch_bounds__(kCombineThreads) void combine_kernel(AttnParams p) 
             m[k] = ml.x;
             l[k] = r < n ? ml.y : 0.0f;
         }
-        float bm = -INFINITY;
+        float bm = M;
 #pragma unroll
         for (uint32_t k = 0; k < kCombinePasses; k++)
             if (l[k] > 0.0f) bm = fmaxf(bm, m[k]);
-        bm = wave_max(bm);
-        if ((t & 63) == 0) s_max[parity][t >> 6] = bm;
-        __syncthreads();
-#pragma unroll
-        for (uint32_t w = 0; w < kCombineThreads / 64; w++) bm = fmaxf(bm, s_max[parity][w]);
-        parity ^= 1;
-        const float nm = fmaxf(M, bm);
-        if (nm != M) {
-            const float f = M == -INFINITY ? 0.0f : fast_exp2(M - nm);
+        if (bm != M) {
+            const float f = M == -INFINITY ? 0.0f : fast_exp2(M - bm);
             num.x *= f; num.y *= f; num.z *= f; num.w *= f;
             den *= f;
-            M = nm;
+            M = bm;
         }
 #pragma unroll
         for (uint32_t k = 0; k < kCombinePasses; k++) {
@@ -1909,17 +1904,37 @@ __global__ __launch_bounds__(kCombineThreads) void combine_kernel(AttnParams p) 
             den = REC ? den + w : fmaf(w, l[k], den);
         }
     }
-    // record groups rg share the quad q: sum them (den likewise counts every record once)
-    s_num[rg][q] = num;
-    s_den[rg][q] = den;
-    __syncthreads();
-    if (rg != 0) return;
+    // merge (M, num, den) of the record groups that share the quad q: lanes Q apart within a
+    // wave by shuffles, then the waves through LDS (a group without records holds M = -inf
+    // and zeros, and weighs zero)
+    auto merge = [&](float mo, float4 no, float dn) {
+        const float nm = fmaxf(M, mo);
+        const float a = M == -INFINITY ? 0.0f : fast_exp2(M - nm);
+        const float b = mo == -INFINITY ? 0.0f : fast_exp2(mo - nm);
+        num.x = num.x * a + no.x * b;
+        num.y = num.y * a + no.y * b;
+        num.z = num.z * a + no.z * b;
+        num.w = num.w * a + no.w * b;
+        den = den * a + dn * b;
+        M = nm;
+    };
 #pragma unroll
-    for (uint32_t g = 1; g < RPP; g++) {
-        const float4 x = s_num[g][q];
-        num.x += x.x; num.y += x.y; num.z += x.z; num.w += x.w;
-        den += s_den[g][q];
+    for (uint32_t sh = Q; sh < 64; sh <<= 1) {
+        const float mo = shfl_xor(M, sh), dn = shfl_xor(den, sh);
+        const float4 no = make_float4(shfl_xor(num.x, sh), shfl_xor(num.y, sh), shfl_xor(num.z, sh),
+                                      shfl_xor(num.w, sh));
+        merge(mo, no, dn);
     }
+    const uint32_t w = t >> 6;
+    if ((t & 63) < Q) {
+        s_num[w][q] = num;
+        s_den[w][q] = den;
+        s_m[w][q] = M;
+    }
+    __syncthreads();
+    if (t >= Q) return;
+#pragma unroll
+    for (uint32_t v = 1; v < WAVES; v++) merge(s_m[v][q], s_num[v][q], s_den[v][q]);
     const float inv = den > 0.0f ? 1.0f / den : 0.0f;
     const uint32_t row = md.rowbeg + col / p.group, head = (md.nrows_hk >> 16) * p.group + col % p.group;
     const size_t at = ((size_t)row * p.hq + head) * D + 4 * (qoff + q);
