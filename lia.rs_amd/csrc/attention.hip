@@ -1829,6 +1829,9 @@ __global__ __launch_bounds__(WCfg<D>::THREADS, 2) void wide_kernel(AttnParams p)
 // a wave and through LDS across the waves, with one barrier.
 constexpr uint32_t kCombineThreads = 256;
 constexpr uint32_t kCombinePasses = 8;
+constexpr uint32_t kCombineWaveCols = kCombineThreads / 64;
+// Units expected to hold at most this many records merge one column per wave.
+constexpr uint32_t kWaveColRecords = 16;
 constexpr uint32_t kWideNTDev = 8; // 16-column tiles of a prefill unit
 
 __device__ __forceinline__ float wave_max(float v) {
@@ -1840,21 +1843,26 @@ __device__ __forceinline__ float wave_max(float v) {
 // REC: record rows in f32 unnormalised (0), or normalised in f16 (1) or bf16 (2).
 template <int D, int NT, int SPLIT, int REC>
 __global__ __launch_bounds__(kCombineThreads) void combine_kernel(AttnParams p) {
+    // SPLIT = 0: one wave per column (kCombineWaveCols columns per workgroup), for units with
+    // few records: no LDS and no barrier
+    constexpr bool WC = SPLIT == 0;
     constexpr uint32_t QF = D / 4;                 // float4 quads per record row
-    constexpr uint32_t Q = QF / SPLIT;             // quads of this workgroup's share (blockIdx.z)
-    const uint32_t qoff = blockIdx.z * Q;
-    constexpr uint32_t RPP = kCombineThreads / Q;  // records per pass
+    constexpr uint32_t Q = QF / (WC ? 1 : SPLIT);  // quads of this workgroup's share (blockIdx.z)
+    const uint32_t qoff = WC ? 0 : blockIdx.z * Q;
+    constexpr uint32_t TPC = WC ? 64 : kCombineThreads; // threads per column
+    constexpr uint32_t RPP = TPC / Q;              // records per pass
     constexpr uint32_t COLS = 16 * NT;
     constexpr uint32_t WAVES = kCombineThreads / 64;
     static_assert(Q <= 64 && 64 % Q == 0, "a wave holds whole record rows");
-    __shared__ float4 s_num[WAVES][Q];
-    __shared__ float s_den[WAVES][Q], s_m[WAVES][Q];
-    const uint32_t u = blockIdx.x, col = blockIdx.y, t = threadIdx.x;
+    __shared__ float4 s_num[WC ? 1 : WAVES][Q];
+    __shared__ float s_den[WC ? 1 : WAVES][Q], s_m[WC ? 1 : WAVES][Q];
+    const uint32_t u = blockIdx.x, t = threadIdx.x;
+    const uint32_t col = WC ? blockIdx.y * kCombineWaveCols + (t >> 6) : blockIdx.y;
     const MergeDesc md = p.merge[u];
     if (md.n == 0) return; // written directly by its only workgroup, or no such unit
     if (col >= (md.nrows_hk & 0xffffu) * p.group) return;
     const uint32_t n = md.n, rec0 = md.rec0;
-    const uint32_t q = t % Q, rg = t / Q;
+    const uint32_t q = t % Q, rg = (t % TPC) / Q;
     const float4 *po = (const float4 *)p.part_o;
     // per thread: its records merged against its own reference maximum M
     float M = -INFINITY, den = 0.0f;
@@ -1925,16 +1933,20 @@ __global__ __launch_bounds__(kCombineThreads) void combine_kernel(AttnParams p) 
                                       shfl_xor(num.w, sh));
         merge(mo, no, dn);
     }
-    const uint32_t w = t >> 6;
-    if ((t & 63) < Q) {
-        s_num[w][q] = num;
-        s_den[w][q] = den;
-        s_m[w][q] = M;
-    }
-    __syncthreads();
-    if (t >= Q) return;
+    if constexpr (WC) {
+        if ((t & 63) >= Q) return;
+    } else {
+        const uint32_t w = t >> 6;
+        if ((t & 63) < Q) {
+            s_num[w][q] = num;
+            s_den[w][q] = den;
+            s_m[w][q] = M;
+        }
+        __syncthreads();
+        if (t >= Q) return;
 #pragma unroll
-    for (uint32_t v = 1; v < WAVES; v++) merge(s_m[v][q], s_num[v][q], s_den[v][q]);
+        for (uint32_t v = 1; v < WAVES; v++) merge(s_m[v][q], s_num[v][q], s_den[v][q]);
+    }
     const float inv = den > 0.0f ? 1.0f / den : 0.0f;
     const uint32_t row = md.rowbeg + col / p.group, head = (md.nrows_hk >> 16) * p.group + col % p.group;
     const size_t at = ((size_t)row * p.hq + head) * D + 4 * (qoff + q);
@@ -2079,6 +2091,10 @@ static hipError_t launch_combine(uint32_t split, dim3 grid, const AttnParams &p,
     const dim3 block(kCombineThreads);
     if (split == 4) return launch<combine_kernel<D, NT, 4, REC>>(grid, block, 0, s, p);
     if (split == 2) return launch<combine_kernel<D, NT, 2, REC>>(grid, block, 0, s, p);
+    if (split == 0) {
+        const dim3 g(grid.x, (grid.y + kCombineWaveCols - 1) / kCombineWaveCols);
+        return launch<combine_kernel<D, NT, 0, REC>>(g, block, 0, s, p);
+    }
     return launch<combine_kernel<D, NT, 1, REC>>(grid, block, 0, s, p);
 }
 
@@ -2396,7 +2412,7 @@ static int run_stages(int stages, const lia_attention_config *c, uint32_t n_seqs
         const int rec = p.out_f32 ? 0 : c->kv_dtype == LIA_BF16 ? 2 : c->kv_dtype == LIA_F16 ? 1 : 0;
         const uint32_t est_units = max((n_rows + rpc - 1) / rpc, n_seqs) * c->num_kv_heads;
         const uint32_t per_unit = n_wg / est_units; // records per unit, roughly
-        const uint32_t split = per_unit >= 128 ? 4 : grid.x * grid.y < 256 ? 2 : 1;
+        const uint32_t split = per_unit >= 128 ? 4 : grid.x * grid.y < 256 ? 2 : per_unit <= kWaveColRecords ? 0 : 1;
         grid.z = split;
 #define LIA_COMBINE(DD, NN)                                                                      \
     do {                                                                                         \
