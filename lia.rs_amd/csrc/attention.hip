@@ -155,6 +155,9 @@ __device__ __forceinline__ uint32_t new_blocks_before(uint32_t m, uint32_t rpc) 
 
 constexpr uint32_t kPlanSeqs = 1024; // sequences the plan keeps in LDS (one per thread)
 constexpr uint32_t kPlanThreads = 1024;
+// Workgroups of plan_lds_kernel: each computes the per-sequence extents and then writes an
+// interleaved share of the descriptors (one workgroup issued them all at 16 waves on one CU).
+constexpr uint32_t kPlanGroups = 8;
 // Cost of starting a unit, in 32-key blocks, that the balanced partition charges each unit: a
 // range crossing into a unit loads its queries, unit descriptor and page window before its first
 // keys.  Measured best: 8 for the prefill kernel (config 3 step 303 -> 246 us against no charge),
@@ -187,6 +190,9 @@ __device__ void plan_lds(uint32_t n_seqs, const uint32_t *cu, const uint32_t *po
     // barriers need not wait for the descriptor stores in flight.
     constexpr uint32_t T = kPlanThreads;
     const uint32_t t = threadIdx.x;
+    // the workgroups of the launch share the descriptor loops; each computes the per-sequence
+    // extents and range starts itself (they live in its LDS)
+    const uint32_t g0 = t * gridDim.x + blockIdx.x, GT = gridDim.x * T; // interleaved shares
     {
         const uint32_t b = t;
         uint32_t nu = 0, nb = 0, r0 = 0, nr = 0, p0 = 0, trow = 0;
@@ -219,11 +225,13 @@ __device__ void plan_lds(uint32_t n_seqs, const uint32_t *cu, const uint32_t *po
         s_u0[n_seqs] = carry_units;
         s_b0[n_seqs] = carry_blocks;
         s_c0[n_seqs] = carry_blocks + unit_cost * carry_units;
-        units[U] = UnitDesc{B, 0, 0, 0, 0, 0, 0, 0};
-        header[0] = U;
-        header[1] = B;
-        header[2] = N;
-        header[3] = overflow;
+        if (blockIdx.x == 0) {
+            units[U] = UnitDesc{B, 0, 0, 0, 0, 0, 0, 0};
+            header[0] = U;
+            header[1] = B;
+            header[2] = N;
+            header[3] = overflow;
+        }
     }
     lds_barrier();
     // last sequence b with arr[b] <= v (empty sequences share their offset with the next
@@ -248,9 +256,9 @@ __device__ void plan_lds(uint32_t n_seqs, const uint32_t *cu, const uint32_t *po
         const uint32_t b = seq_of(s_u0, u), ncb = (s_nr[b] + rpc - 1) / rpc, i = u - s_u0[b];
         return make_unit(b, i / ncb, i % ncb);
     };
-    for (uint32_t u = t; u < U; u += T) units[u] = unit_by_index(u);
+    for (uint32_t u = g0; u < U; u += GT) units[u] = unit_by_index(u);
     const uint32_t P = 1u << page_shift;
-    for (uint32_t w = N + t; w < n_wg; w += T) { // launched workgroups without work
+    for (uint32_t w = N + g0; w < n_wg; w += GT) { // launched workgroups without work
         WorkDesc d = {};
         work[w] = d;
     }
@@ -299,7 +307,7 @@ __device__ void plan_lds(uint32_t n_seqs, const uint32_t *cu, const uint32_t *po
         }
         return a;
     };
-    for (uint32_t u = t; u < max_units; u += T) {
+    for (uint32_t u = g0; u < max_units; u += GT) {
         MergeDesc m = {0, 0, 0, 0};
         if (u < U) {
             const UnitDesc ud = unit_by_index(u);
@@ -332,7 +340,7 @@ __device__ void plan_lds(uint32_t n_seqs, const uint32_t *cu, const uint32_t *po
     };
     // One work descriptor per thread and pass (unconditional page-table loads: an entry not
     // needed reads cu[0] and is replaced by 0).
-    for (uint32_t w0 = t; w0 < N; w0 += T) {
+    for (uint32_t w0 = g0; w0 < N; w0 += GT) {
         WorkDesc d[1];
         uint32_t v[1][kPrePages];
         {
@@ -2371,7 +2379,7 @@ static int run_stages(int stages, const lia_attention_config *c, uint32_t n_seqs
         MergeDesc *merge = (MergeDesc *)(ws + L.merge);
         uint32_t *header = (uint32_t *)(ws + L.header);
         if (n_seqs <= kPlanSeqs && n_wg <= kPlanThreads)
-            e = launch<plan_lds_kernel>(dim3(1), dim3(kPlanThreads), 0, s, n_seqs, cu_seqlens,
+            e = launch<plan_lds_kernel>(dim3(kPlanGroups), dim3(kPlanThreads), 0, s, n_seqs, cu_seqlens,
                                         positions, sequences, pages, c->stride, p.page_shift, rpc,
                                         c->num_kv_heads, L.max_units, n_wg,
                                         NT == kWideNT ? kUnitCostWide : kUnitCostDecode,
