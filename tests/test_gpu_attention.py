@@ -113,15 +113,18 @@ def test_odd_group_sizes(lia, wl, hq, hkv):
         _check(G.Case(b, seed=13), lia, f"group {hq // hkv} {name}")
 
 
-def test_config2_full_size_one_layer(lia, wl):
-    """North-star shape: batch 8, contexts U[1k, 32k], one layer against the oracle."""
-    b = wl.config2(seed=0, layers=1)
-    _check(G.Case(b, seed=0), lia, "cfg2 layer")
+@pytest.mark.parametrize("seed", [0, 1, 2, 3])
+def test_config2_full_size_one_layer(lia, wl, seed):
+    """North-star shape: batch 8, contexts U[1k, 32k], one layer against the oracle; seeds
+    other than the bench's draw other contexts and page tables."""
+    b = wl.config2(seed=seed, layers=1)
+    _check(G.Case(b, seed=seed), lia, f"cfg2 layer seed {seed}")
 
 
-def test_config4_mtp_full_size(lia, wl):
-    b = wl.config4(seed=0)
-    _check(G.Case(b, seed=0), lia, "cfg4")
+@pytest.mark.parametrize("seed", [0, 1, 2])
+def test_config4_mtp_full_size(lia, wl, seed):
+    b = wl.config4(seed=seed)
+    _check(G.Case(b, seed=seed), lia, f"cfg4 seed {seed}")
 
 
 def test_config5_fp8_long_contexts(lia, wl):

@@ -141,16 +141,17 @@ def test_fused_append_canonicalises_nan_like_kv_append(lia, wl, O, kv):
     assert np.array_equal(dev["vc"].cpu().numpy().view(np.uint16), vexp)
 
 
-def test_config3_full_step_with_shared_prefix_pages(lia, wl, O):
+@pytest.mark.parametrize("seed", [0, 1])
+def test_config3_full_step_with_shared_prefix_pages(lia, wl, O, seed):
     """BASELINE config 3 at full size as a step: device packing builds cu_seqlens, positions,
     sequences and the slot mapping from per-sequence counts (bit-exact against the oracle's
     host packing), the plan, the attention launch with the new K/V appended into the pool,
     and the merge.  The prefill chunks and decode rows share a 256-page cached prefix by
     reference count.  Outputs against the float64 oracle; the pool against lo_kv_append of
     the new rows into the pool as it was before the step."""
-    b = wl.config3(seed=0)
+    b = wl.config3(seed=seed)
     assert b.shared, "config 3 shares prefix pages"
-    case = G.Case(b, seed=0)
+    case = G.Case(b, seed=seed)
     g = b.geom
     P, W = g.page_size, g.hkv * g.d
     print(f"[case] cfg3 step: rows={b.n_rows} seqs={b.n_seqs} {b.notes}", flush=True)
