@@ -113,6 +113,29 @@ def test_odd_group_sizes(lia, wl, hq, hkv):
         _check(G.Case(b, seed=13), lia, f"group {hq // hkv} {name}")
 
 
+@pytest.mark.parametrize("n", [1, 2, 3, 4, 5, 8])
+@pytest.mark.parametrize("rows", ["decode", "mtp"])
+def test_batch_sizes_reversed_tables(lia, wl, n, rows):
+    """The reference's small-batch and long-context checks (tests/minicpm5.rs:248-288,
+    tests/minicpm5_long_context.rs:5-97): batches of 1-5 and 8 sequences with contexts up to
+    16k, their block tables handed out from the top of the pool downward and each sequence's
+    pages in reverse logical order (as the reference's reversed tables, llama_attention.rs:
+    222-236); one new row per sequence, or 2-4 verify rows."""
+    ctx = np.array([16384, 3000, 777, 12000, 48, 9000, 1, 5000][:n], np.int64)
+    q = np.ones(n, np.int64) if rows == "decode" else np.array([2, 4, 3, 2, 4, 3, 1, 2][:n], np.int64)
+    ctx = np.maximum(ctx, q)
+    g = wl.Geometry()
+    P = g.page_size
+    need = [-(-int(c) // P) for c in ctx]
+    pool = sum(need) + 3
+    tables, top = [], pool
+    for k in need:
+        tables.append(np.arange(top - k, top, dtype=np.uint32)[::-1].copy())
+        top -= k
+    b = wl.Batch(g, ctx, q, pool, tables, stride=max(need))
+    _check(G.Case(b, seed=70 + n), lia, f"batch {n} {rows} reversed tables")
+
+
 @pytest.mark.parametrize("seed", [0, 1, 2, 3])
 def test_config2_full_size_one_layer(lia, wl, seed):
     """North-star shape: batch 8, contexts U[1k, 32k], one layer against the oracle; seeds
