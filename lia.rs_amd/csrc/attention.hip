@@ -1326,6 +1326,7 @@ struct WideWindow {
     uint32_t base;          // first logical page covered (wave-uniform)
     uint32_t off_lo, off_hi; // per lane
     uint32_t bytes;         // per lane
+    float ks, vs;           // per lane, FP8 pools: the page's K and V scales (1 for a dead page)
 };
 
 // The 16-token tile a load reads: its page's byte offset and live bytes (0: the loads move
@@ -1337,7 +1338,8 @@ struct WideTile {
 
 __device__ __forceinline__ void wide_window(const AttnParams &p, WideWindow &w,
                                             const uint32_t *table, uint32_t first,
-                                            uint32_t limit, uint32_t tlim, uint32_t row_bytes) {
+                                            uint32_t limit, uint32_t tlim, uint32_t row_bytes,
+                                            uint32_t *page_out = nullptr) {
     const uint32_t shift = p.page_shift, P = 1u << shift;
     const uint32_t idx = first + lane_id();
     uint32_t page = idx;
@@ -1352,6 +1354,26 @@ __device__ __forceinline__ void wide_window(const AttnParams &p, WideWindow &w,
     w.off_lo = (uint32_t)off;
     w.off_hi = (uint32_t)(off >> 32);
     w.bytes = in_pool && tlim > pstart ? min(tlim - pstart, P) * row_bytes : 0u;
+    if (page_out) *page_out = page;
+}
+
+// The same with the page's FP8 scales of KV head hk.  A page without live keys (past the
+// range, or a table entry outside the pool) takes scale 1: its scores are masked to -inf
+// after the scaling, which a scale of 0 would turn into NaN.
+__device__ __forceinline__ void wide_window_fp8(const AttnParams &p, WideWindow &w,
+                                                const uint32_t *table, uint32_t first,
+                                                uint32_t limit, uint32_t tlim, uint32_t row_bytes,
+                                                uint32_t hk) {
+    uint32_t page = 0;
+    wide_window(p, w, table, first, limit, tlim, row_bytes, &page);
+    const uint32_t sb = p.pool_pages * p.hkv * 4;
+    const uint32_t at = w.bytes ? (page * p.hkv + hk) * 4 : sb; // past the end: reads 0
+    const float ks = __builtin_bit_cast(float, (uint32_t)__builtin_amdgcn_raw_buffer_load_b32(
+                                                   make_rsrc(p.k_scales, sb), (int)at, 0, 0));
+    const float vs = __builtin_bit_cast(float, (uint32_t)__builtin_amdgcn_raw_buffer_load_b32(
+                                                   make_rsrc(p.v_scales, sb), (int)at, 0, 0));
+    w.ks = w.bytes ? ks : 1.0f;
+    w.vs = w.bytes ? vs : 1.0f;
 }
 
 // Tile at key t0 of a window whose range ends at tlim (t0 past it: no live keys; before it
@@ -1439,6 +1461,77 @@ __device__ __forceinline__ void wide_tiles(const WideWindow &w, uint32_t t, uint
     for (int k = 0; k < WCfg<D>::PER; k++) out[k] = wide_tile(w, wide_tile_key<D>(t, wave, k), shift, tlim);
 }
 
+// FP8 pools: each lane's share of a chunk comes through registers instead of direct-to-LDS
+// loads.  The staged stages keep the 16-bit layout (the same swizzles, the same operand reads
+// and f16 MFMAs): lane L of the wave's k-th share fills LDS slot L of that share's 1 KB, the 16
+// bytes of f16 dims [8c, 8c + 8) of its token with c its swizzled chunk, from the 8 FP8 bytes
+// [8c, 8c + 8) of the token's head row, converted exactly to f16 times 2^-8 (the scales and
+// the 2^8 are applied to the scores and to the weights).
+template <int D>
+__device__ __forceinline__ WideLanes<D> wide_lanes_fp8(uint32_t wave, uint32_t hk, uint32_t row_bytes) {
+    using W = WCfg<D>;
+    const uint32_t lane = lane_id();
+    WideLanes<D> r;
+#pragma unroll
+    for (int k = 0; k < W::PER; k++) {
+        const uint32_t q = wave + k * W::WAVES;
+        const uint32_t tl = q * W::RPI + lane / W::CH;
+        const uint32_t tt = (q * W::RPI) % 16 + lane / W::CH;
+        const uint32_t pos = lane % W::CH;
+        const uint32_t rowoff = tt * row_bytes + hk * D;
+        r.k[k] = rowoff + (pos ^ swz_k<D>(tl)) * 8;
+        r.v[k] = rowoff + (pos ^ swz_v<D>(tl)) * 8;
+    }
+    return r;
+}
+
+template <int D>
+struct Fp8Share {
+    u32x2 k[WCfg<D>::PER], v[WCfg<D>::PER];
+};
+
+// Issue this wave's FP8 loads of chunk t (the tiles as wide_load takes them).
+template <int D>
+__device__ __forceinline__ void wide_issue_fp8(const AttnParams &p, uint32_t t,
+                                               const WideTile (&tile)[WCfg<D>::PER],
+                                               const uint8_t *kbase, const uint8_t *vbase,
+                                               const WideLanes<D> &ln, uint32_t wave,
+                                               Fp8Share<D> &r) {
+    using W = WCfg<D>;
+    const uint32_t P = 1u << p.page_shift;
+    const uint32_t row_bytes = p.hkv * D;
+#pragma unroll
+    for (int k = 0; k < W::PER; k++) {
+        const uint32_t q = wave + k * W::WAVES;
+        if (W::NI % W::WAVES == 0 || q < W::NI) {
+            const uint32_t sh = (wide_tile_key<D>(t, wave, k) & (P - 1)) * row_bytes;
+            const uint32_t nb = tile[k].bytes ? tile[k].bytes - sh : 0u;
+            r.k[k] = __builtin_bit_cast(u32x2, __builtin_amdgcn_raw_buffer_load_b64(
+                                                   make_rsrc(kbase + tile[k].off + sh, nb), (int)ln.k[k], 0, 0));
+            r.v[k] = __builtin_bit_cast(u32x2, __builtin_amdgcn_raw_buffer_load_b64(
+                                                   make_rsrc(vbase + tile[k].off + sh, nb), (int)ln.v[k], 0, 0));
+        }
+    }
+}
+
+// Convert the loaded share and write it into the stage (after the loads have landed).
+template <int D>
+__device__ __forceinline__ void wide_commit_fp8(const Fp8Share<D> &r, uint32_t wave, uint16_t *kst,
+                                                uint16_t *vst) {
+    using W = WCfg<D>;
+    const uint32_t lane = lane_id();
+#pragma unroll
+    for (int k = 0; k < W::PER; k++) {
+        const uint32_t q = wave + k * W::WAVES;
+        if (W::NI % W::WAVES == 0 || q < W::NI) {
+            const u32x2 a = e4m3x4_to_f16x4_scaled(r.k[k].x), b = e4m3x4_to_f16x4_scaled(r.k[k].y);
+            const u32x2 c = e4m3x4_to_f16x4_scaled(r.v[k].x), d = e4m3x4_to_f16x4_scaled(r.v[k].y);
+            *(u32x4 *)(kst + q * 512 + lane * 8) = u32x4{a.x, a.y, b.x, b.y};
+            *(u32x4 *)(vst + q * 512 + lane * 8) = u32x4{c.x, c.y, d.x, d.y};
+        }
+    }
+}
+
 template <int D>
 constexpr int kWideLoads = 2 * WCfg<D>::PER; // memory operations of one wide_load
 
@@ -1502,9 +1595,15 @@ __device__ __forceinline__ void load_q_full(const AttnParams &p, uint32_t row, u
 // wave reduce the maxima across lanes and rescale O and the mass.  The mass is accumulated by
 // the matrix unit: an MFMA of a ones operand against P^T sums each column over the chunk's
 // keys, with the same rounded weights as O.
+//
+// FP8 pools: the staged values are the codes times 2^-8 in f16; ksc[j] (the score scale times the
+// K scale of tile j's page times 2^8) scales the scores of tile j, and vsc[j] (V scale times 2^8)
+// its weights for P.V, while the mass sums the unscaled weights.
 template <int D, int KVT>
 __device__ __forceinline__ void wide_compute(const AttnParams &p, uint32_t t, WState<D, KVT> &st,
-                                             const uint16_t *kst, const uint16_t *vst, bool masked) {
+                                             const uint16_t *kst, const uint16_t *vst, bool masked,
+                                             const float (&ksc)[2], const float (&vsc)[2]) {
+    constexpr bool FP8 = KVT == LIA_FP8_E4M3;
     using W = WCfg<D>;
     constexpr bool MB = KVT == LIA_BF16;
     const uint32_t lane = lane_id(), g = lane >> 4, li = lane & 15;
@@ -1559,14 +1658,15 @@ __device__ __forceinline__ void wide_compute(const AttnParams &p, uint32_t t, WS
                 for (int i = 0; i < 4; i++)
                     if (t + 16 * j + 4 * g + i - st.lo >= st.lim[nt]) acc[j][nt][i] = -INFINITY;
     }
-    u32x4 pb[NTW];
+    u32x4 pb[NTW], pv[NTW]; // weights (the mass), and for FP8 pools the V-scaled ones (P.V)
 #pragma unroll
     for (int nt = 0; nt < NTW; nt++) {
         float e[2][4];
 #pragma unroll
         for (int j = 0; j < 2; j++)
 #pragma unroll
-            for (int i = 0; i < 4; i++) e[j][i] = __builtin_fmaf(acc[j][nt][i], p.scale_log2, -st.m[nt]);
+            for (int i = 0; i < 4; i++)
+                e[j][i] = __builtin_fmaf(acc[j][nt][i], FP8 ? ksc[j] : p.scale_log2, -st.m[nt]);
         float mx = fmaxf(fmaxf(fmaxf(e[0][0], e[0][1]), fmaxf(e[0][2], e[0][3])),
                          fmaxf(fmaxf(e[1][0], e[1][1]), fmaxf(e[1][2], e[1][3])));
         if (__builtin_amdgcn_ballot_w64(mx > st.thr[nt])) { // wave-uniform: rare after the first chunk
@@ -1591,11 +1691,20 @@ __device__ __forceinline__ void wide_compute(const AttnParams &p, uint32_t t, WS
             for (int i = 0; i < 4; i++) pr[j][i] = fast_exp2(e[j][i]);
         pb[nt] = u32x4{pack2<MB>(pr[0][0], pr[0][1]), pack2<MB>(pr[0][2], pr[0][3]),
                        pack2<MB>(pr[1][0], pr[1][1]), pack2<MB>(pr[1][2], pr[1][3])};
+        if constexpr (FP8) {
+#pragma unroll
+            for (int j = 0; j < 2; j++)
+#pragma unroll
+                for (int i = 0; i < 4; i++) pr[j][i] *= vsc[j];
+            pv[nt] = u32x4{pack2<MB>(pr[0][0], pr[0][1]), pack2<MB>(pr[0][2], pr[0][3]),
+                           pack2<MB>(pr[1][0], pr[1][1]), pack2<MB>(pr[1][2], pr[1][3])};
+        }
     }
 #pragma unroll
     for (int n = 0; n < W::DT; n++)
 #pragma unroll
-        for (int nt = 0; nt < NTW; nt++) st.o[nt][n] = mfma16x16x32<MB>(vt[n], pb[nt], st.o[nt][n]);
+        for (int nt = 0; nt < NTW; nt++)
+            st.o[nt][n] = mfma16x16x32<MB>(vt[n], FP8 ? pv[nt] : pb[nt], st.o[nt][n]);
     // the mass: every row of the ones tile is the column's sum of this chunk's weights
     constexpr uint32_t one2 = MB ? 0x3F803F80u : 0x3C003C00u;
     const u32x4 ones = u32x4{one2, one2, one2, one2};
@@ -1623,7 +1732,8 @@ __device__ __forceinline__ void wide_step(const AttnParams &p, uint32_t tn,
     wait_vmcnt<(kWideStages - 2) * kWideLoads<D>>(); // the later chunks' loads stay in flight
     lds_barrier();
     wide_load<D>(p, tn, tpn, kbase, vbase, ln, wave, kn, vn);
-    if (active) wide_compute<D, KVT>(p, tc, st, kc, vc, !(tc >= free_lo && tc + 32 <= free_hi));
+    const float one[2] = {1.0f, 1.0f};
+    if (active) wide_compute<D, KVT>(p, tc, st, kc, vc, !(tc >= free_lo && tc + 32 <= free_hi), one, one);
 }
 
 // Keys [s_lo, s_hi) of one source into the running state (windows of at most 64 pages), through
@@ -1686,6 +1796,71 @@ __device__ __forceinline__ void wide_range(const AttnParams &p, const uint8_t *k
         }
     window_done:
         wait_vmcnt<0>(); // the trailing (empty) loads target stages about to be reused
+        wbeg = wend;
+    }
+}
+
+// Keys [s_lo, s_hi) of an FP8 pool into the running state.  A chunk's FP8 bytes are loaded into
+// registers one step before they are converted into its stage, right after the barrier that
+// retires the stage's previous chunk, and the next barrier publishes them: one chunk is computed
+// while the next is converted and the one after is loaded.
+template <int D>
+__device__ __forceinline__ void wide_range_fp8(const AttnParams &p, const uint8_t *kbase,
+                                               const uint8_t *vbase, const uint32_t *table,
+                                               uint32_t s_lo, uint32_t s_hi, uint32_t hk,
+                                               uint32_t wave, bool active,
+                                               WState<D, LIA_FP8_E4M3> &st,
+                                               uint16_t *const (&st_k)[4],
+                                               uint16_t *const (&st_v)[4], uint32_t free_lo,
+                                               uint32_t free_hi) {
+    constexpr int NS = kWideStages;
+    using W = WCfg<D>;
+    const uint32_t shift = p.page_shift;
+    const uint32_t page_limit = (s_hi + (1u << shift) - 1) >> shift;
+    const uint32_t row_bytes = p.hkv * D; // one byte per element
+    const WideLanes<D> ln = wide_lanes_fp8<D>(wave, hk, row_bytes);
+    kbase = uniform_ptr(kbase);
+    vbase = uniform_ptr(vbase);
+    const float sl = p.scale_log2 * 256.0f;
+    for (uint32_t wbeg = s_lo & ~31u; wbeg < s_hi;) {
+        const uint32_t wend = min(s_hi, ((wbeg >> shift) + 64) << shift);
+        WideWindow win;
+        wide_window_fp8(p, win, table, wbeg >> shift, page_limit, wend, row_bytes, hk);
+        WideTile tp[W::PER];
+        Fp8Share<D> r;
+        // every wave finished the previous window's chunks before their stages are refilled
+        lds_barrier();
+        wide_tiles<D>(win, wbeg, wave, shift, wend, tp);
+        wide_issue_fp8<D>(p, wbeg, tp, kbase, vbase, ln, wave, r);
+        wait_vmcnt<0>();
+        wide_commit_fp8<D>(r, wave, st_k[0], st_v[0]);
+        wide_tiles<D>(win, wbeg + 32, wave, shift, wend, tp);
+        wide_issue_fp8<D>(p, wbeg + 32, tp, kbase, vbase, ln, wave, r);
+        for (uint32_t t = wbeg;; t += 32 * NS) {
+#pragma unroll
+            for (int c = 0; c < NS; c++) {
+                const uint32_t tc = t + 32 * c;
+                lds_barrier(); // chunk tc is in its stage; chunk tc - 32 is retired
+                wait_vmcnt<0>();
+                wide_commit_fp8<D>(r, wave, st_k[(c + 1) % NS], st_v[(c + 1) % NS]); // chunk tc + 32
+                wide_tiles<D>(win, tc + 64, wave, shift, wend, tp);
+                wide_issue_fp8<D>(p, tc + 64, tp, kbase, vbase, ln, wave, r);
+                if (active) {
+                    float ksc[2], vsc[2];
+#pragma unroll
+                    for (int j = 0; j < 2; j++) {
+                        const int rel = (int)((((tc + 16 * j) >> shift) - win.base) & 63);
+                        ksc[j] = sl * __builtin_bit_cast(float, __builtin_amdgcn_readlane(__builtin_bit_cast(int, win.ks), rel));
+                        vsc[j] = 256.0f * __builtin_bit_cast(float, __builtin_amdgcn_readlane(__builtin_bit_cast(int, win.vs), rel));
+                    }
+                    wide_compute<D, LIA_FP8_E4M3>(p, tc, st, st_k[c], st_v[c],
+                                                  !(tc >= free_lo && tc + 32 <= free_hi), ksc, vsc);
+                }
+                if (tc + 32 >= wend) goto window_done;
+            }
+        }
+    window_done:
+        wait_vmcnt<0>(); // the trailing (empty) loads
         wbeg = wend;
     }
 }
@@ -1761,7 +1936,13 @@ __global__ __launch_bounds__(WCfg<D>::THREADS, 2) void wide_kernel(AttnParams p)
             free_hi = r_lo + (w0 > 0 ? (uint32_t)w0 : 0u);
         };
         const uint8_t *kpool = (const uint8_t *)p.kc, *vpool = (const uint8_t *)p.vc;
-        if (!fused) {
+        if constexpr (KVT == LIA_FP8_E4M3) {
+            // FP8 pools: the step's rows are appended by a launch of their own first
+            const uint32_t r_lo = key_of(a), r_hi = min(key_of(e), kend);
+            set_limits(r_lo, r_hi, 0);
+            wide_range_fp8<D>(p, kpool, vpool, table, r_lo, r_hi, hk, wave, active, st, st_k, st_v,
+                              r_lo, free_hi);
+        } else if (!fused) {
             const uint32_t r_lo = key_of(a), r_hi = min(key_of(e), kend);
             set_limits(r_lo, r_hi, 0);
             wide_range<D, KVT>(p, kpool, vpool, table, r_lo, r_hi, use_pre, wd.pre, hk, wave, active,
@@ -1813,7 +1994,7 @@ __global__ __launch_bounds__(WCfg<D>::THREADS, 2) void wide_kernel(AttnParams p)
                 // with the mass and maximum in f32
                 const size_t rb = (size_t)rec * COLS + col;
                 const float inv = lt > 0.0f ? 1.0f / lt : 0.0f;
-                if (p.out_f32) {
+                if (p.out_f32 || KVT == LIA_FP8_E4M3) { // the combine reads f32 rows for both
                     float *po = p.part_o + rb * D + 4 * g;
 #pragma unroll
                     for (int n = 0; n < W::DT; n++) *(f32x4 *)(po + 16 * n) = st.o[nt][n] * inv;
@@ -2096,10 +2277,10 @@ struct Layout {
 // Columns per unit / 16.  Decode-only batches (one row per sequence) use one 16-column tile
 // and batches with multi-row sequences (MTP verify, short chunks) two, in the decode kernel;
 // batches averaging 16 or more rows per sequence (prefill chunks) use the prefill kernel's
-// 128 columns (16-bit pools; FP8 pools stay on the decode kernel).
+// 128 columns (on FP8 pools with the rows staged through registers).
 constexpr uint32_t kWideNT = kWideNTDev;
 static inline uint32_t nt_for(uint32_t n_rows, uint32_t n_seqs, uint32_t group, int kv_dtype) {
-    if (n_rows >= 16 * n_seqs && kv_dtype != LIA_FP8_E4M3 && group <= 32) return kWideNT;
+    if (n_rows >= 16 * n_seqs && group <= 32) return kWideNT;
     return (n_rows > n_seqs || group > 16) ? 2 : 1;
 }
 
@@ -2129,9 +2310,8 @@ static Layout layout_for(const lia_attention_config *c, uint32_t n_wg) {
     off = (off + 255) & ~(size_t)255;
     L.merge = off; off += (size_t)L.max_units * sizeof(MergeDesc);
     off = (off + 255) & ~(size_t)255;
-    // record columns: 16 per tile, up to two tiles on the decode kernel (FP8 pools) or the
-    // prefill kernel's kWideNT
-    const size_t rec_cols = 16 * (c->kv_dtype == LIA_FP8_E4M3 ? 2 : kWideNT);
+    // record columns: 16 per tile, up to the prefill kernel's kWideNT
+    const size_t rec_cols = 16 * kWideNT;
     L.part_ml = off; off += (size_t)L.max_records * rec_cols * 2 * sizeof(float);
     off = (off + 255) & ~(size_t)255;
     L.part_o = off; off += (size_t)L.max_records * rec_cols * c->head_dim * sizeof(float);
@@ -2241,7 +2421,8 @@ static uint32_t resident_wide() {
 template <int D, int NT>
 static uint32_t resident_kv(int kv) {
     if constexpr (NT == kWideNT) {
-        return kv == LIA_BF16 ? resident_wide<D, LIA_BF16>() : resident_wide<D, LIA_F16>();
+        return kv == LIA_BF16 ? resident_wide<D, LIA_BF16>()
+               : kv == LIA_F16 ? resident_wide<D, LIA_F16>() : resident_wide<D, LIA_FP8_E4M3>();
     } else {
         if (kv == LIA_BF16) return resident_workgroups<D, NT, LIA_BF16>();
         if (kv == LIA_F16) return resident_workgroups<D, NT, LIA_F16>();
@@ -2296,7 +2477,8 @@ template <int D>
 static hipError_t launch_wide(int kv, const AttnParams &p, uint32_t n_wg, hipStream_t s) {
     const dim3 block(WCfg<D>::THREADS);
     if (kv == LIA_BF16) return launch<wide_kernel<D, LIA_BF16>>(dim3(n_wg), block, 0, s, p);
-    return launch<wide_kernel<D, LIA_F16>>(dim3(n_wg), block, 0, s, p);
+    if (kv == LIA_F16) return launch<wide_kernel<D, LIA_F16>>(dim3(n_wg), block, 0, s, p);
+    return launch<wide_kernel<D, LIA_FP8_E4M3>>(dim3(n_wg), block, 0, s, p);
 }
 
 template <int D, int NT>
@@ -2390,7 +2572,7 @@ static int run_stages(int stages, const lia_attention_config *c, uint32_t n_seqs
         // Ranges in launch order, or XCD-major (each XCD a contiguous share) on FP8 pools.
         // Measured: launch order makes config 2 1.1 % faster and the config-3 step 2 us shorter;
         // XCD-major keeps config 5 2 us shorter.
-        const uint32_t xcd = c->kv_dtype == LIA_FP8_E4M3;
+        const uint32_t xcd = c->kv_dtype == LIA_FP8_E4M3 && NT != kWideNT;
         if (n_seqs <= kPlanSeqs && n_wg <= kPlanThreads)
             e = launch<plan_lds_kernel>(dim3(kPlanGroups), dim3(kPlanThreads), 0, s, n_seqs, cu_seqlens,
                                         positions, sequences, pages, c->stride, p.page_shift, rpc,

@@ -282,7 +282,7 @@ def test_many_sequences(lia, wl, rows_kind):
     _check(G.Case(b, seed=29), lia, f"many sequences {rows_kind}")
 
 
-@pytest.mark.parametrize("kv", [BF16, F16])
+@pytest.mark.parametrize("kv", [BF16, F16, FP8])
 def test_prefill_few_units_long_prefix(lia, wl, kv):
     """A short chunk after a long prefix on the prefill kernel: one or two 128-column units per
     KV head take every workgroup, so each unit leaves hundreds of split records and the
@@ -350,9 +350,10 @@ def test_prefill_bf16_values_beyond_f16_range(lia, wl):
     assert mx < 2e-2 * 2e5 and mean < 2e-3 * 2e5
 
 
-@pytest.mark.parametrize("kv,d,page", [(F16, 128, 32), (BF16, 64, 16)])
+@pytest.mark.parametrize("kv,d,page", [(F16, 128, 32), (BF16, 64, 16), (FP8, 128, 16),
+                                       (FP8, 128, 32), (FP8, 64, 16)])
 def test_prefill_kernel_geometries(lia, wl, kv, d, page):
-    """Prefill units of 128 columns over other page sizes, head_dim 64 and f16 pools, with
+    """Prefill units of 128 columns over other page sizes, head_dim 64, f16 and FP8 pools, with
     chunks that are not multiples of the unit's rows and prefixes not page-aligned."""
     g = wl.Geometry(hq=16, hkv=2, d=d, page_size=page, kv_dtype=kv, q_dtype=F32, out_dtype=F32)
     b = wl.custom([300, 1000 + 77, 40, 513], [300, 77, 40, 33], geom=g, seed=9)

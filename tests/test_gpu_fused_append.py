@@ -209,7 +209,7 @@ def test_config3_full_step_with_shared_prefix_pages(lia, wl, O, seed):
     assert mx < 2e-2 and mean < 2e-3
 
 
-@pytest.mark.parametrize("case_name", ["decode_mtp_prefill", "config5_head"])
+@pytest.mark.parametrize("case_name", ["decode_mtp_prefill", "config5_head", "prefill_chunks"])
 def test_fused_fp8_append(lia, wl, O, case_name):
     """lia_attention_partial_append_fp8: the step's bf16 rows are quantised into the FP8 pool
     exactly as lia_kv_append(src bf16) stores them - bytes and per-(page, head) scales, fresh
@@ -220,6 +220,11 @@ def test_fused_fp8_append(lia, wl, O, case_name):
         keep = 8
         ctx, q_len = b5.ctx[:keep], b5.q_len[:keep]
         g = b5.geom
+    elif case_name == "prefill_chunks":
+        # prefill chunks after cached prefixes next to decode rows: 152 rows per sequence on
+        # average, so the prefill kernel attends the FP8 pool
+        ctx, q_len = [300, 1000 + 200, 2048 + 260, 700, 1500], [300, 200, 260, 1, 1]
+        g = wl.Geometry(kv_dtype=FP8)
     else:
         # decode rows at and past page boundaries (fresh pages), MTP rows crossing a page,
         # a prefill chunk of 40 rows after 16 cached keys
