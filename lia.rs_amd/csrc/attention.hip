@@ -1465,8 +1465,8 @@ __device__ __forceinline__ void wide_tiles(const WideWindow &w, uint32_t t, uint
 // loads.  The staged stages keep the 16-bit layout (the same swizzles, the same operand reads
 // and f16 MFMAs): lane L of the wave's k-th share fills LDS slot L of that share's 1 KB, the 16
 // bytes of f16 dims [8c, 8c + 8) of its token with c its swizzled chunk, from the 8 FP8 bytes
-// [8c, 8c + 8) of the token's head row, converted exactly to f16 times 2^-8 (the scales and
-// the 2^8 are applied to the scores and to the weights).
+// [8c, 8c + 8) of the token's head row, converted exactly to f16 by the hardware conversion
+// (every e4m3 code is an f16 value; the scales are applied to the scores and to the weights).
 template <int D>
 __device__ __forceinline__ WideLanes<D> wide_lanes_fp8(uint32_t wave, uint32_t hk, uint32_t row_bytes) {
     using W = WCfg<D>;
@@ -1483,6 +1483,17 @@ __device__ __forceinline__ WideLanes<D> wide_lanes_fp8(uint32_t wave, uint32_t h
         r.v[k] = rowoff + (pos ^ swz_v<D>(tl)) * 8;
     }
     return r;
+}
+
+// Eight e4m3 bytes (byte i of the pair's dwords in order) -> eight f16, exactly.
+__device__ __forceinline__ u32x4 e4m3x8_to_f16x8(u32x2 w) {
+    typedef _Float16 h2 __attribute__((ext_vector_type(2)));
+    const h2 a = __builtin_amdgcn_cvt_scalef32_pk_f16_fp8(w.x, 1.0f, false);
+    const h2 b = __builtin_amdgcn_cvt_scalef32_pk_f16_fp8(w.x, 1.0f, true);
+    const h2 c = __builtin_amdgcn_cvt_scalef32_pk_f16_fp8(w.y, 1.0f, false);
+    const h2 d = __builtin_amdgcn_cvt_scalef32_pk_f16_fp8(w.y, 1.0f, true);
+    return u32x4{__builtin_bit_cast(uint32_t, a), __builtin_bit_cast(uint32_t, b),
+                 __builtin_bit_cast(uint32_t, c), __builtin_bit_cast(uint32_t, d)};
 }
 
 template <int D>
@@ -1524,10 +1535,8 @@ __device__ __forceinline__ void wide_commit_fp8(const Fp8Share<D> &r, uint32_t w
     for (int k = 0; k < W::PER; k++) {
         const uint32_t q = wave + k * W::WAVES;
         if (W::NI % W::WAVES == 0 || q < W::NI) {
-            const u32x2 a = e4m3x4_to_f16x4_scaled(r.k[k].x), b = e4m3x4_to_f16x4_scaled(r.k[k].y);
-            const u32x2 c = e4m3x4_to_f16x4_scaled(r.v[k].x), d = e4m3x4_to_f16x4_scaled(r.v[k].y);
-            *(u32x4 *)(kst + q * 512 + lane * 8) = u32x4{a.x, a.y, b.x, b.y};
-            *(u32x4 *)(vst + q * 512 + lane * 8) = u32x4{c.x, c.y, d.x, d.y};
+            *(u32x4 *)(kst + q * 512 + lane * 8) = e4m3x8_to_f16x8(r.k[k]);
+            *(u32x4 *)(vst + q * 512 + lane * 8) = e4m3x8_to_f16x8(r.v[k]);
         }
     }
 }
@@ -1596,9 +1605,9 @@ __device__ __forceinline__ void load_q_full(const AttnParams &p, uint32_t row, u
 // the matrix unit: an MFMA of a ones operand against P^T sums each column over the chunk's
 // keys, with the same rounded weights as O.
 //
-// FP8 pools: the staged values are the codes times 2^-8 in f16; ksc[j] (the score scale times the
-// K scale of tile j's page times 2^8) scales the scores of tile j, and vsc[j] (V scale times 2^8)
-// its weights for P.V, while the mass sums the unscaled weights.
+// FP8 pools: the staged values are the codes' values in f16; ksc[j] (the score scale times the
+// K scale of tile j's page) scales the scores of tile j, and vsc[j] (its V scale) its weights for
+// P.V, while the mass sums the unscaled weights.
 template <int D, int KVT>
 __device__ __forceinline__ void wide_compute(const AttnParams &p, uint32_t t, WState<D, KVT> &st,
                                              const uint16_t *kst, const uint16_t *vst, bool masked,
@@ -1821,7 +1830,7 @@ __device__ __forceinline__ void wide_range_fp8(const AttnParams &p, const uint8_
     const WideLanes<D> ln = wide_lanes_fp8<D>(wave, hk, row_bytes);
     kbase = uniform_ptr(kbase);
     vbase = uniform_ptr(vbase);
-    const float sl = p.scale_log2 * 256.0f;
+    const float sl = p.scale_log2;
     for (uint32_t wbeg = s_lo & ~31u; wbeg < s_hi;) {
         const uint32_t wend = min(s_hi, ((wbeg >> shift) + 64) << shift);
         WideWindow win;
@@ -1851,7 +1860,7 @@ __device__ __forceinline__ void wide_range_fp8(const AttnParams &p, const uint8_
                     for (int j = 0; j < 2; j++) {
                         const int rel = (int)((((tc + 16 * j) >> shift) - win.base) & 63);
                         ksc[j] = sl * __builtin_bit_cast(float, __builtin_amdgcn_readlane(__builtin_bit_cast(int, win.ks), rel));
-                        vsc[j] = 256.0f * __builtin_bit_cast(float, __builtin_amdgcn_readlane(__builtin_bit_cast(int, win.vs), rel));
+                        vsc[j] = __builtin_bit_cast(float, __builtin_amdgcn_readlane(__builtin_bit_cast(int, win.vs), rel));
                     }
                     wide_compute<D, LIA_FP8_E4M3>(p, tc, st, st_k[c], st_v[c],
                                                   !(tc >= free_lo && tc + 32 <= free_hi), ksc, vsc);
