@@ -51,6 +51,8 @@ def parse():
     ap.add_argument("--config", type=int, default=2, choices=(2, 3, 4, 5),
                     help="3, 4 or 5: time one layer of that BASELINE configuration's attention "
                          "(a parity workload, not the headline line) and print its own JSON line")
+    ap.add_argument("--kv", default=None, choices=("fp8",),
+                    help="with --config 3 or 4: the same batch on an FP8 e4m3 pool (per-page scales)")
     return ap.parse_args()
 
 
@@ -75,6 +77,8 @@ def side_config(args):
     lia = package()
     import lia_rs_amd.workloads as wl
     b = getattr(wl, "config%d" % args.config)(seed=args.seed)
+    if args.kv == "fp8":
+        b.geom = wl.Geometry(kv_dtype=wl.FP8)
     g = b.geom
     P = g.page_size
     tokens = b.pool_pages * P
@@ -156,7 +160,7 @@ def side_config(args):
         "value": round(us, 3), "unit": "us", "higher_is_better": False, "n_gpus": 1,
         "steps": args.steps, "warmup": args.warmup, "dtype": "fp8-e4m3 KV, bf16 Q" if fp8 else "bf16",
         "data": "synthetic (seeded, resident in HBM)",
-        "config": {"workload": f"BASELINE config {args.config}", "rows": rows,
+        "config": {"workload": f"BASELINE config {args.config}" + (" on an FP8 pool" if args.kv == "fp8" and args.config != 5 else ""), "rows": rows,
                    "sequences": b.n_seqs, "sum_ctx": int(b.ctx.sum())},
         "roofline": {"bound": "mfma" if mfma else "hbm",
                      "achieved": round(tflops if mfma else gbps, 1),
