@@ -864,8 +864,11 @@ __device__ __forceinline__ void compute_chunk(const AttnParams &p, const Chunk<D
     if constexpr (C::FP8) {
 #pragma unroll
         for (int j = 0; j < 2; j++) {
+            // the staged f16 V holds value * 2^-8 and O carries that factor until the unit
+            // ends (kFp8VUnscale), so a weight x * vs (x <= 2^8) stays finite in f16 for every
+            // page scale below 256
             kscale[j] = p.scale_log2 * c.ks[j] * 256.0f;
-            vscale[j] = c.vs[j] * 256.0f;
+            vscale[j] = c.vs[j];
         }
     }
     // partial scores of this wave's slice -> LDS
@@ -1131,6 +1134,9 @@ __device__ __forceinline__ void store_record(const AttnParams &p, size_t rb, con
     }
 }
 
+// FP8 pools stage V as value * 2^-8 (e4m3x4_to_f16x4_scaled); O is scaled back when a unit ends.
+constexpr float kFp8VUnscale = 256.0f;
+
 // At most 6 (16-bit pools) or 8 (FP8) decode waves run per CU, so the kernel may use the
 // registers of 3 (168) or 2 (256) waves per SIMD instead of squeezing into 4's (128).
 template <int KVT>
@@ -1247,6 +1253,10 @@ __global__ __launch_bounds__(D / 32 * 64, kMinWavesPerEU<KVT>) void attention_ke
             if (col >= ncols) continue;
             const uint32_t row = ud.rowbeg + col / p.group;
             const uint32_t head = hk * p.group + col % p.group;
+            if constexpr (C::FP8) {
+#pragma unroll
+                for (int n = 0; n < C::DTW; n++) st.o[nt][n] *= kFp8VUnscale;
+            }
             if (whole) {
                 const float inv = lt > 0.0f ? 1.0f / lt : 0.0f;
                 const size_t base = ((size_t)row * p.hq + head) * D + C::SW * wave + 4 * g;

@@ -415,3 +415,27 @@ def test_f16_split_records_saturate_at_the_f16_maximum(lia, wl):
     print(f"[case] f16 V at +-65504: max_abs={mx:.3e} mean_abs={mean:.3e}", flush=True)
     assert np.all(np.isfinite(got))
     assert mx < 2e-2 * 65504 and mean < 2e-3 * 65504
+
+
+def test_fp8_decode_large_v_scales(lia, wl):
+    """FP8 pool with V page scales of about 1-4 (V amax ~ 1000) and queries scaled by 4, so the
+    lazily raised softmax reference trails the scores by up to 8 log2 units (weights up to
+    2^8): the f16 weights of P.V stay finite for every page scale below 256.  Errors are
+    relative to the output's scale."""
+    from oracle import oracle as O
+    g = wl.Geometry(hq=16, hkv=2, d=128, kv_dtype=FP8)
+    b = wl.custom([4000, 9000, 700, 20000], [1, 1, 1, 1], geom=g, seed=25)
+    case = G.Case(b, seed=25, v_scale=250.0)
+    assert 0.5 < float(np.median(case.v_scales)) < 8.0
+    case.q_store = O.from_f32((case.q32 * 4.0).astype(np.float32), BF16)
+    case.q32 = O.to_f32(case.q_store, BF16)
+    print(f"[case] fp8 large V scales: v_scales {case.v_scales.min():.2f}..{case.v_scales.max():.2f}",
+          flush=True)
+    got = case.run(lia)
+    ref = case.f64()
+    assert np.all(np.isfinite(got))
+    scale = float(np.max(np.abs(ref)))
+    mx, mean = G.errors(got, ref)
+    print(f"[case] fp8 large V scales: max_abs/scale={mx / scale:.3e} mean/scale={mean / scale:.3e}",
+          flush=True)
+    assert mx / scale < 5e-2 and mean / scale < 5e-3
