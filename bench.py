@@ -171,6 +171,51 @@ def side_config(args):
     }), flush=True)
 
 
+def read_ceiling(lia, layer_bytes, L, reps):
+    """The contiguous-read ceiling on this device: lia_hbm_read of layer_bytes, timed exactly
+    as the attention kernel is (a graph of L back-to-back launches, replayed `reps` times, HIP
+    events on the replaying stream), over rotating buffers totalling >= 1 GiB so the 256 MB
+    last-level cache cannot serve them.  The best of three grid sizes; plus the rate of 1 GiB
+    reads."""
+    import torch
+    cus = lia.lib().lia_device_cus() or 256
+
+    def timed(nbytes, nbuf, wgs):
+        bufs = [torch.empty(nbytes, dtype=torch.uint8, device="cuda") for _ in range(nbuf)]
+        sink = torch.empty(wgs, dtype=torch.int32, device="cuda")
+        graph, stream = torch.cuda.CUDAGraph(), torch.cuda.Stream()
+        with torch.cuda.stream(stream):
+            lia.hbm_read(bufs[0], wgs, sink, stream=stream)
+            with torch.cuda.graph(graph, stream=stream):
+                for i in range(L):
+                    lia.hbm_read(bufs[i % nbuf], wgs, sink, stream=stream)
+        torch.cuda.synchronize()
+        for _ in range(3):
+            graph.replay()
+        torch.cuda.synchronize()
+        e0, e1 = torch.cuda.Event(enable_timing=True), torch.cuda.Event(enable_timing=True)
+        cur = torch.cuda.current_stream()
+        e0.record(cur)
+        for _ in range(reps):
+            graph.replay()
+        e1.record(cur)
+        torch.cuda.synchronize()
+        del bufs
+        return e0.elapsed_time(e1) * 1e3 / (reps * L)
+
+    nbuf = max(4, -(-(1 << 30) // layer_bytes))
+    runs = {wgs: timed(layer_bytes, nbuf, wgs) for wgs in (2 * cus, 4 * cus, 8 * cus)}
+    wgs, us = min(runs.items(), key=lambda kv: kv[1])
+    us_1g = min(timed(1 << 30, 3, w) for w in (4 * cus, 8 * cus))
+    torch.cuda.empty_cache()
+    gbps = layer_bytes / (us * 1e-6) / 1e9
+    return {"bytes": layer_bytes, "us": round(us, 3), "GBps": round(gbps, 1),
+            "frac_of_peak": round(gbps / PEAK_HBM_GBPS, 4), "workgroups": wgs,
+            "us_by_workgroups": {str(k): round(v, 3) for k, v in runs.items()},
+            "GBps_1GiB": round((1 << 30) / (us_1g * 1e-6) / 1e9, 1),
+            "kernel": "hbm_read_kernel (lia_hbm_read: contiguous, 16-byte non-temporal loads)"}
+
+
 def cpu_baseline(args, b, g, kpool, vpool, q, layer_bytes, L):
     """The oracle's scalar split-K + merge (kernels/llama.rs:63-159, 201-290) on one layer of
     the batch, compiled here at -O3 -march=native with OpenMP over (row, head, split): one
@@ -318,6 +363,12 @@ def main():
     log(f"attention kernel: {kernel_us:.2f} us/launch, {achieved:.1f} GB/s "
         f"({achieved / PEAK_HBM_GBPS:.1%} of peak), layer bytes {layer_bytes}")
 
+    # ---- the same bytes read contiguously on this device: the ceiling the kernel is held to
+    ceiling = read_ceiling(lia, layer_bytes, L, args.kernel_reps)
+    log(f"contiguous read of {layer_bytes} B: {ceiling['us']:.2f} us/launch, {ceiling['GBps']:.1f} GB/s "
+        f"({ceiling['frac_of_peak']:.1%} of peak; 1 GiB reads {ceiling['GBps_1GiB']:.1f} GB/s); "
+        f"attention kernel at {achieved / ceiling['GBps']:.1%} of it")
+
     # ---- the reference algorithm on the host cores (bounded sample, one layer repeated)
     cpu = None
     if not args.no_cpu:
@@ -353,6 +404,7 @@ def main():
             "traffic": load_traffic(args.traffic, kernel_us, layer_bytes),
             "kernel": "attention_kernel<128,1,bf16> (fused append)", "kernel_us": round(kernel_us, 3),
             "bytes_per_launch": layer_bytes,
+            "read_ceiling": dict(ceiling, kernel_frac_of_ceiling=round(achieved / ceiling["GBps"], 4)),
         },
         "cpu_baseline": cpu,
     }

@@ -367,6 +367,17 @@ int lia_attention_partial_append_fp8(const lia_attention_config *config, uint32_
                                      size_t workspace_bytes, void *out, lia_stream_t stream);
 
 /*
+ * Read-only HBM stream over [src, src + bytes): `workgroups` workgroups each read one
+ * contiguous share with 16-byte non-temporal loads and write one word (the XOR of what they
+ * read) to sink[workgroup].  No counterpart in the reference: it measures, on the same device,
+ * the rate of a contiguous read of as many bytes as an attention launch reads - the ceiling the
+ * HBM-bound kernels are compared with.  src 16-byte aligned; a share above 4 GiB returns
+ * LIA_E_UNSUPPORTED.
+ */
+int lia_hbm_read(const void *src, size_t bytes, uint32_t workgroups, uint32_t *sink,
+                 lia_stream_t stream);
+
+/*
  * lia_paged_attention without a workspace argument: the work list and split records live in
  * a device array the library holds for the process (lia_static_workspace_bytes() bytes on each
  * device it runs on), so the call allocates nothing.  No counterpart in the reference: this

@@ -164,6 +164,7 @@ EXPORTS = {
                                         C.c_void_p, C.c_void_p]),
     "lia_attention_merge": (C.c_int, [C.POINTER(AttentionConfig), C.c_uint32, C.c_uint32,
                                       C.c_void_p, C.c_size_t, C.c_void_p, C.c_void_p]),
+    "lia_hbm_read": (C.c_int, [C.c_void_p, C.c_size_t, C.c_uint32, C.c_void_p, C.c_void_p]),
     "lia_kv_page_bytes": (C.c_size_t, [C.POINTER(KVLayout), C.c_uint32]),
     "lia_kv_transfer_bytes": (C.c_size_t, [C.POINTER(KVLayout), C.c_uint32]),
     "lia_kv_write_pages": (C.c_int, [C.POINTER(KVLayout), C.POINTER(KVPlanes), C.c_uint32,
@@ -779,6 +780,13 @@ def attention_partial_append_fp8(config, n_seqs, pages, slot_mapping, q, new_k, 
         _dptr(new_k), _dptr(new_v), _dptr(kc), _dptr(vc), _dptr(k_scales), _dptr(v_scales),
         _dptr(workspace), workspace.numel() * workspace.element_size(), _dptr(out), _stream(stream))
     _check(st, "attention_partial_append_fp8")
+
+
+def hbm_read(src, workgroups, sink, nbytes=None, stream=None):
+    """Read-only HBM stream over a device tensor (lia_hbm_read): the contiguous-read ceiling."""
+    nbytes = src.numel() * src.element_size() if nbytes is None else nbytes
+    st = lib().lia_hbm_read(_dptr(src), nbytes, workgroups, _dptr(sink), _stream(stream))
+    _check(st, "hbm_read")
 
 
 def attention_merge(config, n_seqs, n_rows, out, workspace, stream=None):

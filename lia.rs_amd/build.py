@@ -13,7 +13,7 @@ CSRC = os.path.join(HERE, "csrc")
 OBJ = os.path.join(HERE, "_build")
 OUT = os.path.join(HERE, "liblia_hip.so")
 HIPCC = os.environ.get("HIPCC", "/opt/rocm/bin/hipcc")
-SOURCES = ["attention.hip", "kv.hip", "transfer.hip", "sampling.hip", "host.cpp", "page_cache.cpp"]
+SOURCES = ["attention.hip", "kv.hip", "transfer.hip", "sampling.hip", "hbm.hip", "host.cpp", "page_cache.cpp"]
 DEVICE_FLAGS = ["--offload-arch=gfx950", "-Xclang", "-target-feature", "-Xclang", "-packed-fp32-ops"]
 COMMON = ["-O3", "-fPIC", "-std=c++17", "-Wall", "-Wno-unused-result"]
 
