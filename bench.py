@@ -44,6 +44,10 @@ def parse():
     ap.add_argument("--seed", type=int, default=0)
     ap.add_argument("--cpu-seconds", type=float, default=10.0)
     ap.add_argument("--no-cpu", action="store_true")
+    ap.add_argument("--no-side", action="store_true",
+                    help="skip the one-layer steps of configs 3, 4 and 5 in the default run")
+    ap.add_argument("--side-steps", type=int, default=20,
+                    help="graph replays timed per side configuration (10 steps each)")
     ap.add_argument("--kernel-reps", type=int, default=20)
     ap.add_argument("--traffic", default=os.path.join(ROOT, "profiles",
                                                     "attention_decode_cfg2_traffic.json"),
@@ -65,26 +69,32 @@ def load_traffic(path, kernel_us, layer_bytes):
     return round((t["fetch_kib"] * t["fetch_scale"] + t["write_kib"] * t["write_scale"]) * 1024)
 
 
-def side_config(args):
+SIDE_NAMES = {3: "mixed chunked-prefill + decode attention step", 4: "MTP-verify attention step",
+              5: "FP8-KV decode attention step"}
+
+
+def side_measure(config, seed, steps, warmup, reps, kv=None):
     """One layer of BASELINE config 3 (mixed prefill + decode, MFMA-bound), 4 (MTP verify) or
     5 (FP8 decode) on resident synthetic data, timed as a step of its own: device packing,
     the plan, the KV append of the step's rows (fused into the attention launch on 16-bit
     pools; on FP8 pools quantised by the append launch of the same call, just before the
-    attention launch), split attention and the combine, replayed from a graph.  Prints a JSON line with the step time and the roofline of the
-    layer's algorithmic work."""
+    attention launch), split attention and the combine, replayed from a graph (`reps` steps
+    per graph).  The attention launch alone is timed the same way (a graph of `reps` launches
+    on one plan).  Returns the step and kernel times with their rooflines: MFMA for config 3,
+    HBM (and MFMA) for configs 4 and 5, against the layer's algorithmic work."""
     import torch
     from __graft_entry__ import package
     lia = package()
     import lia_rs_amd.workloads as wl
-    b = getattr(wl, "config%d" % args.config)(seed=args.seed)
-    if args.kv == "fp8":
+    b = getattr(wl, "config%d" % config)(seed=seed)
+    if kv == "fp8":
         b.geom = wl.Geometry(kv_dtype=wl.FP8)
     g = b.geom
     P = g.page_size
     tokens = b.pool_pages * P
     dev = "cuda"
     gen = torch.Generator(device=dev)
-    gen.manual_seed(args.seed)
+    gen.manual_seed(seed)
     fp8 = g.kv_dtype == lia.FP8
     rows = b.n_rows
     if fp8:
@@ -92,15 +102,12 @@ def side_config(args):
         vp = torch.randint(0, 120, (tokens, g.hkv, g.d), generator=gen, dtype=torch.uint8, device=dev)
         ks = torch.full((b.pool_pages * g.hkv,), 0.01, device=dev)
         vs = ks.clone()
-        newk = torch.randn((rows, g.hkv * g.d), generator=gen, device=dev).to(torch.bfloat16)
-        newv = torch.randn((rows, g.hkv * g.d), generator=gen, device=dev).to(torch.bfloat16)
-        layout = lia.KVLayout(g.hkv, g.d, P, b.pool_pages, g.kv_dtype)
     else:
         kp = torch.randn((tokens, g.hkv, g.d), generator=gen, device=dev).to(torch.bfloat16)
         vp = torch.randn((tokens, g.hkv, g.d), generator=gen, device=dev).to(torch.bfloat16)
         ks = vs = None
-        newk = torch.randn((rows, g.hkv * g.d), generator=gen, device=dev).to(torch.bfloat16)
-        newv = torch.randn((rows, g.hkv * g.d), generator=gen, device=dev).to(torch.bfloat16)
+    newk = torch.randn((rows, g.hkv * g.d), generator=gen, device=dev).to(torch.bfloat16)
+    newv = torch.randn((rows, g.hkv * g.d), generator=gen, device=dev).to(torch.bfloat16)
     q = torch.randn((rows, g.hq, g.d), generator=gen, device=dev).to(torch.bfloat16)
     out = torch.empty((rows, g.hq, g.d), dtype=torch.bfloat16, device=dev)
     i32 = lambda a: torch.from_numpy(np.asarray(a, np.uint32).view(np.int32)).to(dev)
@@ -115,59 +122,89 @@ def side_config(args):
                               g.out_dtype, g.scale, b.n_seqs, rows, int(b.ctx.max()))
     ws = torch.zeros(lia.workspace_bytes(cfg), dtype=torch.uint8, device=dev)
     context = b.stride * P
-    reps = max(args.kernel_reps, 1)
+    reps = max(reps, 1)
 
-    def step():
-        lia.pack_device(seq_slots, q_lens, cached, flat, b.stride, P, b.pool_pages, context, rows,
-                        cu, positions, sequences, slots, status)
-        lia.attention_plan(cfg, b.n_seqs, rows, cu, positions, sequences, ws, pages=flat)
+    def attend():
         if fp8:
             lia.attention_partial_append_fp8(cfg, b.n_seqs, flat, slots, q, newk, newv, kp, vp, ks, vs,
                                              out, ws)
         else:
             lia.attention_partial_append(cfg, b.n_seqs, flat, slots, q, newk, newv, kp, vp, out, ws)
+
+    def step():
+        lia.pack_device(seq_slots, q_lens, cached, flat, b.stride, P, b.pool_pages, context, rows,
+                        cu, positions, sequences, slots, status)
+        lia.attention_plan(cfg, b.n_seqs, rows, cu, positions, sequences, ws, pages=flat)
+        attend()
         lia.attention_merge(cfg, b.n_seqs, rows, out, ws)
+
+    def timed(body):
+        graph, stream = torch.cuda.CUDAGraph(), torch.cuda.Stream()
+        with torch.cuda.stream(stream):
+            with torch.cuda.graph(graph, stream=stream):
+                for _ in range(reps):
+                    body()
+        for _ in range(max(warmup, 1)):
+            graph.replay()
+        torch.cuda.synchronize()
+        e0, e1 = torch.cuda.Event(enable_timing=True), torch.cuda.Event(enable_timing=True)
+        cur = torch.cuda.current_stream()
+        e0.record(cur)
+        for _ in range(steps):
+            graph.replay()
+        e1.record(cur)
+        torch.cuda.synchronize()
+        return e0.elapsed_time(e1) * 1e3 / (steps * reps)
 
     step()
     torch.cuda.synchronize()
     if status.item() != 0:
         raise RuntimeError(f"device packing failed: status {status.item()}")
-    graph, stream = torch.cuda.CUDAGraph(), torch.cuda.Stream()
-    with torch.cuda.stream(stream):
-        with torch.cuda.graph(graph, stream=stream):
-            for _ in range(reps):
-                step()
-    for _ in range(max(args.warmup, 1)):
-        graph.replay()
-    torch.cuda.synchronize()
-    e0, e1 = torch.cuda.Event(enable_timing=True), torch.cuda.Event(enable_timing=True)
-    cur = torch.cuda.current_stream()
-    e0.record(cur)
-    for _ in range(args.steps):
-        graph.replay()
-    e1.record(cur)
-    torch.cuda.synchronize()
-    us = e0.elapsed_time(e1) * 1e3 / (args.steps * reps)
+    us = timed(step)
+    # the attention launch alone, on the plan the steps left (the FP8 call includes its append
+    # launch: the two launches of lia_attention_partial_append_fp8)
+    kus = timed(attend)
     # the appended rows: read from the step's rows (bf16) and written to the pool
     append_bytes = rows * g.hkv * g.d * 2 * (2 + (1 if fp8 else 2))
     nbytes, flops = b.algorithmic_bytes() + append_bytes, b.flops()
-    gbps, tflops = nbytes / (us * 1e-6) / 1e9, flops / (us * 1e-6) / 1e12
-    mfma = args.config == 3
-    names = {3: "mixed chunked-prefill + decode attention step", 4: "MTP-verify attention step",
-             5: "FP8-KV decode attention step"}
+    mfma = config == 3
+
+    def roof(t_us):
+        gbps, tflops = nbytes / (t_us * 1e-6) / 1e9, flops / (t_us * 1e-6) / 1e12
+        r = {"bound": "mfma" if mfma else "hbm", "achieved": round(tflops if mfma else gbps, 1),
+             "peak": PEAK_BF16_TFLOPS if mfma else PEAK_HBM_GBPS, "unit": "TFLOP/s" if mfma else "GB/s",
+             "frac": round((tflops / PEAK_BF16_TFLOPS) if mfma else (gbps / PEAK_HBM_GBPS), 4)}
+        if config == 4:  # MTP verify also reports its matrix-unit rate
+            r["mfma_TFLOPs"] = round(tflops, 1)
+            r["mfma_frac"] = round(tflops / PEAK_BF16_TFLOPS, 4)
+        return r
+
+    return {
+        "metric": f"{SIDE_NAMES[config]}, us per layer (pack + plan + append + split attention + combine)",
+        "workload": f"BASELINE config {config}" + (" on an FP8 pool" if kv == "fp8" and config != 5 else ""),
+        "dtype": "fp8-e4m3 KV, bf16 Q" if fp8 else "bf16", "rows": rows, "sequences": b.n_seqs,
+        "sum_ctx": int(b.ctx.sum()), "bytes_per_layer": nbytes, "flops_per_layer": flops,
+        "step_us": round(us, 3), "step_roofline": roof(us),
+        "kernel_us": round(kus, 3), "kernel_roofline": roof(kus),
+        "kernel": ("append_kernel + " if fp8 else "") +
+                  ("wide_kernel (prefill)" if mfma else "attention_kernel (decode, fused append)"
+                   if not fp8 else "attention_kernel (decode)"),
+    }
+
+
+def side_config(args):
+    """bench.py --config 3|4|5: the side measurement of that configuration on its own JSON line."""
+    r = side_measure(args.config, args.seed, args.steps, args.warmup, args.kernel_reps, args.kv)
+    log(f"config {args.config}: step {r['step_us']:.2f} us, attention {r['kernel_us']:.2f} us")
     print(json.dumps({
-        "metric": f"{names[args.config]}, us per layer (pack + plan + append + split attention + combine)",
-        "value": round(us, 3), "unit": "us", "higher_is_better": False, "n_gpus": 1,
-        "steps": args.steps, "warmup": args.warmup, "dtype": "fp8-e4m3 KV, bf16 Q" if fp8 else "bf16",
+        "metric": r["metric"], "value": r["step_us"], "unit": "us", "higher_is_better": False,
+        "n_gpus": 1, "steps": args.steps, "warmup": args.warmup, "dtype": r["dtype"],
         "data": "synthetic (seeded, resident in HBM)",
-        "config": {"workload": f"BASELINE config {args.config}" + (" on an FP8 pool" if args.kv == "fp8" and args.config != 5 else ""), "rows": rows,
-                   "sequences": b.n_seqs, "sum_ctx": int(b.ctx.sum())},
-        "roofline": {"bound": "mfma" if mfma else "hbm",
-                     "achieved": round(tflops if mfma else gbps, 1),
-                     "peak": PEAK_BF16_TFLOPS if mfma else PEAK_HBM_GBPS,
-                     "unit": "TFLOP/s" if mfma else "GB/s",
-                     "frac": round((tflops / PEAK_BF16_TFLOPS) if mfma else (gbps / PEAK_HBM_GBPS), 4),
-                     "bytes_per_layer": nbytes, "flops_per_layer": flops},
+        "config": {"workload": r["workload"], "rows": r["rows"], "sequences": r["sequences"],
+                   "sum_ctx": r["sum_ctx"]},
+        "roofline": dict(r["step_roofline"], bytes_per_layer=r["bytes_per_layer"],
+                         flops_per_layer=r["flops_per_layer"]),
+        "kernel": {"name": r["kernel"], "us": r["kernel_us"], "roofline": r["kernel_roofline"]},
     }), flush=True)
 
 
@@ -216,6 +253,22 @@ def read_ceiling(lia, layer_bytes, L, reps):
             "kernel": "hbm_read_kernel (lia_hbm_read: contiguous, 16-byte non-temporal loads)"}
 
 
+def host_cpus():
+    """The host's CPU count as this process sees it (its affinity set: the cores the job may
+    run on), the machine's count, the OpenMP thread setting of the environment and the model."""
+    model = None
+    try:
+        with open("/proc/cpuinfo") as f:
+            for line in f:
+                if line.startswith("model name"):
+                    model = line.split(":", 1)[1].strip()
+                    break
+    except OSError:
+        pass
+    return {"nproc": len(os.sched_getaffinity(0)), "machine_cpus": os.cpu_count(),
+            "omp_num_threads_env": os.environ.get("OMP_NUM_THREADS"), "cpu_model": model}
+
+
 def cpu_baseline(args, b, g, kpool, vpool, q, layer_bytes, L):
     """The oracle's scalar split-K + merge (kernels/llama.rs:63-159, 201-290) on one layer of
     the batch, compiled here at -O3 -march=native with OpenMP over (row, head, split): one
@@ -241,7 +294,7 @@ def cpu_baseline(args, b, g, kpool, vpool, q, layer_bytes, L):
     per_layer = float(np.median(times))
     threads = int(blib.lo_omp_threads())
     return {"value": round(b.n_rows / (per_layer * L), 4), "unit": "tokens/s",
-            "cores": threads, "kind": "port",
+            "cores": threads, "kind": "port", **host_cpus(),
             "sample": f"median of {len(times)} runs (after 1 warm-up) of one layer of the config-2 "
                       f"batch (8 rows, sum ctx {int(b.ctx.sum())}) in f32 split-K (span 256) + merge, "
                       f"gcc -O3 -march=native, OpenMP {threads} threads, scaled to {L} layers; "
@@ -375,6 +428,17 @@ def main():
         cpu = cpu_baseline(args, b, g, kpool[0], vpool[0], qs[0], layer_bytes, L)
         log(f"cpu baseline: {cpu}")
 
+    # ---- one-layer steps of configs 3, 4 and 5 (parity workloads, timed for the record)
+    side = {}
+    if not args.no_side:
+        del kpool, vpool, qs, newk, newv
+        torch.cuda.empty_cache()
+        for c in (3, 4, 5):
+            side["config%d" % c] = side_measure(c, args.seed, args.side_steps, 3, 10)
+            torch.cuda.empty_cache()
+            log(f"config {c}: step {side['config%d' % c]['step_us']:.2f} us, attention "
+                f"{side['config%d' % c]['kernel_us']:.2f} us")
+
     out = {
         "metric": METRIC,
         "value": round(b.n_rows / (ms_step * 1e-3), 2),
@@ -407,6 +471,7 @@ def main():
             "read_ceiling": dict(ceiling, kernel_frac_of_ceiling=round(achieved / ceiling["GBps"], 4)),
         },
         "cpu_baseline": cpu,
+        "side": side or None,
     }
     print(json.dumps(out), flush=True)
 
