@@ -358,6 +358,12 @@ int lia_attention_partial_append(const lia_attention_config *config, uint32_t n_
  * argument is checked before either is issued).  Other pool types return LIA_E_UNSUPPORTED
  * (and lia_attention_partial_append returns it for FP8 pools).  No counterpart in the
  * reference, whose KV cache is f16 only.
+ * Ranges on FP8 pools (every attention entry point): the kernels multiply e4m3 codes, converted
+ * exactly to f16, by f16 softmax weights of at most 2^8 times the page's V scale, so V page
+ * scales must stay below 256 (a V amax below about 114,000; amax/448 is the quantiser's scale)
+ * for the weights to stay finite, and weights of pages whose scale is below about 2^-14 lose
+ * precision as f16 subnormals.  Queries are rounded to f16 on FP8 pools: |q| above 65504 becomes
+ * infinite.  16-bit pools keep bf16 queries and weights and have neither limit.
  */
 int lia_attention_partial_append_fp8(const lia_attention_config *config, uint32_t n_seqs,
                                      uint32_t n_rows, const uint32_t *pages,
