@@ -166,8 +166,10 @@ constexpr uint32_t kUnitCostWide = 8, kUnitCostDecode = 4;
 // Weight lag (of 256) of the workgroups that share a CU with an older one.  Measured per
 // workgroup on the prefill kernel (two per CU): with equal shares the CU's first workgroup
 // finished in 183 us and the second in 216 us, the older waves being issued first.  Lag 56
-// (22 %) gave the best step (lags 24-96 measured); the decode kernels lose with any lag
-// (HBM-bound: the order of issue does not change their rate).
+// (22 %) gave the best step (lags 24-96 measured).  The decode kernel loses with any lag (16-64
+// measured 1.5-2.5 % slower on config 2): its first-round workgroups do finish earlier, but more
+// blocks for them leave the other rounds' end unchanged, since the chip's aggregate rate while
+// every workgroup runs is the cap.
 constexpr uint32_t kLagWide = 56, kLagDecode = 0;
 
 // The plan for up to kPlanSeqs sequences, one thread each (kPlanThreads): per-sequence extents
