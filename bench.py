@@ -4,8 +4,9 @@ Workload: ragged bf16 decode, batch 8, contexts U[1024,
 (seeded), 16 query / 2 KV heads, head_dim 128, 16-token pages scattered by a seeded
 permutation, N(0,1) data, 40 layers as independent KV slices.
 
-One step = device packing of the batch (cu_seqlens, positions, slot mapping), the work
-plan, then per layer: the split attention kernel with the KV append of the 8 new tokens
+One step = device packing of the batch (cu_seqlens, positions, slot mapping) and the work
+plan (lia_pack_plan_device: the plan runs beside the packing, then the table checks), then per
+layer: the split attention kernel with the KV append of the 8 new tokens
 fused in (lia_attention_partial_append: the new keys are read from the step's rows and
 scattered into the pool by the same launch) and the split combine.  The step is captured once as a HIP graph and replayed (the reference
 replays CUDA graphs of the paged forward, src/inference/paging.rs:238-259).
@@ -132,9 +133,8 @@ def side_measure(config, seed, steps, warmup, reps, kv=None):
             lia.attention_partial_append(cfg, b.n_seqs, flat, slots, q, newk, newv, kp, vp, out, ws)
 
     def step():
-        lia.pack_device(seq_slots, q_lens, cached, flat, b.stride, P, b.pool_pages, context, rows,
-                        cu, positions, sequences, slots, status)
-        lia.attention_plan(cfg, b.n_seqs, rows, cu, positions, sequences, ws, pages=flat)
+        lia.pack_plan_device(cfg, seq_slots, q_lens, cached, flat, rows, context, cu, positions,
+                             sequences, slots, status, ws)
         attend()
         lia.attention_merge(cfg, b.n_seqs, rows, out, ws)
 
@@ -353,9 +353,8 @@ def main():
     torch.cuda.synchronize()
 
     def step():
-        lia.pack_device(seq_slots, q_lens, cached, flat, b.stride, P, b.pool_pages, context, rows,
-                        cu, positions, sequences, slots, status)
-        lia.attention_plan(cfg, b.n_seqs, rows, cu, positions, sequences, ws, pages=flat)
+        lia.pack_plan_device(cfg, seq_slots, q_lens, cached, flat, rows, context, cu, positions,
+                             sequences, slots, status, ws)
         for layer in range(L):
             lia.attention_partial_append(cfg, b.n_seqs, flat, slots, qs[layer], newk[layer],
                                          newv[layer], kpool[layer], vpool[layer], outs[layer], ws)
@@ -455,8 +454,8 @@ def main():
         "config": {
             "workload": "BASELINE config 2: ragged bf16 paged decode, batch 8, ctx U[1024,32768] "
                         "seed %d, 16q/2kv heads, head_dim 128, page 16, %d layers as independent "
-                        "KV slices; step = device pack + plan + per layer (split attention with "
-                        "the KV append fused in + combine), HIP-graph replay" % (args.seed, L),
+                        "KV slices; step = device pack and plan (two launches) + per layer (split attention "
+                        "with the KV append fused in + combine), HIP-graph replay" % (args.seed, L),
             "batch": b.n_seqs, "layers": L, "ctx": b.ctx.tolist(), "sum_ctx": int(b.ctx.sum()),
             "page_size": P, "pool_pages": b.pool_pages,
             "step_hbm_GBps": round(step_gbps, 1),

@@ -323,6 +323,23 @@ int lia_attention_plan(const lia_attention_config *config, uint32_t n_seqs, uint
                        const uint32_t *cu_seqlens, const uint32_t *positions,
                        const uint32_t *sequences, const uint32_t *pages, void *workspace,
                        size_t workspace_bytes, lia_stream_t stream);
+/*
+ * lia_pack_device followed by lia_attention_plan (with pages) on one workspace, in two launches
+ * instead of three: the plan is built from the packing's inputs (seq_slots, q_lens, cached) by
+ * workgroups that run beside the packing workgroup, then the table checks run.  The metadata,
+ * status and plan afterwards are those of the two calls, with the config's stride, page_size,
+ * pool_pages and max_rows as the packing's.  A rejected step (status != 0) is marked in the
+ * workspace, and the attention and merge entry points then read and write nothing for it, as
+ * they would on the empty plan of a rejected packing.  n_rows must equal the sum of q_lens;
+ * otherwise nothing is scheduled.  Batches of more than 1024 sequences take the three launches.
+ * No counterpart in the reference, which packs on the host (paging.rs:118-201).
+ */
+int lia_pack_plan_device(const lia_attention_config *config, uint32_t n_seqs, uint32_t n_rows,
+                         const uint32_t *seq_slots, const uint32_t *q_lens, const uint32_t *cached,
+                         const uint32_t *pages, uint32_t context, uint32_t *cu_seqlens,
+                         uint32_t *positions, uint32_t *sequences, uint32_t *slot_mapping,
+                         uint32_t *status, void *workspace, size_t workspace_bytes,
+                         lia_stream_t stream);
 int lia_attention_partial(const lia_attention_config *config, uint32_t n_seqs, uint32_t n_rows,
                           const uint32_t *pages, const void *q, const void *kc, const void *vc,
                           const float *k_scales, const float *v_scales, void *workspace,

@@ -125,6 +125,10 @@ EXPORTS = {
                                   C.c_uint32, C.c_uint32, C.c_uint32, C.c_uint32, C.c_uint32,
                                   C.c_void_p, C.c_void_p, C.c_void_p, C.c_void_p, C.c_void_p,
                                   C.c_void_p]),
+    "lia_pack_plan_device": (C.c_int, [C.POINTER(AttentionConfig), C.c_uint32, C.c_uint32,
+                                       C.c_void_p, C.c_void_p, C.c_void_p, C.c_void_p, C.c_uint32,
+                                       C.c_void_p, C.c_void_p, C.c_void_p, C.c_void_p, C.c_void_p,
+                                       C.c_void_p, C.c_size_t, C.c_void_p]),
     "lia_kv_append": (C.c_int, [C.POINTER(KVLayout), C.c_uint32, C.c_void_p, C.c_void_p,
                                 C.c_void_p, C.c_uint32, C.c_void_p, C.c_int32, C.c_void_p,
                                 C.c_void_p, C.c_void_p, C.c_void_p, C.c_void_p, C.c_void_p,
@@ -315,6 +319,17 @@ def pack_device(seq_slots, q_lens, cached, pages, stride, page_size, pool_pages,
                                _dptr(cu_seqlens), _dptr(positions), _dptr(sequences),
                                _dptr(slot_mapping), _dptr(status), _stream(stream))
     _check(st, "pack_device")
+
+
+def pack_plan_device(config, seq_slots, q_lens, cached, pages, n_rows, context, cu_seqlens,
+                     positions, sequences, slot_mapping, status, workspace, stream=None):
+    """Device packing and the attention plan in two launches (lia_pack_plan_device)."""
+    st = lib().lia_pack_plan_device(C.byref(config), seq_slots.numel(), n_rows, _dptr(seq_slots),
+                                    _dptr(q_lens), _dptr(cached), _dptr(pages), context,
+                                    _dptr(cu_seqlens), _dptr(positions), _dptr(sequences),
+                                    _dptr(slot_mapping), _dptr(status), _dptr(workspace),
+                                    workspace.numel() * workspace.element_size(), _stream(stream))
+    _check(st, "pack_plan_device")
 
 
 def kv_append(layout, k, v, kc, vc, positions=None, sequences=None, pages=None, stride=0,

@@ -33,6 +33,7 @@
 
 #include "common.hpp"
 #include "launch.hpp"
+#include "pack.hpp"
 
 namespace lia {
 
@@ -73,6 +74,12 @@ struct MergeDesc {
     uint32_t rowbeg;      // as in UnitDesc
     uint32_t nrows_hk;
 };
+
+// Word of the workspace header holding the step's verdict: 0, or the failure (a positive
+// lia_status) of the packing that lia_pack_plan_device ran beside the plan, whose table checks
+// then empty the plan (every work range and merge descriptor), so the attention and combine
+// kernels do nothing for a rejected step.
+constexpr uint32_t kVerdict = 4;
 
 struct AttnParams {
     const void *q;
@@ -178,16 +185,27 @@ constexpr uint32_t kLagWide = 56, kLagDecode = 0;
 // descriptors and the work list are each written in parallel with no serial per-sequence loop
 // and no reads of the units just written.  Workgroups get shares of cost - the blocks plus
 // unit_cost per unit (its start) - equal, or weighted by dispatch round (round_wg, lag).
+//
+// Per-sequence extents come from the packed metadata (cu_seqlens, positions, sequences), or,
+// with `raw` set, from the packing's own inputs (raw->q_lens, cached, seq_slots), so the plan
+// can run beside the packing in one launch; a raw batch whose rows differ from raw->n_rows is
+// planned empty.  The workgroup is `grp` of `ngrp` sharing the descriptor loops.
+struct RawSeqs {
+    const uint32_t *q_lens, *cached, *seq_slots;
+    uint32_t n_rows;
+};
+
 __device__ void plan_lds(uint32_t n_seqs, const uint32_t *cu, const uint32_t *positions,
-                         const uint32_t *sequences, const uint32_t *pages, uint32_t stride,
-                         uint32_t page_shift, uint32_t rpc, uint32_t hkv, uint32_t max_units,
-                         uint32_t n_wg, uint32_t unit_cost, uint32_t round_wg, uint32_t lag,
-                         uint32_t xcd, UnitDesc *units, WorkDesc *work, MergeDesc *merge,
-                         uint32_t *header) {
+                         const uint32_t *sequences, const RawSeqs *raw, const uint32_t *pages,
+                         uint32_t stride, uint32_t page_shift, uint32_t rpc, uint32_t hkv,
+                         uint32_t max_units, uint32_t n_wg, uint32_t unit_cost, uint32_t round_wg,
+                         uint32_t lag, uint32_t xcd, uint32_t grp, uint32_t ngrp, UnitDesc *units,
+                         WorkDesc *work, MergeDesc *merge, uint32_t *header) {
     __shared__ uint32_t s_r0[kPlanSeqs], s_nr[kPlanSeqs], s_p0[kPlanSeqs], s_trow[kPlanSeqs];
     __shared__ uint32_t s_u0[kPlanSeqs + 1], s_b0[kPlanSeqs + 1], s_c0[kPlanSeqs + 1];
     __shared__ uint32_t w_a[kPlanThreads / 64], w_b[kPlanThreads / 64];
-    __shared__ uint32_t carry_units, carry_blocks;
+    __shared__ uint32_t w_r[kPlanThreads / 64], w_z[kPlanThreads / 64];
+    __shared__ uint32_t carry_units, carry_blocks, carry_rows, raw_bad;
     __shared__ uint64_t s_rlo[kPlanThreads + 1];
     // Threads exchange only LDS data (nothing written to global memory is read back), so the
     // barriers need not wait for the descriptor stores in flight.
@@ -195,16 +213,32 @@ __device__ void plan_lds(uint32_t n_seqs, const uint32_t *cu, const uint32_t *po
     const uint32_t t = threadIdx.x;
     // the workgroups of the launch share the descriptor loops; each computes the per-sequence
     // extents and range starts itself (they live in its LDS)
-    const uint32_t g0 = t * gridDim.x + blockIdx.x, GT = gridDim.x * T; // interleaved shares
+    const uint32_t g0 = t * ngrp + grp, GT = ngrp * T; // interleaved shares
     {
         const uint32_t b = t;
         uint32_t nu = 0, nb = 0, r0 = 0, nr = 0, p0 = 0, trow = 0;
+        if (raw) {
+            // rows of the batch: an exclusive scan of the new-token counts.  The packing beside
+            // this plan has not validated them: a sequence whose keys pass its table row (which
+            // the packing rejects) plans nothing, so no table read leaves the row.
+            nr = b < n_seqs ? raw->q_lens[b] : 0u;
+            p0 = b < n_seqs ? raw->cached[b] : 0u;
+            trow = b < n_seqs ? raw->seq_slots[b] : 0u;
+            uint32_t sr = nr, sbad = (uint64_t)p0 + nr > ((uint64_t)stride << page_shift) ? 1u : 0u;
+            block_scan2(sr, sbad, w_r, w_z); // rows before this sequence, and the bad ones
+            r0 = sr - nr;
+            if (t == T - 1) { carry_rows = sr; raw_bad = sbad; }
+        }
         if (b < n_seqs) {
-            r0 = cu[b];
-            nr = cu[b + 1] - r0;
+            if (!raw) {
+                r0 = cu[b];
+                nr = cu[b + 1] - r0;
+            }
             if (nr > 0) {
-                p0 = positions[r0];
-                trow = sequences[r0];
+                if (!raw) {
+                    p0 = positions[r0];
+                    trow = sequences[r0];
+                }
                 const uint32_t ncb = (nr + rpc - 1) / rpc;
                 nu = ncb * hkv;
                 nb = (ncb * ((p0 + 31) / 32) + new_blocks_before(ncb - 1, rpc) + (nr + 31) / 32) * hkv;
@@ -221,19 +255,22 @@ __device__ void plan_lds(uint32_t n_seqs, const uint32_t *cu, const uint32_t *po
         if (t == T - 1) { carry_units = su; carry_blocks = sb; }
         lds_barrier();
     }
-    const bool overflow = carry_units > max_units;
+    const bool overflow = carry_units > max_units || (raw && (carry_rows != raw->n_rows || raw_bad));
     const uint32_t U = overflow ? 0 : carry_units, B = overflow ? 0 : carry_blocks;
     const uint32_t N = min(n_wg, B);
     if (t == 0) {
         s_u0[n_seqs] = carry_units;
         s_b0[n_seqs] = carry_blocks;
         s_c0[n_seqs] = carry_blocks + unit_cost * carry_units;
-        if (blockIdx.x == 0) {
+        if (grp == 0) {
             units[U] = UnitDesc{B, 0, 0, 0, 0, 0, 0, 0};
             header[0] = U;
             header[1] = B;
             header[2] = N;
             header[3] = overflow;
+            // the batch verdict: a plan of packed metadata is never of a rejected batch (its
+            // rejection empties cu_seqlens); the packing beside a raw plan writes it instead
+            if (!raw) header[kVerdict] = 0;
         }
     }
     lds_barrier();
@@ -344,7 +381,9 @@ __device__ void plan_lds(uint32_t n_seqs, const uint32_t *cu, const uint32_t *po
         return s_b0[b] + h * nbh + ustart + (off < unit_cost ? 0u : off - unit_cost);
     };
     // One work descriptor per thread and pass (unconditional page-table loads: an entry not
-    // needed reads cu[0] and is replaced by 0).
+    // needed reads a word the plan reads anyway - cu[0], or q_lens[0] of a raw plan, whose
+    // cu is null - and is replaced by 0).
+    const uint32_t *dummy = raw ? raw->q_lens : cu;
     for (uint32_t w0 = g0; w0 < N; w0 += GT) {
         WorkDesc d[1];
         uint32_t v[1][kPrePages];
@@ -370,7 +409,7 @@ __device__ void plan_lds(uint32_t n_seqs, const uint32_t *cu, const uint32_t *po
 #pragma unroll
             for (uint32_t i = 0; i < kPrePages; i++) {
                 const bool use = pre && lp + i < lend;
-                const uint32_t *src = use ? pages + (size_t)d[k].first.table_row * stride + lp + i : cu;
+                const uint32_t *src = use ? pages + (size_t)d[k].first.table_row * stride + lp + i : dummy;
                 v[k][i] = *src;
                 v[k][i] = use ? v[k][i] : 0u;
             }
@@ -386,8 +425,50 @@ __global__ __launch_bounds__(kPlanThreads) void plan_lds_kernel(
     const uint32_t *pages, uint32_t stride, uint32_t page_shift, uint32_t rpc, uint32_t hkv,
     uint32_t max_units, uint32_t n_wg, uint32_t unit_cost, uint32_t round_wg, uint32_t lag,
     uint32_t xcd, UnitDesc *units, WorkDesc *work, MergeDesc *merge, uint32_t *header) {
-    plan_lds(n_seqs, cu, positions, sequences, pages, stride, page_shift, rpc, hkv, max_units, n_wg,
-             unit_cost, round_wg, lag, xcd, units, work, merge, header);
+    plan_lds(n_seqs, cu, positions, sequences, nullptr, pages, stride, page_shift, rpc, hkv, max_units,
+             n_wg, unit_cost, round_wg, lag, xcd, blockIdx.x, gridDim.x, units, work, merge, header);
+}
+
+struct PackArgs {
+    const uint32_t *seq_slots, *q_lens, *cached, *pages;
+    uint32_t stride, page_shift, pool_pages, context, max_rows;
+    uint32_t *cu, *positions, *sequences, *slot_mapping, *status;
+};
+
+// lia_pack_plan_device's second launch: table_check_kernel (kv.hip), with the verdict raised
+// too, and a rejected step's plan emptied - by every workgroup that sees the failure (the
+// packing's, read from the verdict the first launch wrote, or its own table checks): the
+// empty descriptors are the same whoever writes them.
+__global__ __launch_bounds__(kCheckThreads) void verdict_check_kernel(uint32_t n_seqs, PackArgs pk,
+                                                                      uint32_t *header, WorkDesc *work,
+                                                                      uint32_t n_wg, MergeDesc *merge,
+                                                                      uint32_t max_units) {
+    const bool packing_failed = header[kVerdict] != 0; // final: written by the previous launch
+    const bool found = table_check_block(blockIdx.x, gridDim.x, n_seqs, pk.seq_slots, pk.q_lens,
+                                         pk.cached, pk.pages, pk.stride, pk.page_shift, pk.pool_pages,
+                                         pk.context, pk.max_rows, pk.cu, pk.slot_mapping, pk.status,
+                                         header + kVerdict);
+    if (!found && !(packing_failed && blockIdx.x == 0)) return;
+    for (uint32_t w = threadIdx.x; w < n_wg; w += kCheckThreads) work[w] = WorkDesc{};
+    for (uint32_t u = threadIdx.x; u < max_units; u += kCheckThreads) merge[u] = MergeDesc{0, 0, 0, 0};
+}
+
+// lia_pack_plan_device's first launch: workgroups 0 .. kPlanGroups-1 plan the step from the
+// packing's inputs while workgroup kPlanGroups packs it (one 1024-thread workgroup each); the
+// packing's status is copied to the header's verdict word.
+
+__global__ __launch_bounds__(kPlanThreads) void pack_plan_kernel(
+    uint32_t n_seqs, PackArgs pk, RawSeqs raw, uint32_t rpc, uint32_t hkv, uint32_t max_units,
+    uint32_t n_wg, uint32_t unit_cost, uint32_t round_wg, uint32_t lag, uint32_t xcd, UnitDesc *units,
+    WorkDesc *work, MergeDesc *merge, uint32_t *header) {
+    if (blockIdx.x < kPlanGroups)
+        plan_lds(n_seqs, nullptr, nullptr, nullptr, &raw, pk.pages, pk.stride, pk.page_shift, rpc, hkv,
+                 max_units, n_wg, unit_cost, round_wg, lag, xcd, blockIdx.x, kPlanGroups, units, work,
+                 merge, header);
+    else
+        pack_rows_block(n_seqs, pk.seq_slots, pk.q_lens, pk.cached, pk.pages, pk.stride, pk.page_shift,
+                        pk.pool_pages, pk.context, pk.max_rows, pk.cu, pk.positions, pk.sequences,
+                        pk.slot_mapping, pk.status, header + kVerdict);
 }
 
 // The plan for more sequences than plan_lds_kernel holds: units written by a serial walk of
@@ -461,6 +542,7 @@ __global__ __launch_bounds__(256) void plan_kernel(uint32_t n_seqs, const uint32
         header[1] = B;
         header[2] = N;
         header[3] = overflow;
+        header[kVerdict] = 0;
     }
     __threadfence();
     __syncthreads();
@@ -2522,7 +2604,8 @@ static int run_stages(int stages, const lia_attention_config *c, uint32_t n_seqs
                       const uint32_t *sequences, const uint32_t *pages, const void *q,
                       const void *kc, const void *vc, const float *k_scales,
                       const float *v_scales, void *workspace, size_t workspace_bytes, void *out,
-                      lia_stream_t stream, const FusedAppend *fa = nullptr, bool enqueue = true) {
+                      lia_stream_t stream, const FusedAppend *fa = nullptr, bool enqueue = true,
+                      const PackArgs *pk = nullptr) {
     int st = validate(c);
     if (st) return st;
     if (n_seqs == 0 || n_seqs > c->max_seqs || n_rows == 0 || n_rows > c->max_rows) return LIA_E_ARG;
@@ -2594,17 +2677,38 @@ static int run_stages(int stages, const lia_attention_config *c, uint32_t n_seqs
         // Measured: launch order makes config 2 1.1 % faster and the config-3 step 2 us shorter;
         // XCD-major keeps config 5 2 us shorter.
         const uint32_t xcd = c->kv_dtype == LIA_FP8_E4M3 && NT != kWideNT;
-        if (n_seqs <= kPlanSeqs && n_wg <= kPlanThreads)
+        const uint32_t cost = NT == kWideNT ? kUnitCostWide : kUnitCostDecode;
+        const uint32_t lag = NT == kWideNT ? kLagWide : kLagDecode;
+        if (pk && n_seqs <= kPlanSeqs && n_wg <= kPlanThreads) {
+            // the packing and the plan in one launch (the plan from the packing's inputs), then
+            // the table checks, which also raise the verdict the attention kernels read
+            const RawSeqs raw{pk->q_lens, pk->cached, pk->seq_slots, n_rows};
+            e = launch<pack_plan_kernel>(dim3(kPlanGroups + 1), dim3(kPlanThreads), 0, s, n_seqs, *pk,
+                                         raw, rpc, c->num_kv_heads, L.max_units, n_wg, cost,
+                                         lia_device_cus(), lag, xcd, units, work, merge, header);
+            if (e == hipSuccess)
+                e = launch<verdict_check_kernel>(dim3(kCheckGroups), dim3(kCheckThreads), 0, s, n_seqs,
+                                                 *pk, header, work, n_wg, merge, L.max_units);
+        } else {
+            if (pk) { // too many sequences or workgroups for the one-launch form: pack first
+                const int ps = lia_pack_device(n_seqs, pk->seq_slots, pk->q_lens, pk->cached, pk->pages,
+                                               pk->stride, 1u << pk->page_shift, pk->pool_pages,
+                                               pk->context, pk->max_rows, pk->cu, pk->positions,
+                                               pk->sequences, pk->slot_mapping, pk->status, stream);
+                if (ps) return ps;
+            }
+            if (n_seqs <= kPlanSeqs && n_wg <= kPlanThreads)
             e = launch<plan_lds_kernel>(dim3(kPlanGroups), dim3(kPlanThreads), 0, s, n_seqs, cu_seqlens,
                                         positions, sequences, pages, c->stride, p.page_shift, rpc,
                                         c->num_kv_heads, L.max_units, n_wg,
                                         NT == kWideNT ? kUnitCostWide : kUnitCostDecode,
                                         lia_device_cus(), NT == kWideNT ? kLagWide : kLagDecode,
                                         xcd, units, work, merge, header);
-        else
+            else
             e = launch<plan_kernel>(dim3(1), dim3(256), 0, s, n_seqs, cu_seqlens, positions,
                                     sequences, pages, c->stride, p.page_shift, rpc, c->num_kv_heads,
                                     L.max_units, n_wg, xcd, units, work, merge, header);
+        }
     }
     if (e == hipSuccess && (stages & kPartial)) {
         if (c->head_dim == 128) {
@@ -2681,6 +2785,28 @@ extern "C" int lia_attention_plan(const lia_attention_config *c, uint32_t n_seqs
     return run_stages(kPlan, c, n_seqs, n_rows, cu_seqlens, positions, sequences, pages,
                       nullptr, nullptr, nullptr, nullptr, nullptr, workspace, workspace_bytes,
                       nullptr, stream);
+}
+
+extern "C" int lia_pack_plan_device(const lia_attention_config *c, uint32_t n_seqs, uint32_t n_rows,
+                                    const uint32_t *seq_slots, const uint32_t *q_lens,
+                                    const uint32_t *cached, const uint32_t *pages, uint32_t context,
+                                    uint32_t *cu_seqlens, uint32_t *positions, uint32_t *sequences,
+                                    uint32_t *slot_mapping, uint32_t *status, void *workspace,
+                                    size_t workspace_bytes, lia_stream_t stream) {
+    if (!c || !seq_slots || !q_lens || !cached || !pages || !cu_seqlens || !positions || !sequences ||
+        !slot_mapping || !status)
+        return LIA_E_ARG;
+    // every check of the plan stage before anything is enqueued
+    int st = run_stages(kPlan, c, n_seqs, n_rows, cu_seqlens, positions, sequences, pages, nullptr,
+                        nullptr, nullptr, nullptr, nullptr, workspace, workspace_bytes, nullptr, stream,
+                        nullptr, false);
+    if (st) return st;
+    const PackArgs pk{seq_slots, q_lens, cached, pages, c->stride, (uint32_t)__builtin_ctz(c->page_size),
+                      c->pool_pages, context, c->max_rows, cu_seqlens, positions, sequences,
+                      slot_mapping, status};
+    return run_stages(kPlan, c, n_seqs, n_rows, cu_seqlens, positions, sequences, pages, nullptr,
+                      nullptr, nullptr, nullptr, nullptr, workspace, workspace_bytes, nullptr, stream,
+                      nullptr, true, &pk);
 }
 
 extern "C" int lia_attention_partial(const lia_attention_config *c, uint32_t n_seqs,
