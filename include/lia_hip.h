@@ -325,8 +325,8 @@ int lia_attention_plan(const lia_attention_config *config, uint32_t n_seqs, uint
                        size_t workspace_bytes, lia_stream_t stream);
 /*
  * lia_pack_device followed by lia_attention_plan (with pages) on one workspace, in two launches
- * instead of three: the plan is built from the packing's inputs (seq_slots, q_lens, cached) by
- * workgroups that run beside the packing workgroup, then the table checks run.  The metadata,
+ * instead of three: the packing, the table checks and the plan - built from the packing's inputs
+ * (seq_slots, q_lens, cached) - run side by side, then one small launch settles the status.  The metadata,
  * status and plan afterwards are those of the two calls, with the config's stride, page_size,
  * pool_pages and max_rows as the packing's.  A rejected step (status != 0) is marked in the
  * workspace, and the attention and merge entry points then read and write nothing for it, as

@@ -435,40 +435,64 @@ struct PackArgs {
     uint32_t *cu, *positions, *sequences, *slot_mapping, *status;
 };
 
-// lia_pack_plan_device's second launch: table_check_kernel (kv.hip), with the verdict raised
-// too, and a rejected step's plan emptied - by every workgroup that sees the failure (the
-// packing's, read from the verdict the first launch wrote, or its own table checks): the
-// empty descriptors are the same whoever writes them.
-__global__ __launch_bounds__(kCheckThreads) void verdict_check_kernel(uint32_t n_seqs, PackArgs pk,
-                                                                      uint32_t *header, WorkDesc *work,
-                                                                      uint32_t n_wg, MergeDesc *merge,
-                                                                      uint32_t max_units) {
-    const bool packing_failed = header[kVerdict] != 0; // final: written by the previous launch
-    const bool found = table_check_block(blockIdx.x, gridDim.x, n_seqs, pk.seq_slots, pk.q_lens,
-                                         pk.cached, pk.pages, pk.stride, pk.page_shift, pk.pool_pages,
-                                         pk.context, pk.max_rows, pk.cu, pk.slot_mapping, pk.status,
-                                         header + kVerdict);
-    if (!found && !(packing_failed && blockIdx.x == 0)) return;
-    for (uint32_t w = threadIdx.x; w < n_wg; w += kCheckThreads) work[w] = WorkDesc{};
-    for (uint32_t u = threadIdx.x; u < max_units; u += kCheckThreads) merge[u] = MergeDesc{0, 0, 0, 0};
-}
+// Workgroups of lia_pack_plan_device's first launch that check the block tables (1024 threads
+// each, as many threads as table_check_kernel's 64 x 256); each writes its failure bits to
+// header[kFoundWords + its index] on every call, so no word needs clearing first.
+constexpr uint32_t kSetupChecks = 16, kFoundWords = 16;
 
-// lia_pack_plan_device's first launch: workgroups 0 .. kPlanGroups-1 plan the step from the
-// packing's inputs while workgroup kPlanGroups packs it (one 1024-thread workgroup each); the
-// packing's status is copied to the header's verdict word.
-
+// lia_pack_plan_device's first launch (1024-thread workgroups): 0 .. kPlanGroups-1 plan the step
+// from the packing's inputs, kPlanGroups packs it (its status also to the header's verdict
+// word), and the kSetupChecks after it check the block tables.
 __global__ __launch_bounds__(kPlanThreads) void pack_plan_kernel(
     uint32_t n_seqs, PackArgs pk, RawSeqs raw, uint32_t rpc, uint32_t hkv, uint32_t max_units,
     uint32_t n_wg, uint32_t unit_cost, uint32_t round_wg, uint32_t lag, uint32_t xcd, UnitDesc *units,
     WorkDesc *work, MergeDesc *merge, uint32_t *header) {
-    if (blockIdx.x < kPlanGroups)
+    const uint32_t bid = blockIdx.x;
+    if (bid < kPlanGroups) {
         plan_lds(n_seqs, nullptr, nullptr, nullptr, &raw, pk.pages, pk.stride, pk.page_shift, rpc, hkv,
-                 max_units, n_wg, unit_cost, round_wg, lag, xcd, blockIdx.x, kPlanGroups, units, work,
-                 merge, header);
-    else
+                 max_units, n_wg, unit_cost, round_wg, lag, xcd, bid, kPlanGroups, units, work, merge,
+                 header);
+    } else if (bid == kPlanGroups) {
         pack_rows_block(n_seqs, pk.seq_slots, pk.q_lens, pk.cached, pk.pages, pk.stride, pk.page_shift,
                         pk.pool_pages, pk.context, pk.max_rows, pk.cu, pk.positions, pk.sequences,
                         pk.slot_mapping, pk.status, header + kVerdict);
+    } else {
+        const uint32_t grp = bid - kPlanGroups - 1;
+        const uint32_t found = table_check_scan<kPlanThreads>(grp, kSetupChecks, n_seqs, pk.seq_slots,
+                                                              pk.q_lens, pk.cached, pk.pages, pk.stride,
+                                                              pk.page_shift, pk.pool_pages, pk.context);
+        if (threadIdx.x == 0) header[kFoundWords + grp] = found;
+    }
+}
+
+// lia_pack_plan_device's second launch (one workgroup): the step's status from the packing's
+// (header[kVerdict]) and the table checks' bits, in the reference's order of checks (the row
+// count, then the tables, then the rows: paging.rs:120-172), written to status and to the
+// verdict word.  A table failure rejects the rows as the packing rejects its own; any failure
+// empties the plan, so the attention and combine kernels do nothing for the step.
+__global__ __launch_bounds__(kPlanThreads) void setup_verdict_kernel(
+    uint32_t n_seqs, uint32_t max_rows, uint32_t *cu, uint32_t *slot_mapping, uint32_t *status,
+    uint32_t *header, WorkDesc *work, uint32_t n_wg, MergeDesc *merge, uint32_t max_units) {
+    const uint32_t t = threadIdx.x;
+    const uint32_t packing = header[kVerdict];
+    uint32_t bits = 0;
+#pragma unroll
+    for (uint32_t i = 0; i < kSetupChecks; i++) bits |= header[kFoundWords + i];
+    const uint32_t verdict = packing == (uint32_t)(-LIA_E_ROWS) ? packing : bits ? table_failure(bits) : packing;
+    if (verdict == 0) {
+        if (t == 0) *status = 0;
+        return;
+    }
+    if (verdict != packing) { // a table failure: the packing wrote the rows
+        for (uint32_t b = t; b <= n_seqs; b += kPlanThreads) cu[b] = 0;
+        for (uint32_t r = t; r < max_rows; r += kPlanThreads) slot_mapping[r] = kNone;
+    }
+    for (uint32_t w = t; w < n_wg; w += kPlanThreads) work[w] = WorkDesc{};
+    for (uint32_t u = t; u < max_units; u += kPlanThreads) merge[u] = MergeDesc{0, 0, 0, 0};
+    if (t == 0) {
+        *status = verdict;
+        header[kVerdict] = verdict;
+    }
 }
 
 // The plan for more sequences than plan_lds_kernel holds: units written by a serial walk of
@@ -2680,15 +2704,16 @@ static int run_stages(int stages, const lia_attention_config *c, uint32_t n_seqs
         const uint32_t cost = NT == kWideNT ? kUnitCostWide : kUnitCostDecode;
         const uint32_t lag = NT == kWideNT ? kLagWide : kLagDecode;
         if (pk && n_seqs <= kPlanSeqs && n_wg <= kPlanThreads) {
-            // the packing and the plan in one launch (the plan from the packing's inputs), then
-            // the table checks, which also raise the verdict the attention kernels read
+            // the packing, the plan (from the packing's inputs) and the table checks in one
+            // launch, then the step's verdict
             const RawSeqs raw{pk->q_lens, pk->cached, pk->seq_slots, n_rows};
-            e = launch<pack_plan_kernel>(dim3(kPlanGroups + 1), dim3(kPlanThreads), 0, s, n_seqs, *pk,
-                                         raw, rpc, c->num_kv_heads, L.max_units, n_wg, cost,
+            e = launch<pack_plan_kernel>(dim3(kPlanGroups + 1 + kSetupChecks), dim3(kPlanThreads), 0, s,
+                                         n_seqs, *pk, raw, rpc, c->num_kv_heads, L.max_units, n_wg, cost,
                                          lia_device_cus(), lag, xcd, units, work, merge, header);
             if (e == hipSuccess)
-                e = launch<verdict_check_kernel>(dim3(kCheckGroups), dim3(kCheckThreads), 0, s, n_seqs,
-                                                 *pk, header, work, n_wg, merge, L.max_units);
+                e = launch<setup_verdict_kernel>(dim3(1), dim3(kPlanThreads), 0, s, n_seqs, pk->max_rows,
+                                                 pk->cu, pk->slot_mapping, pk->status, header, work, n_wg,
+                                                 merge, L.max_units);
         } else {
             if (pk) { // too many sequences or workgroups for the one-launch form: pack first
                 const int ps = lia_pack_device(n_seqs, pk->seq_slots, pk->q_lens, pk->cached, pk->pages,

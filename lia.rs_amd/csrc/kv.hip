@@ -32,10 +32,9 @@ __global__ __launch_bounds__(1024) void pack_kernel(uint32_t n_seqs, const uint3
 __global__ __launch_bounds__(kCheckThreads) void table_check_kernel(
     uint32_t n_seqs, const uint32_t *seq_slots, const uint32_t *q_lens, const uint32_t *cached,
     const uint32_t *pages, uint32_t stride, uint32_t page_shift, uint32_t pool_pages,
-    uint32_t context, uint32_t max_rows, uint32_t *cu, uint32_t *slot_mapping, uint32_t *status,
-    uint32_t *verdict) {
+    uint32_t context, uint32_t max_rows, uint32_t *cu, uint32_t *slot_mapping, uint32_t *status) {
     table_check_block(blockIdx.x, gridDim.x, n_seqs, seq_slots, q_lens, cached, pages, stride,
-                      page_shift, pool_pages, context, max_rows, cu, slot_mapping, status, verdict);
+                      page_shift, pool_pages, context, max_rows, cu, slot_mapping, status);
 }
 
 // Slot of append row r (slot_mapping[r], or the table's page of its position); kNone for
@@ -365,7 +364,7 @@ extern "C" int lia_pack_device(uint32_t n_seqs, const uint32_t *seq_slots, const
     const hipError_t e = launch<table_check_kernel>(dim3(kCheckGroups), dim3(kCheckThreads), 0, s,
                                                     n_seqs, seq_slots, q_lens, cached, pages, stride,
                                                     shift, pool_pages, context, max_rows, cu_seqlens,
-                                                    slot_mapping, status, nullptr);
+                                                    slot_mapping, status);
     return e == hipSuccess ? LIA_OK : LIA_E_HIP;
 }
 

@@ -254,23 +254,22 @@ __device__ void pack_rows_block(uint32_t n_seqs, const uint32_t *seq_slots, cons
 // itself, 256 sequences at a time.
 constexpr uint32_t kCheckThreads = 256, kCheckGroups = 64;
 
-// `verdict` (may be null) is raised with status, under the same precedence.  Returns whether
-// this workgroup found a failure (uniform).
-__device__ bool table_check_block(uint32_t grp, uint32_t ngrp, uint32_t n_seqs,
-                                  const uint32_t *seq_slots, const uint32_t *q_lens,
-                                  const uint32_t *cached, const uint32_t *pages, uint32_t stride,
-                                  uint32_t page_shift, uint32_t pool_pages, uint32_t context,
-                                  uint32_t max_rows, uint32_t *cu, uint32_t *slot_mapping,
-                                  uint32_t *status, uint32_t *verdict) {
-    __shared__ uint32_t iscan[kCheckThreads], s_slot[kCheckThreads], s_c0[kCheckThreads],
-        s_npg[kCheckThreads], w_a[16], w_b[16];
-    __shared__ uint32_t found; // bit 0: a page outside the pool, bit 1: a missing cached page
+// The table checks of workgroup grp of ngrp (T threads each): failure bits found in its share
+// of the entries (bit 0: a page outside the pool, bit 1: a missing cached page), uniform over
+// the workgroup.
+template <uint32_t T>
+__device__ uint32_t table_check_scan(uint32_t grp, uint32_t ngrp, uint32_t n_seqs,
+                                     const uint32_t *seq_slots, const uint32_t *q_lens,
+                                     const uint32_t *cached, const uint32_t *pages, uint32_t stride,
+                                     uint32_t page_shift, uint32_t pool_pages, uint32_t context) {
+    __shared__ uint32_t iscan[T], s_slot[T], s_c0[T], s_npg[T], w_a[16], w_b[16];
+    __shared__ uint32_t found;
     const uint32_t t = threadIdx.x, P = 1u << page_shift;
     if (t == 0) found = 0;
     const bool quads = (stride & 3) == 0 && ((uintptr_t)pages & 15) == 0;
     const uint32_t per = quads ? 4u : 1u;
     constexpr int K = 4; // items in flight per thread
-    for (uint32_t base = 0; base < n_seqs; base += kCheckThreads) {
+    for (uint32_t base = 0; base < n_seqs; base += T) {
         const uint32_t b = base + t;
         const uint32_t n = b < n_seqs ? q_lens[b] : 0u, c0 = b < n_seqs ? cached[b] : 0u;
         const uint32_t keys = min(c0 + n, context);
@@ -282,9 +281,9 @@ __device__ bool table_check_block(uint32_t grp, uint32_t ngrp, uint32_t n_seqs,
         block_scan2(items, unused, w_a, w_b);
         iscan[t] = items;
         __syncthreads();
-        const uint32_t cnt = min(n_seqs - base, kCheckThreads), total = iscan[cnt - 1];
-        const uint32_t step = ngrp * kCheckThreads;
-        for (uint32_t e0 = grp * kCheckThreads + t; e0 < total; e0 += K * step) {
+        const uint32_t cnt = min(n_seqs - base, T), total = iscan[cnt - 1];
+        const uint32_t step = ngrp * T;
+        for (uint32_t e0 = grp * T + t; e0 < total; e0 += K * step) {
             uint32_t e[K], bl[K];
 #pragma unroll
             for (int k = 0; k < K; k++) e[k] = min(e0 + k * step, total - 1);
@@ -313,24 +312,38 @@ __device__ bool table_check_block(uint32_t grp, uint32_t ngrp, uint32_t n_seqs,
         }
         __syncthreads(); // the LDS arrays are rewritten by the next chunk of sequences
     }
-    if (!found) return false;
+    return found;
+}
+
+// Status of the table-check failure bits: a page outside the pool outranks a missing page.
+__device__ __forceinline__ uint32_t table_failure(uint32_t bits) {
+    return (bits & 1) ? (uint32_t)(-LIA_E_PAGE_RANGE) : (bits & 2) ? (uint32_t)(-LIA_E_MISSING_PAGE) : 0u;
+}
+
+// table_check_kernel's workgroup: the checks, and on a failure the batch rejected as the
+// packing rejects one and the status raised to it unless it holds a failure the reference
+// checks earlier.
+__device__ void table_check_block(uint32_t grp, uint32_t ngrp, uint32_t n_seqs,
+                                  const uint32_t *seq_slots, const uint32_t *q_lens,
+                                  const uint32_t *cached, const uint32_t *pages, uint32_t stride,
+                                  uint32_t page_shift, uint32_t pool_pages, uint32_t context,
+                                  uint32_t max_rows, uint32_t *cu, uint32_t *slot_mapping,
+                                  uint32_t *status) {
+    const uint32_t found = table_check_scan<kCheckThreads>(grp, ngrp, n_seqs, seq_slots, q_lens, cached,
+                                                           pages, stride, page_shift, pool_pages, context);
+    if (!found) return;
+    const uint32_t t = threadIdx.x;
     for (uint32_t b = t; b <= n_seqs; b += kCheckThreads) cu[b] = 0;
     for (uint32_t r = t; r < max_rows; r += kCheckThreads) slot_mapping[r] = kNone;
     if (t == 0) {
-        const uint32_t want = (found & 1) ? (uint32_t)(-LIA_E_PAGE_RANGE) : (uint32_t)(-LIA_E_MISSING_PAGE);
-        // raise a word to `want` unless it holds a failure the reference checks earlier
-        auto raise = [&](uint32_t *w) {
-            uint32_t old = __hip_atomic_load(w, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
-            while (old != (uint32_t)(-LIA_E_ROWS) && old != (uint32_t)(-LIA_E_PAGE_RANGE) && old != want) {
-                const uint32_t prev = atomicCAS(w, old, want);
-                if (prev == old) break;
-                old = prev;
-            }
-        };
-        raise(status);
-        if (verdict) raise(verdict);
+        const uint32_t want = table_failure(found);
+        uint32_t old = __hip_atomic_load(status, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
+        while (old != (uint32_t)(-LIA_E_ROWS) && old != (uint32_t)(-LIA_E_PAGE_RANGE) && old != want) {
+            const uint32_t prev = atomicCAS(status, old, want);
+            if (prev == old) break;
+            old = prev;
+        }
     }
-    return true;
 }
 
 } // namespace lia
