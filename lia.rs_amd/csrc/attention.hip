@@ -203,8 +203,7 @@ __device__ void plan_lds(uint32_t n_seqs, const uint32_t *cu, const uint32_t *po
                          WorkDesc *work, MergeDesc *merge, uint32_t *header) {
     __shared__ uint32_t s_r0[kPlanSeqs], s_nr[kPlanSeqs], s_p0[kPlanSeqs], s_trow[kPlanSeqs];
     __shared__ uint32_t s_u0[kPlanSeqs + 1], s_b0[kPlanSeqs + 1], s_c0[kPlanSeqs + 1];
-    __shared__ uint32_t w_a[kPlanThreads / 64], w_b[kPlanThreads / 64];
-    __shared__ uint32_t w_r[kPlanThreads / 64], w_z[kPlanThreads / 64];
+    __shared__ uint32_t w_s[4][kPlanThreads / 64];
     __shared__ uint32_t carry_units, carry_blocks, carry_rows, raw_bad;
     __shared__ uint64_t s_rlo[kPlanThreads + 1];
     // Threads exchange only LDS data (nothing written to global memory is read back), so the
@@ -214,45 +213,52 @@ __device__ void plan_lds(uint32_t n_seqs, const uint32_t *cu, const uint32_t *po
     // the workgroups of the launch share the descriptor loops; each computes the per-sequence
     // extents and range starts itself (they live in its LDS)
     const uint32_t g0 = t * ngrp + grp, GT = ngrp * T; // interleaved shares
+    // up to 64 sequences: the scans stay in wave 0, with no barrier of their own
+    const bool one_wave = n_seqs <= 64;
+    const uint32_t last = one_wave ? 63 : T - 1; // the thread holding the totals
     {
         const uint32_t b = t;
         uint32_t nu = 0, nb = 0, r0 = 0, nr = 0, p0 = 0, trow = 0;
-        if (raw) {
-            // rows of the batch: an exclusive scan of the new-token counts.  The packing beside
-            // this plan has not validated them: a sequence whose keys pass its table row (which
-            // the packing rejects) plans nothing, so no table read leaves the row.
-            nr = b < n_seqs ? raw->q_lens[b] : 0u;
-            p0 = b < n_seqs ? raw->cached[b] : 0u;
-            trow = b < n_seqs ? raw->seq_slots[b] : 0u;
-            uint32_t sr = nr, sbad = (uint64_t)p0 + nr > ((uint64_t)stride << page_shift) ? 1u : 0u;
-            block_scan2(sr, sbad, w_r, w_z); // rows before this sequence, and the bad ones
-            r0 = sr - nr;
-            if (t == T - 1) { carry_rows = sr; raw_bad = sbad; }
-        }
         if (b < n_seqs) {
-            if (!raw) {
+            if (raw) {
+                // the packing's inputs; the rows before this sequence are a scan of the
+                // new-token counts, below
+                nr = raw->q_lens[b];
+                p0 = raw->cached[b];
+                trow = raw->seq_slots[b];
+            } else {
                 r0 = cu[b];
                 nr = cu[b + 1] - r0;
-            }
-            if (nr > 0) {
-                if (!raw) {
+                if (nr > 0) {
                     p0 = positions[r0];
                     trow = sequences[r0];
                 }
+            }
+            if (nr > 0) {
                 const uint32_t ncb = (nr + rpc - 1) / rpc;
                 nu = ncb * hkv;
                 nb = (ncb * ((p0 + 31) / 32) + new_blocks_before(ncb - 1, rpc) + (nr + 31) / 32) * hkv;
             }
-            s_r0[b] = r0; s_nr[b] = nr; s_p0[b] = p0; s_trow[b] = trow;
         }
-        uint32_t su = nu, sb = nb;
-        block_scan2(su, sb, w_a, w_b); // inclusive
+        // inclusive scans of the units and blocks, and on raw inputs of the rows and of the
+        // sequences whose keys pass their table row.  The packing beside a raw plan has not
+        // validated its inputs: such a sequence makes the plan empty, so no table read leaves
+        // the row.
+        uint32_t v[4] = {nu, nb, nr,
+                         raw && (uint64_t)p0 + nr > ((uint64_t)stride << page_shift) ? 1u : 0u};
+        if (raw) block_scan_n<4>(v, w_s, one_wave);
+        else block_scan_n<2>(v, w_s, one_wave);
+        if (raw) r0 = v[2] - nr;
         if (b < n_seqs) {
-            s_u0[b] = su - nu;
-            s_b0[b] = sb - nb;
-            s_c0[b] = sb - nb + unit_cost * (su - nu);
+            s_r0[b] = r0; s_nr[b] = nr; s_p0[b] = p0; s_trow[b] = trow;
+            s_u0[b] = v[0] - nu;
+            s_b0[b] = v[1] - nb;
+            s_c0[b] = v[1] - nb + unit_cost * (v[0] - nu);
         }
-        if (t == T - 1) { carry_units = su; carry_blocks = sb; }
+        if (t == last) {
+            carry_units = v[0]; carry_blocks = v[1];
+            if (raw) { carry_rows = v[2]; raw_bad = v[3]; }
+        }
         lds_barrier();
     }
     const bool overflow = carry_units > max_units || (raw && (carry_rows != raw->n_rows || raw_bad));
@@ -296,7 +302,6 @@ __device__ void plan_lds(uint32_t n_seqs, const uint32_t *cu, const uint32_t *po
         const uint32_t b = seq_of(s_u0, u), ncb = (s_nr[b] + rpc - 1) / rpc, i = u - s_u0[b];
         return make_unit(b, i / ncb, i % ncb);
     };
-    for (uint32_t u = g0; u < U; u += GT) units[u] = unit_by_index(u);
     const uint32_t P = 1u << page_shift;
     for (uint32_t w = N + g0; w < n_wg; w += GT) { // launched workgroups without work
         WorkDesc d = {};
@@ -338,10 +343,16 @@ __device__ void plan_lds(uint32_t n_seqs, const uint32_t *cu, const uint32_t *po
         for (uint32_t r = t; r <= N; r += T) s_rlo[r] = weight_before(r) * TC / FN;
         lds_barrier();
     }
-    auto range_lo = [&](uint32_t r) { return skew ? s_rlo[r] : (uint64_t)r * TC / N; };
+    // equal shares in 32-bit arithmetic when TC * N fits (every batch up to 2^32 / n_wg
+    // blocks): a 64-bit division is a long software sequence on the plan's critical path
+    const bool narrow = TC * N < (1ull << 32);
+    auto range_lo = [&](uint32_t r) -> uint64_t {
+        if (skew) return s_rlo[r];
+        return narrow ? r * (uint32_t)TC / N : (uint64_t)r * TC / N;
+    };
     // the last range starting at or before cost c
     auto range_of = [&](uint64_t c) {
-        if (!skew) return (uint32_t)(((c + 1) * N - 1) / TC);
+        if (!skew) return narrow ? ((uint32_t)c * N + N - 1) / (uint32_t)TC : (uint32_t)(((c + 1) * N - 1) / TC);
         uint32_t a = 0, e = N;
         while (a + 1 < e) {
             const uint32_t mid = (a + e) >> 1;
@@ -349,10 +360,12 @@ __device__ void plan_lds(uint32_t n_seqs, const uint32_t *cu, const uint32_t *po
         }
         return a;
     };
+    // each unit's descriptor, and its merge descriptor from it
     for (uint32_t u = g0; u < max_units; u += GT) {
         MergeDesc m = {0, 0, 0, 0};
         if (u < U) {
             const UnitDesc ud = unit_by_index(u);
+            units[u] = ud;
             const uint64_t cu0 = (uint64_t)ud.block_start + unit_cost * (u + 1); // cost of its first block
             const uint32_t wf = range_of(cu0), wl = range_of(cu0 + ud.nblocks - 1);
             if (wf != wl) m = MergeDesc{wf + u, wl - wf + 1, ud.rowbeg, ud.nrows_hk};
@@ -384,7 +397,9 @@ __device__ void plan_lds(uint32_t n_seqs, const uint32_t *cu, const uint32_t *po
     // needed reads a word the plan reads anyway - cu[0], or q_lens[0] of a raw plan, whose
     // cu is null - and is replaced by 0).
     const uint32_t *dummy = raw ? raw->q_lens : cu;
-    for (uint32_t w0 = g0; w0 < N; w0 += GT) {
+    // the work descriptors from the last threads, so that their chain (searches, divisions,
+    // table loads) runs beside the units' on other waves
+    for (uint32_t w0 = (T - 1 - t) * ngrp + grp; w0 < N; w0 += GT) {
         WorkDesc d[1];
         uint32_t v[1][kPrePages];
         {

@@ -190,6 +190,35 @@ __device__ __forceinline__ void block_scan2(uint32_t &a, uint32_t &b, uint32_t *
     b += pb;
 }
 
+// Inclusive scan of the first N of four values over the workgroup (thread order), through
+// ws[value][wave].  With one_wave (every nonzero value in wave 0) the scan stays in wave 0:
+// no barrier, and only wave 0's threads hold the sums.
+template <int N, int W>
+__device__ __forceinline__ void block_scan_n(uint32_t (&v)[4], uint32_t (*ws)[W], bool one_wave) {
+    const uint32_t lane = threadIdx.x & 63, w = threadIdx.x >> 6;
+#pragma unroll
+    for (int off = 1; off < 64; off <<= 1) {
+#pragma unroll
+        for (int i = 0; i < N; i++) {
+            const uint32_t x = __shfl_up(v[i], off);
+            if (lane >= (uint32_t)off) v[i] += x;
+        }
+    }
+    if (one_wave) return;
+    if (lane == 63) {
+#pragma unroll
+        for (int i = 0; i < N; i++) ws[i][w] = v[i];
+    }
+    lds_barrier();
+    uint32_t p[N] = {};
+    for (uint32_t j = 0; j < w; j++) {
+#pragma unroll
+        for (int i = 0; i < N; i++) p[i] += ws[i][j];
+    }
+#pragma unroll
+    for (int i = 0; i < N; i++) v[i] += p[i];
+}
+
 // Raw buffer resource over [base, base + bytes): loads at or past `bytes` return zeros and
 // touch no memory, which lets a loop issue every load unconditionally.
 constexpr int kBufferConfig = 0x00020000; // gfx9 raw buffer, 32-bit data format
