@@ -415,6 +415,34 @@ def main():
     log(f"attention kernel: {kernel_us:.2f} us/launch, {achieved:.1f} GB/s "
         f"({achieved / PEAK_HBM_GBPS:.1%} of peak), layer bytes {layer_bytes}")
 
+    # ---- the kernel's own loads without its arithmetic (lia_paged_read: same plan, ranges,
+    # loads and pipeline waits), timed the same way: the ceiling of its access pattern
+    sink = torch.zeros(lia.paged_read_sink_words(cfg), dtype=torch.int32, device=dev)
+    rgraph = torch.cuda.CUDAGraph()
+    with torch.cuda.stream(stream):
+        with torch.cuda.graph(rgraph, stream=stream):
+            for layer in range(L):
+                lia.paged_read(cfg, b.n_seqs, flat, qs[layer], kpool[layer], vpool[layer], sink, ws,
+                               stream=stream)
+    torch.cuda.synchronize()
+    for _ in range(3):
+        rgraph.replay()
+    torch.cuda.synchronize()
+    ks.record(cur)
+    for _ in range(args.kernel_reps):
+        rgraph.replay()
+    ke.record(cur)
+    torch.cuda.synchronize()
+    read_us = ks.elapsed_time(ke) * 1e3 / (args.kernel_reps * L)
+    read_gbps = layer_bytes / (read_us * 1e-6) / 1e9
+    paged = {"us": round(read_us, 3), "GBps": round(read_gbps, 1),
+             "frac_of_peak": round(read_gbps / PEAK_HBM_GBPS, 4),
+             "kernel_frac_of_paged_read": round(read_us / kernel_us, 4),
+             "kernel": "attention_kernel<128,1,bf16> read-only variant (lia_paged_read: the "
+                       "kernel's plan, loads and pipeline waits, no attention arithmetic)"}
+    log(f"paged read (the kernel's loads alone): {read_us:.2f} us/launch, {read_gbps:.1f} GB/s "
+        f"({read_gbps / PEAK_HBM_GBPS:.1%} of peak); attention kernel at {read_us / kernel_us:.1%} of it")
+
     # ---- the same bytes read contiguously on this device: the ceiling the kernel is held to
     ceiling = read_ceiling(lia, layer_bytes, L, args.kernel_reps)
     log(f"contiguous read of {layer_bytes} B: {ceiling['us']:.2f} us/launch, {ceiling['GBps']:.1f} GB/s "
@@ -468,6 +496,7 @@ def main():
             "kernel": "attention_kernel<128,1,bf16> (fused append)", "kernel_us": round(kernel_us, 3),
             "bytes_per_launch": layer_bytes,
             "read_ceiling": dict(ceiling, kernel_frac_of_ceiling=round(achieved / ceiling["GBps"], 4)),
+            "paged_read_ceiling": paged,
         },
         "cpu_baseline": cpu,
         "side": side or None,

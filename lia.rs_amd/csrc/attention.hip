@@ -953,6 +953,9 @@ struct State {
     // at the end
     f32x4 l[NT];
     f32x4 o[NT][Cfg<D, KVT>::DTW];
+    uint32_t fold;    // read-only variant: XOR of the K words this lane loaded of keys in
+    uint32_t fold_hi; // [lo, fold_hi), the range (a chunk starts at a 32-key boundary, so a
+                      // range's first chunk also loads keys of the range before it)
 };
 
 // One chunk: partial scores for this wave's d slice, cross-wave sum through LDS, online
@@ -1104,11 +1107,28 @@ __device__ __forceinline__ void compute_chunk(const AttnParams &p, const Chunk<D
     }
 }
 
+// The read-only variant's chunk t: wait for the chunk's loads as compute_chunk does and fold
+// the K words of its keys inside the range, with no attention arithmetic, score exchange or
+// barrier.  Lane (g, li) holds key t + 16j + li of tile j.
+template <int D, int NT, int KVT, int VW = kLoadsPerChunk<D, KVT>>
+__device__ __forceinline__ void fold_chunk(const Chunk<D, KVT> &c, uint32_t t, State<D, NT, KVT> &st) {
+    wait_vmcnt<VW>();
+    const uint32_t li = lane_id() & 15;
+#pragma unroll
+    for (int j = 0; j < 2; j++) {
+        uint32_t x = 0;
+#pragma unroll
+        for (int w = 0; w < Cfg<D, KVT>::KW; w++) x ^= c.k[j][w];
+        const uint32_t key = t + 16 * j + li;
+        st.fold ^= key >= st.lo && key < st.fold_hi ? x : 0u;
+    }
+}
+
 // One pipeline step: issue the loads of chunk `tn` into stage `sn` (registers cn), then
 // compute chunk `tc` from stage `sc` (registers cc).  The two stages are restrict
 // parameters: the transpose reads of `sc` are then known not to alias the direct-to-LDS
 // loads still in flight into `sn`, so no full vmcnt drain is needed before them.
-template <int D, int NT, int KVT>
+template <int D, int NT, int KVT, bool RO = false>
 __device__ __forceinline__ void pipeline_step(const AttnParams &p, Chunk<D, KVT> &cn, uint32_t tn,
                                               const TilePages &tpn, uint16_t *__restrict__ sn,
                                               const Chunk<D, KVT> &cc, uint32_t tc,
@@ -1116,13 +1136,14 @@ __device__ __forceinline__ void pipeline_step(const AttnParams &p, Chunk<D, KVT>
                                               const uint8_t *vbase, const DecLanes<D, KVT> &ln,
                                               uint32_t wave, State<D, NT, KVT> &st, f32x4 *sx) {
     load_chunk<D, KVT, kVAux<NT>>(p, cn, tn, tpn, kbase, vbase, ln, sn);
-    compute_chunk<D, NT, KVT>(p, cc, tc, st, sc, sx, wave);
+    if constexpr (RO) fold_chunk<D, NT, KVT>(cc, tc, st);
+    else compute_chunk<D, NT, KVT>(p, cc, tc, st, sc, sx, wave);
 }
 
 // Attends keys [s_lo, s_hi) of one source (coordinates of that source: token index in the
 // pool, or new-row index) into the running state.  Windows of at most 64 pages; the
 // first two chunks of the workgroup's first range take their pages from the plan.
-template <int D, int NT, int KVT>
+template <int D, int NT, int KVT, bool RO = false>
 __device__ __forceinline__ void run_range(const AttnParams &p, const uint8_t *kbase,
                                           const uint8_t *vbase, const uint32_t *table,
                                           uint32_t s_lo, uint32_t s_hi, bool use_pre,
@@ -1153,20 +1174,20 @@ __device__ __forceinline__ void run_range(const AttnParams &p, const uint8_t *kb
             tp1 = tile_pages<C::FP8>(win, wbeg + 32, shift, wend);
         }
         load_chunk<D, KVT, kVAux<NT>>(p, c0, wbeg, tp0, kbase, vbase, ln, stage0);
-        pipeline_step<D, NT, KVT>(p, c1, wbeg + 32, tp1, stage1, c0, wbeg, stage0, kbase, vbase, ln,
-                                  wave, st, sxb + parity * SX);
+        pipeline_step<D, NT, KVT, RO>(p, c1, wbeg + 32, tp1, stage1, c0, wbeg, stage0, kbase, vbase, ln,
+                                      wave, st, sxb + parity * SX);
         parity ^= 1;
         if (wbeg + 32 < wend) {
             for (uint32_t t = wbeg + 32;; t += 64) {
                 // loads past wend carry no traffic
-                pipeline_step<D, NT, KVT>(p, c0, t + 32, tile_pages<C::FP8>(win, t + 32, shift, wend),
-                                          stage0, c1, t, stage1, kbase, vbase, ln, wave, st,
-                                          sxb + parity * SX);
+                pipeline_step<D, NT, KVT, RO>(p, c0, t + 32, tile_pages<C::FP8>(win, t + 32, shift, wend),
+                                              stage0, c1, t, stage1, kbase, vbase, ln, wave, st,
+                                              sxb + parity * SX);
                 parity ^= 1;
                 if (t + 32 >= wend) break;
-                pipeline_step<D, NT, KVT>(p, c1, t + 64, tile_pages<C::FP8>(win, t + 64, shift, wend),
-                                          stage1, c0, t + 32, stage0, kbase, vbase, ln, wave, st,
-                                          sxb + parity * SX);
+                pipeline_step<D, NT, KVT, RO>(p, c1, t + 64, tile_pages<C::FP8>(win, t + 64, shift, wend),
+                                              stage1, c0, t + 32, stage0, kbase, vbase, ln, wave, st,
+                                              sxb + parity * SX);
                 parity ^= 1;
                 if (t + 64 >= wend) break;
             }
@@ -1267,7 +1288,12 @@ constexpr int kMinWavesPerEU = KVT == LIA_FP8_E4M3 ? 2 : 3;
 
 // The workgroup-size bound (D/32 waves) is looser than the D/SW waves launched: the
 // exact bound changes register allocation and measured 1 % slower on a batch-8 bf16 decode.
-template <int D, int NT, int KVT>
+//
+// RO (lia_paged_read): the same plan, ranges, loads, pipeline and waits with the attention
+// arithmetic, the score exchange and every store but one left out - each wave folds the K words
+// it loaded and writes the fold to ((uint32_t *)p.out)[wg * waves + wave].  It times the
+// kernel's own memory access on its own.
+template <int D, int NT, int KVT, bool RO = false>
 __global__ __launch_bounds__(D / 32 * 64, kMinWavesPerEU<KVT>) void attention_kernel(AttnParams p) {
     using C = Cfg<D, KVT>;
     constexpr uint32_t COLS = 16 * NT;
@@ -1290,6 +1316,7 @@ __global__ __launch_bounds__(D / 32 * 64, kMinWavesPerEU<KVT>) void attention_ke
     const uint32_t row_bytes = p.hkv * D * C::EB;
     uint32_t parity = 0; // alternates the score-exchange buffer across all chunks
     bool first = true;
+    uint32_t fold = 0;
 
     // the plan guarantees a unit covers every block of a non-empty range
     while (lo < hi) {
@@ -1308,6 +1335,7 @@ __global__ __launch_bounds__(D / 32 * 64, kMinWavesPerEU<KVT>) void attention_ke
         const uint32_t ncols = nrows * p.group;
 
         State<D, NT, KVT> st;
+        st.fold = 0;
         uint32_t climit[NT]; // per column: keys it attends (causal limit), 0 for padding
 #pragma unroll
         for (int nt = 0; nt < NT; nt++) {
@@ -1339,33 +1367,40 @@ __global__ __launch_bounds__(D / 32 * 64, kMinWavesPerEU<KVT>) void attention_ke
             const int w0 = (int)min(pos0 + 1 - origin, r_hi) - (int)r_lo;
             st.free_lo = r_lo;
             st.free_hi = r_lo + (w0 > 0 ? (uint32_t)w0 : 0u);
+            st.fold_hi = r_hi;
         };
         const uint8_t *kpool = (const uint8_t *)p.kc, *vpool = (const uint8_t *)p.vc;
         if (!fused) {
             // both runs from the pool: one contiguous key range
             const uint32_t r_lo = key_of(a), r_hi = min(key_of(e), kend);
             set_limits(r_lo, r_hi, 0);
-            run_range<D, NT, KVT>(p, kpool, vpool, table, r_lo, r_hi, use_pre, wd.pre, hk, wave, st,
-                                  stage0, stage1, sxb, parity);
+            run_range<D, NT, KVT, RO>(p, kpool, vpool, table, r_lo, r_hi, use_pre, wd.pre, hk, wave, st,
+                                      stage0, stage1, sxb, parity);
         } else {
             if (a < cb) {
                 const uint32_t r_lo = 32 * a, r_hi = min(32 * min(e, cb), kcache);
                 set_limits(r_lo, r_hi, 0);
-                run_range<D, NT, KVT>(p, kpool, vpool, table, r_lo, r_hi, use_pre, wd.pre, hk, wave,
-                                      st, stage0, stage1, sxb, parity);
+                run_range<D, NT, KVT, RO>(p, kpool, vpool, table, r_lo, r_hi, use_pre, wd.pre, hk, wave,
+                                          st, stage0, stage1, sxb, parity);
             }
             if (e > cb) {
                 // new keys: row kcache + i of the sequence is packed row r0 + i
                 const uint32_t r0 = ud.rowbeg - (pos0 - kcache);
                 const uint32_t r_lo = 32 * (max(a, cb) - cb), r_hi = min(32 * (e - cb), kend - kcache);
                 set_limits(r_lo, r_hi, kcache);
-                run_range<D, NT, KVT>(p, (const uint8_t *)p.newk + (size_t)r0 * row_bytes,
-                                      (const uint8_t *)p.newv + (size_t)r0 * row_bytes, nullptr,
-                                      r_lo, r_hi, false, wd.pre, hk, wave, st, stage0, stage1, sxb,
-                                      parity);
+                run_range<D, NT, KVT, RO>(p, (const uint8_t *)p.newk + (size_t)r0 * row_bytes,
+                                          (const uint8_t *)p.newv + (size_t)r0 * row_bytes, nullptr,
+                                          r_lo, r_hi, false, wd.pre, hk, wave, st, stage0, stage1, sxb,
+                                          parity);
             }
         }
 
+        if constexpr (RO) {
+            fold ^= st.fold;
+            lo = seg_end;
+            u++;
+            continue;
+        }
         // Finalise this wave's d slice: normalised output or a split record.
         const bool whole = lo == bs && seg_end == uend;
         const uint32_t rec = (wd.flags >> 8) + u;
@@ -1399,6 +1434,12 @@ __global__ __launch_bounds__(D / 32 * 64, kMinWavesPerEU<KVT>) void attention_ke
         }
         lo = seg_end;
         u++;
+    }
+    if constexpr (RO) {
+#pragma unroll
+        for (int m = 32; m >= 1; m >>= 1) fold ^= (uint32_t)__shfl_xor((int)fold, m, 64);
+        if (lane == 0) ((uint32_t *)p.out)[wg * C::WAVES + wave] = fold;
+        return;
     }
     if constexpr (!C::FP8) {
         if (fused) append_rows<D, KVT>(p, wg, gridDim.x);
@@ -2610,9 +2651,9 @@ static int validate(const lia_attention_config *c) {
     return LIA_OK;
 }
 
-template <int D, int NT, int KVT>
+template <int D, int NT, int KVT, bool RO = false>
 static hipError_t launch_partial(const AttnParams &p, uint32_t n_wg, hipStream_t s) {
-    return launch<attention_kernel<D, NT, KVT>>(dim3(n_wg), dim3(Cfg<D, KVT>::THREADS), 0, s, p);
+    return launch<attention_kernel<D, NT, KVT, RO>>(dim3(n_wg), dim3(Cfg<D, KVT>::THREADS), 0, s, p);
 }
 
 template <int D>
@@ -2630,7 +2671,7 @@ static hipError_t launch_partial_kv(int kv, const AttnParams &p, uint32_t n_wg, 
     return launch_partial<D, NT, LIA_FP8_E4M3>(p, n_wg, s);
 }
 
-enum Stage { kPlan = 1, kPartial = 2, kMerge = 4 };
+enum Stage { kPlan = 1, kPartial = 2, kMerge = 4, kRead = 8 };
 
 // New rows appended by the attention launch itself (lia_attention_partial_append).
 struct FusedAppend {
@@ -2659,7 +2700,11 @@ static int run_stages(int stages, const lia_attention_config *c, uint32_t n_seqs
         if (!fa->k || !fa->v || !fa->slots) return LIA_E_ARG;
         if (((uintptr_t)fa->k | (uintptr_t)fa->v) & 15) return LIA_E_ALIGN;
     }
-    if (stages & kPartial) {
+    if (stages & kRead) {
+        if (!out) return LIA_E_ARG;
+        if ((uintptr_t)out & 3) return LIA_E_ALIGN;
+    }
+    if (stages & (kPartial | kRead)) {
         if (!pages || !q || !kc || !vc) return LIA_E_ARG;
         if (c->kv_dtype == LIA_FP8_E4M3 && (!k_scales || !v_scales)) return LIA_E_ARG;
         if (((uintptr_t)q | (uintptr_t)kc | (uintptr_t)vc) & 15) return LIA_E_ALIGN;
@@ -2759,6 +2804,20 @@ static int run_stages(int stages, const lia_attention_config *c, uint32_t n_seqs
             if (NT == 1) e = launch_partial_kv<64, 1>(c->kv_dtype, p, n_wg, s);
             else if (NT == 2) e = launch_partial_kv<64, 2>(c->kv_dtype, p, n_wg, s);
             else e = launch_wide<64>(c->kv_dtype, p, n_wg, s);
+        }
+    }
+    if (e == hipSuccess && (stages & kRead)) {
+        // the decode kernel's loads alone (lia_paged_read): 16-bit pools, decode tiles
+        if (c->head_dim == 128) {
+            if (NT == 1) e = c->kv_dtype == LIA_BF16 ? launch_partial<128, 1, LIA_BF16, true>(p, n_wg, s)
+                                                     : launch_partial<128, 1, LIA_F16, true>(p, n_wg, s);
+            else e = c->kv_dtype == LIA_BF16 ? launch_partial<128, 2, LIA_BF16, true>(p, n_wg, s)
+                                             : launch_partial<128, 2, LIA_F16, true>(p, n_wg, s);
+        } else {
+            if (NT == 1) e = c->kv_dtype == LIA_BF16 ? launch_partial<64, 1, LIA_BF16, true>(p, n_wg, s)
+                                                     : launch_partial<64, 1, LIA_F16, true>(p, n_wg, s);
+            else e = c->kv_dtype == LIA_BF16 ? launch_partial<64, 2, LIA_BF16, true>(p, n_wg, s)
+                                             : launch_partial<64, 2, LIA_F16, true>(p, n_wg, s);
         }
     }
     if (e == hipSuccess && (stages & kMerge)) {
@@ -2898,6 +2957,33 @@ extern "C" int lia_attention_partial_append_fp8(const lia_attention_config *c, u
     if (st) return st;
     return run_stages(kPartial, c, n_seqs, n_rows, &dummy, &dummy, nullptr, pages, q, kc, vc,
                       k_scales, v_scales, workspace, workspace_bytes, out, stream);
+}
+
+// The memory access of one lia_attention_partial launch on its own: the plan in `workspace`, the
+// same workgroups, block ranges, loads and pipeline waits, without the attention arithmetic.
+// Each wave writes the XOR of the K words it loaded to sink[workgroup * waves + wave] (the
+// XOR of all sink words is the XOR of every attended key's K words).  16-bit pools and decode
+// tiles only (batches the decode kernel serves).
+extern "C" int lia_paged_read(const lia_attention_config *c, uint32_t n_seqs, uint32_t n_rows,
+                              const uint32_t *pages, const void *q, const void *kc, const void *vc,
+                              void *workspace, size_t workspace_bytes, uint32_t *sink,
+                              size_t sink_words, lia_stream_t stream) {
+    static const uint32_t dummy = 0;
+    int st = validate(c);
+    if (st) return st;
+    if (c->kv_dtype == LIA_FP8_E4M3) return LIA_E_UNSUPPORTED;
+    if (n_seqs == 0 || n_seqs > c->max_seqs || n_rows == 0 || n_rows > c->max_rows) return LIA_E_ARG;
+    const uint32_t group = c->num_q_heads / c->num_kv_heads;
+    if (nt_for(n_rows, n_seqs, group, c->kv_dtype) == kWideNT) return LIA_E_UNSUPPORTED;
+    if (!sink) return LIA_E_ARG;
+    if (sink_words < lia_paged_read_sink_words(c)) return LIA_E_ARG;
+    return run_stages(kRead, c, n_seqs, n_rows, &dummy, &dummy, nullptr, pages, q, kc, vc, nullptr,
+                      nullptr, workspace, workspace_bytes, sink, stream);
+}
+
+extern "C" size_t lia_paged_read_sink_words(const lia_attention_config *c) {
+    if (!c || validate(c)) return 0;
+    return (size_t)max_workgroups(c) * (c->head_dim / 64);
 }
 
 extern "C" int lia_attention_merge(const lia_attention_config *c, uint32_t n_seqs, uint32_t n_rows,

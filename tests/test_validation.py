@@ -196,3 +196,54 @@ def test_fp8_partial_append_validates_both_launches_first(lia):
     assert call(fp8, new_k=ODD16) == E_ALIGN
     assert call(fp8, ks=None) == E_ARG
     assert call(fp8, ws_bytes=1) == E_WORKSPACE
+
+
+def _read(lia, cfg, a, sink=A, sink_words=None):
+    p = lambda x: None if x is None else C.c_void_p(x)
+    words = lia.lib().lia_paged_read_sink_words(C.byref(cfg)) if sink_words is None else sink_words
+    return lia.lib().lia_paged_read(C.byref(cfg), a["n_seqs"], a["n_rows"], p(a["pages"]), p(a["q"]),
+                                    p(a["kc"]), p(a["vc"]), p(a["ws"]), a["ws_bytes"], p(sink), words,
+                                    None)
+
+
+def test_paged_read_sink_words(lia):
+    cfg = _cfg(lia)
+    # one word per wave (head_dim / 64 waves) of every workgroup the plan may use
+    assert lia.lib().lia_paged_read_sink_words(C.byref(cfg)) > 0
+    assert lia.lib().lia_paged_read_sink_words(C.byref(cfg)) % 2 == 0
+    assert lia.lib().lia_paged_read_sink_words(C.byref(_cfg(lia, num_kv_heads=0))) == 0
+
+
+@pytest.mark.parametrize("case,expect", [
+    ("fp8", E_UNSUPPORTED),          # FP8 pools: the decode kernel loads V through registers
+    ("prefill", E_UNSUPPORTED),      # a batch the prefill kernel serves
+    ("no_sink", E_ARG),
+    ("short_sink", E_ARG),
+    ("odd_sink", E_ALIGN),
+    ("no_q", E_ARG),
+    ("no_pages", E_ARG),
+    ("workspace", E_WORKSPACE),
+    ("rows", E_ARG),
+])
+def test_paged_read_validation(lia, case, expect):
+    """lia_paged_read checks its arguments like lia_attention_partial, plus its sink."""
+    cfg = _cfg(lia, kv_dtype=FP8) if case == "fp8" else _cfg(lia, max_rows=4096, max_seqs=4)
+    a = _args(lia, cfg)
+    sink, words = A, None
+    if case == "prefill":
+        a.update(n_seqs=1, n_rows=2048)
+    elif case == "no_sink":
+        sink = None
+    elif case == "short_sink":
+        words = lia.lib().lia_paged_read_sink_words(C.byref(cfg)) - 1
+    elif case == "odd_sink":
+        sink = A + 2
+    elif case == "no_q":
+        a.update(q=None)
+    elif case == "no_pages":
+        a.update(pages=None)
+    elif case == "workspace":
+        a.update(ws_bytes=a["ws_bytes"] - 1)
+    elif case == "rows":
+        a.update(n_rows=0)
+    assert _read(lia, cfg, a, sink, words) == expect
