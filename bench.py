@@ -169,6 +169,19 @@ def side_measure(config, seed, steps, warmup, reps, kv=None):
     nbytes, flops = b.algorithmic_bytes() + append_bytes, b.flops()
     mfma = config == 3
 
+    # the decode kernel's loads alone (lia_paged_read) on the same plan, against the attention
+    # launch alone (on FP8 pools without its append launch)
+    paged = None
+    if not mfma:
+        sink = torch.zeros(lia.paged_read_sink_words(cfg), dtype=torch.int32, device=dev)
+        rus = timed(lambda: lia.paged_read(cfg, b.n_seqs, flat, q, kp, vp, sink, ws, ks, vs))
+        aus = timed(lambda: lia.attention_partial(cfg, b.n_seqs, flat, q, kp, vp, out, ws, ks, vs)) \
+            if fp8 else kus
+        rbytes = b.algorithmic_bytes()
+        paged = {"us": round(rus, 3), "GBps": round(rbytes / (rus * 1e-6) / 1e9, 1),
+                 "frac_of_peak": round(rbytes / (rus * 1e-6) / 1e9 / PEAK_HBM_GBPS, 4),
+                 "attention_us": round(aus, 3), "kernel_frac_of_paged_read": round(rus / aus, 4)}
+
     def roof(t_us):
         gbps, tflops = nbytes / (t_us * 1e-6) / 1e9, flops / (t_us * 1e-6) / 1e12
         r = {"bound": "mfma" if mfma else "hbm", "achieved": round(tflops if mfma else gbps, 1),
@@ -186,6 +199,7 @@ def side_measure(config, seed, steps, warmup, reps, kv=None):
         "sum_ctx": int(b.ctx.sum()), "bytes_per_layer": nbytes, "flops_per_layer": flops,
         "step_us": round(us, 3), "step_roofline": roof(us),
         "kernel_us": round(kus, 3), "kernel_roofline": roof(kus),
+        "paged_read_ceiling": paged,
         "kernel": ("append_kernel + " if fp8 else "") +
                   ("wide_kernel (prefill)" if mfma else "attention_kernel (decode, fused append)"
                    if not fp8 else "attention_kernel (decode)"),

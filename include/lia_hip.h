@@ -393,17 +393,19 @@ int lia_attention_partial_append_fp8(const lia_attention_config *config, uint32_
  * The memory access of one lia_attention_partial launch on its own: over the plan already in
  * `workspace` (lia_attention_plan or lia_pack_plan_device), the same workgroups, block ranges,
  * K/V loads and pipeline waits as the decode kernel, with the attention arithmetic, the
- * score exchange and the outputs left out.  Each wave writes the XOR of the K words it loaded
+ * score exchange and the outputs left out.  Each wave writes the XOR of the words it loaded
  * to sink[workgroup * (head_dim / 64) + wave]; the XOR of all sink words is the XOR of every
- * attended key's K words.  No counterpart in the reference: it measures the rate of the
- * kernel's own paged access pattern, the ceiling the decode kernel is compared with.
- * 16-bit pools and batches served by the decode kernel (LIA_E_UNSUPPORTED otherwise); sink
- * 4-byte aligned and at least lia_paged_read_sink_words(config) words.
+ * attended key's K words, and on FP8 pools of its V words too (16-bit pools load V straight
+ * into LDS).  No counterpart in the reference: it measures the rate of the kernel's own
+ * paged access pattern, the ceiling the decode kernel is compared with.  Batches served by
+ * the decode kernel (LIA_E_UNSUPPORTED for a prefill batch); FP8 pools take their scales as
+ * lia_attention_partial does; sink 4-byte aligned and at least
+ * lia_paged_read_sink_words(config) words.
  */
 int lia_paged_read(const lia_attention_config *config, uint32_t n_seqs, uint32_t n_rows,
                    const uint32_t *pages, const void *q, const void *kc, const void *vc,
-                   void *workspace, size_t workspace_bytes, uint32_t *sink, size_t sink_words,
-                   lia_stream_t stream);
+                   const float *k_scales, const float *v_scales, void *workspace,
+                   size_t workspace_bytes, uint32_t *sink, size_t sink_words, lia_stream_t stream);
 
 /* Words of the sink lia_paged_read needs for a configuration (0 for an invalid one). */
 size_t lia_paged_read_sink_words(const lia_attention_config *config);

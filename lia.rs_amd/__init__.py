@@ -170,8 +170,8 @@ EXPORTS = {
                                       C.c_void_p, C.c_size_t, C.c_void_p, C.c_void_p]),
     "lia_hbm_read": (C.c_int, [C.c_void_p, C.c_size_t, C.c_uint32, C.c_void_p, C.c_void_p]),
     "lia_paged_read": (C.c_int, [C.POINTER(AttentionConfig), C.c_uint32, C.c_uint32, C.c_void_p,
-                                 C.c_void_p, C.c_void_p, C.c_void_p, C.c_void_p, C.c_size_t,
-                                 C.c_void_p, C.c_size_t, C.c_void_p]),
+                                 C.c_void_p, C.c_void_p, C.c_void_p, C.c_void_p, C.c_void_p,
+                                 C.c_void_p, C.c_size_t, C.c_void_p, C.c_size_t, C.c_void_p]),
     "lia_paged_read_sink_words": (C.c_size_t, [C.POINTER(AttentionConfig)]),
     "lia_kv_page_bytes": (C.c_size_t, [C.POINTER(KVLayout), C.c_uint32]),
     "lia_kv_transfer_bytes": (C.c_size_t, [C.POINTER(KVLayout), C.c_uint32]),
@@ -813,13 +813,15 @@ def paged_read_sink_words(config):
     return lib().lia_paged_read_sink_words(C.byref(config))
 
 
-def paged_read(config, n_seqs, pages, q, kc, vc, sink, workspace, stream=None):
+def paged_read(config, n_seqs, pages, q, kc, vc, sink, workspace, k_scales=None, v_scales=None,
+               stream=None):
     """The decode kernel's loads over the planned work list without the attention arithmetic
     (lia_paged_read): the ceiling of its own access pattern.  sink: int32 device tensor of at
     least paged_read_sink_words(config) words."""
     st = lib().lia_paged_read(C.byref(config), n_seqs, q.shape[0], _dptr(pages), _dptr(q), _dptr(kc),
-                              _dptr(vc), _dptr(workspace), workspace.numel() * workspace.element_size(),
-                              _dptr(sink), sink.numel(), _stream(stream))
+                              _dptr(vc), _dptr(k_scales), _dptr(v_scales), _dptr(workspace),
+                              workspace.numel() * workspace.element_size(), _dptr(sink), sink.numel(),
+                              _stream(stream))
     _check(st, "paged_read")
 
 

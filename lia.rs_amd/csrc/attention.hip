@@ -1107,20 +1107,31 @@ __device__ __forceinline__ void compute_chunk(const AttnParams &p, const Chunk<D
     }
 }
 
-// The read-only variant's chunk t: wait for the chunk's loads as compute_chunk does and fold
-// the K words of its keys inside the range, with no attention arithmetic, score exchange or
-// barrier.  Lane (g, li) holds key t + 16j + li of tile j.
+// The read-only variant's chunk t: wait for the chunk's loads as compute_chunk does, pass the
+// per-chunk barrier that keeps the workgroup's waves in step (on FP8 pools the two waves' K
+// slices share each 128-byte line: without it the waves drift apart and a line is fetched
+// twice), and fold the loaded words of its keys inside the range, with no attention arithmetic
+// or score exchange.  Lane (g, li) holds K of key t + 16j + li of tile j; on FP8 pools, whose V
+// comes through registers, it also holds V of key t + 16j + TPI * wave + lane / CPT (16-bit
+// pools load V straight into LDS, which nothing reads here).
 template <int D, int NT, int KVT, int VW = kLoadsPerChunk<D, KVT>>
-__device__ __forceinline__ void fold_chunk(const Chunk<D, KVT> &c, uint32_t t, State<D, NT, KVT> &st) {
-    wait_vmcnt<VW>();
-    const uint32_t li = lane_id() & 15;
+__device__ __forceinline__ void fold_chunk(const Chunk<D, KVT> &c, uint32_t t, State<D, NT, KVT> &st,
+                                           uint32_t wave) {
+    using C = Cfg<D, KVT>;
+    if constexpr (!C::FP8) wait_vmcnt<VW>(); // V in LDS; register loads are waited for on use
+    lds_barrier();
+    const uint32_t lane = lane_id(), li = lane & 15;
+    auto in = [&](uint32_t key) { return key >= st.lo && key < st.fold_hi; };
 #pragma unroll
     for (int j = 0; j < 2; j++) {
         uint32_t x = 0;
 #pragma unroll
-        for (int w = 0; w < Cfg<D, KVT>::KW; w++) x ^= c.k[j][w];
-        const uint32_t key = t + 16 * j + li;
-        st.fold ^= key >= st.lo && key < st.fold_hi ? x : 0u;
+        for (int w = 0; w < C::KW; w++) x ^= c.k[j][w];
+        st.fold ^= in(t + 16 * j + li) ? x : 0u;
+        if constexpr (C::FP8) {
+            const uint32_t y = c.v[j].x ^ c.v[j].y ^ c.v[j].z ^ c.v[j].w;
+            st.fold ^= in(t + 16 * j + C::TPI * wave + lane / C::CPT) ? y : 0u;
+        }
     }
 }
 
@@ -1136,7 +1147,7 @@ __device__ __forceinline__ void pipeline_step(const AttnParams &p, Chunk<D, KVT>
                                               const uint8_t *vbase, const DecLanes<D, KVT> &ln,
                                               uint32_t wave, State<D, NT, KVT> &st, f32x4 *sx) {
     load_chunk<D, KVT, kVAux<NT>>(p, cn, tn, tpn, kbase, vbase, ln, sn);
-    if constexpr (RO) fold_chunk<D, NT, KVT>(cc, tc, st);
+    if constexpr (RO) fold_chunk<D, NT, KVT>(cc, tc, st, wave);
     else compute_chunk<D, NT, KVT>(p, cc, tc, st, sc, sx, wave);
 }
 
@@ -1289,8 +1300,8 @@ constexpr int kMinWavesPerEU = KVT == LIA_FP8_E4M3 ? 2 : 3;
 // The workgroup-size bound (D/32 waves) is looser than the D/SW waves launched: the
 // exact bound changes register allocation and measured 1 % slower on a batch-8 bf16 decode.
 //
-// RO (lia_paged_read): the same plan, ranges, loads, pipeline and waits with the attention
-// arithmetic, the score exchange and every store but one left out - each wave folds the K words
+// RO (lia_paged_read): the same plan, ranges, loads, pipeline, waits and per-chunk barrier with
+// the attention arithmetic, the score exchange and every store but one left out - each wave folds the K words
 // it loaded and writes the fold to ((uint32_t *)p.out)[wg * waves + wave].  It times the
 // kernel's own memory access on its own.
 template <int D, int NT, int KVT, bool RO = false>
@@ -2664,11 +2675,11 @@ static hipError_t launch_wide(int kv, const AttnParams &p, uint32_t n_wg, hipStr
     return launch<wide_kernel<D, LIA_FP8_E4M3>>(dim3(n_wg), block, 0, s, p);
 }
 
-template <int D, int NT>
+template <int D, int NT, bool RO = false>
 static hipError_t launch_partial_kv(int kv, const AttnParams &p, uint32_t n_wg, hipStream_t s) {
-    if (kv == LIA_BF16) return launch_partial<D, NT, LIA_BF16>(p, n_wg, s);
-    if (kv == LIA_F16) return launch_partial<D, NT, LIA_F16>(p, n_wg, s);
-    return launch_partial<D, NT, LIA_FP8_E4M3>(p, n_wg, s);
+    if (kv == LIA_BF16) return launch_partial<D, NT, LIA_BF16, RO>(p, n_wg, s);
+    if (kv == LIA_F16) return launch_partial<D, NT, LIA_F16, RO>(p, n_wg, s);
+    return launch_partial<D, NT, LIA_FP8_E4M3, RO>(p, n_wg, s);
 }
 
 enum Stage { kPlan = 1, kPartial = 2, kMerge = 4, kRead = 8 };
@@ -2809,15 +2820,11 @@ static int run_stages(int stages, const lia_attention_config *c, uint32_t n_seqs
     if (e == hipSuccess && (stages & kRead)) {
         // the decode kernel's loads alone (lia_paged_read): 16-bit pools, decode tiles
         if (c->head_dim == 128) {
-            if (NT == 1) e = c->kv_dtype == LIA_BF16 ? launch_partial<128, 1, LIA_BF16, true>(p, n_wg, s)
-                                                     : launch_partial<128, 1, LIA_F16, true>(p, n_wg, s);
-            else e = c->kv_dtype == LIA_BF16 ? launch_partial<128, 2, LIA_BF16, true>(p, n_wg, s)
-                                             : launch_partial<128, 2, LIA_F16, true>(p, n_wg, s);
+            if (NT == 1) e = launch_partial_kv<128, 1, true>(c->kv_dtype, p, n_wg, s);
+            else e = launch_partial_kv<128, 2, true>(c->kv_dtype, p, n_wg, s);
         } else {
-            if (NT == 1) e = c->kv_dtype == LIA_BF16 ? launch_partial<64, 1, LIA_BF16, true>(p, n_wg, s)
-                                                     : launch_partial<64, 1, LIA_F16, true>(p, n_wg, s);
-            else e = c->kv_dtype == LIA_BF16 ? launch_partial<64, 2, LIA_BF16, true>(p, n_wg, s)
-                                             : launch_partial<64, 2, LIA_F16, true>(p, n_wg, s);
+            if (NT == 1) e = launch_partial_kv<64, 1, true>(c->kv_dtype, p, n_wg, s);
+            else e = launch_partial_kv<64, 2, true>(c->kv_dtype, p, n_wg, s);
         }
     }
     if (e == hipSuccess && (stages & kMerge)) {
@@ -2961,24 +2968,24 @@ extern "C" int lia_attention_partial_append_fp8(const lia_attention_config *c, u
 
 // The memory access of one lia_attention_partial launch on its own: the plan in `workspace`, the
 // same workgroups, block ranges, loads and pipeline waits, without the attention arithmetic.
-// Each wave writes the XOR of the K words it loaded to sink[workgroup * waves + wave] (the
-// XOR of all sink words is the XOR of every attended key's K words).  16-bit pools and decode
-// tiles only (batches the decode kernel serves).
+// Each wave writes the XOR of the words it loaded to sink[workgroup * waves + wave]: the XOR of
+// all sink words is the XOR of every attended key's K words (and V words on FP8 pools).
+// Batches the decode kernel serves only.
 extern "C" int lia_paged_read(const lia_attention_config *c, uint32_t n_seqs, uint32_t n_rows,
                               const uint32_t *pages, const void *q, const void *kc, const void *vc,
-                              void *workspace, size_t workspace_bytes, uint32_t *sink,
-                              size_t sink_words, lia_stream_t stream) {
+                              const float *k_scales, const float *v_scales, void *workspace,
+                              size_t workspace_bytes, uint32_t *sink, size_t sink_words,
+                              lia_stream_t stream) {
     static const uint32_t dummy = 0;
     int st = validate(c);
     if (st) return st;
-    if (c->kv_dtype == LIA_FP8_E4M3) return LIA_E_UNSUPPORTED;
     if (n_seqs == 0 || n_seqs > c->max_seqs || n_rows == 0 || n_rows > c->max_rows) return LIA_E_ARG;
     const uint32_t group = c->num_q_heads / c->num_kv_heads;
     if (nt_for(n_rows, n_seqs, group, c->kv_dtype) == kWideNT) return LIA_E_UNSUPPORTED;
     if (!sink) return LIA_E_ARG;
     if (sink_words < lia_paged_read_sink_words(c)) return LIA_E_ARG;
-    return run_stages(kRead, c, n_seqs, n_rows, &dummy, &dummy, nullptr, pages, q, kc, vc, nullptr,
-                      nullptr, workspace, workspace_bytes, sink, stream);
+    return run_stages(kRead, c, n_seqs, n_rows, &dummy, &dummy, nullptr, pages, q, kc, vc, k_scales,
+                      v_scales, workspace, workspace_bytes, sink, stream);
 }
 
 extern "C" size_t lia_paged_read_sink_words(const lia_attention_config *c) {

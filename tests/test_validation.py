@@ -202,8 +202,8 @@ def _read(lia, cfg, a, sink=A, sink_words=None):
     p = lambda x: None if x is None else C.c_void_p(x)
     words = lia.lib().lia_paged_read_sink_words(C.byref(cfg)) if sink_words is None else sink_words
     return lia.lib().lia_paged_read(C.byref(cfg), a["n_seqs"], a["n_rows"], p(a["pages"]), p(a["q"]),
-                                    p(a["kc"]), p(a["vc"]), p(a["ws"]), a["ws_bytes"], p(sink), words,
-                                    None)
+                                    p(a["kc"]), p(a["vc"]), p(a["ks"]), p(a["vs"]), p(a["ws"]),
+                                    a["ws_bytes"], p(sink), words, None)
 
 
 def test_paged_read_sink_words(lia):
@@ -215,7 +215,7 @@ def test_paged_read_sink_words(lia):
 
 
 @pytest.mark.parametrize("case,expect", [
-    ("fp8", E_UNSUPPORTED),          # FP8 pools: the decode kernel loads V through registers
+    ("fp8", E_ARG),                  # an FP8 pool without its scales
     ("prefill", E_UNSUPPORTED),      # a batch the prefill kernel serves
     ("no_sink", E_ARG),
     ("short_sink", E_ARG),
