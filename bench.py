@@ -74,15 +74,20 @@ SIDE_NAMES = {3: "mixed chunked-prefill + decode attention step", 4: "MTP-verify
               5: "FP8-KV decode attention step"}
 
 
-def side_measure(config, seed, steps, warmup, reps, kv=None):
+def side_measure(config, seed, steps, warmup, reps, kv=None, layers=40):
     """One layer of BASELINE config 3 (mixed prefill + decode, MFMA-bound), 4 (MTP verify) or
     5 (FP8 decode) on resident synthetic data, timed as a step of its own: device packing,
     the plan, the KV append of the step's rows (fused into the attention launch on 16-bit
     pools; on FP8 pools quantised by the append launch of the same call, just before the
     attention launch), split attention and the combine, replayed from a graph (`reps` steps
     per graph).  The attention launch alone is timed the same way (a graph of `reps` launches
-    on one plan).  Returns the step and kernel times with their rooflines: MFMA for config 3,
-    HBM (and MFMA) for configs 4 and 5, against the layer's algorithmic work."""
+    on one plan).  Every layer has its own KV pool, queries and rows, and the `reps` steps or
+    launches of a graph go to `reps` different layers, so no timed launch re-reads a pool the
+    256 MB last-level cache may still hold (config 3's pool is 101 MB, config 4's 274 MB).
+    Returns the step and kernel times with their rooflines: MFMA for config 3, HBM (and MFMA)
+    for configs 4 and 5, against the layer's algorithmic work.  It also times a model step as
+    config 2's is: the packing and plan once, then per layer the attention launch and the
+    combine, `layers` layers in one graph; reported per layer."""
     import torch
     from __graft_entry__ import package
     lia = package()
@@ -98,19 +103,25 @@ def side_measure(config, seed, steps, warmup, reps, kv=None):
     gen.manual_seed(seed)
     fp8 = g.kv_dtype == lia.FP8
     rows = b.n_rows
-    if fp8:
-        kp = torch.randint(0, 120, (tokens, g.hkv, g.d), generator=gen, dtype=torch.uint8, device=dev)
-        vp = torch.randint(0, 120, (tokens, g.hkv, g.d), generator=gen, dtype=torch.uint8, device=dev)
-        ks = torch.full((b.pool_pages * g.hkv,), 0.01, device=dev)
-        vs = ks.clone()
-    else:
-        kp = torch.randn((tokens, g.hkv, g.d), generator=gen, device=dev).to(torch.bfloat16)
-        vp = torch.randn((tokens, g.hkv, g.d), generator=gen, device=dev).to(torch.bfloat16)
-        ks = vs = None
-    newk = torch.randn((rows, g.hkv * g.d), generator=gen, device=dev).to(torch.bfloat16)
-    newv = torch.randn((rows, g.hkv * g.d), generator=gen, device=dev).to(torch.bfloat16)
-    q = torch.randn((rows, g.hq, g.d), generator=gen, device=dev).to(torch.bfloat16)
-    out = torch.empty((rows, g.hq, g.d), dtype=torch.bfloat16, device=dev)
+    reps = max(reps, 1)
+    L = max(layers, reps)
+
+    def layer():
+        if fp8:
+            kp = torch.randint(0, 120, (tokens, g.hkv, g.d), generator=gen, dtype=torch.uint8, device=dev)
+            vp = torch.randint(0, 120, (tokens, g.hkv, g.d), generator=gen, dtype=torch.uint8, device=dev)
+        else:
+            kp = torch.randn((tokens, g.hkv, g.d), generator=gen, device=dev).to(torch.bfloat16)
+            vp = torch.randn((tokens, g.hkv, g.d), generator=gen, device=dev).to(torch.bfloat16)
+        return dict(kp=kp, vp=vp,
+                    newk=torch.randn((rows, g.hkv * g.d), generator=gen, device=dev).to(torch.bfloat16),
+                    newv=torch.randn((rows, g.hkv * g.d), generator=gen, device=dev).to(torch.bfloat16),
+                    q=torch.randn((rows, g.hq, g.d), generator=gen, device=dev).to(torch.bfloat16),
+                    out=torch.empty((rows, g.hq, g.d), dtype=torch.bfloat16, device=dev))
+
+    pools = [layer() for _ in range(L)]
+    ks = torch.full((b.pool_pages * g.hkv,), 0.01, device=dev) if fp8 else None
+    vs = ks.clone() if fp8 else None
     i32 = lambda a: torch.from_numpy(np.asarray(a, np.uint32).view(np.int32)).to(dev)
     seq_slots, q_lens, cached = i32(np.arange(b.n_seqs)), i32(b.q_len), i32(b.cached)
     flat = i32(b.flat_table())
@@ -123,27 +134,35 @@ def side_measure(config, seed, steps, warmup, reps, kv=None):
                               g.out_dtype, g.scale, b.n_seqs, rows, int(b.ctx.max()))
     ws = torch.zeros(lia.workspace_bytes(cfg), dtype=torch.uint8, device=dev)
     context = b.stride * P
-    reps = max(reps, 1)
 
-    def attend():
-        if fp8:
-            lia.attention_partial_append_fp8(cfg, b.n_seqs, flat, slots, q, newk, newv, kp, vp, ks, vs,
-                                             out, ws)
-        else:
-            lia.attention_partial_append(cfg, b.n_seqs, flat, slots, q, newk, newv, kp, vp, out, ws)
-
-    def step():
+    def pack():
         lia.pack_plan_device(cfg, seq_slots, q_lens, cached, flat, rows, context, cu, positions,
                              sequences, slots, status, ws)
-        attend()
-        lia.attention_merge(cfg, b.n_seqs, rows, out, ws)
 
-    def timed(body):
+    def attend(i):
+        t = pools[i]
+        if fp8:
+            lia.attention_partial_append_fp8(cfg, b.n_seqs, flat, slots, t["q"], t["newk"], t["newv"],
+                                             t["kp"], t["vp"], ks, vs, t["out"], ws)
+        else:
+            lia.attention_partial_append(cfg, b.n_seqs, flat, slots, t["q"], t["newk"], t["newv"],
+                                         t["kp"], t["vp"], t["out"], ws)
+
+    def merge(i):
+        lia.attention_merge(cfg, b.n_seqs, rows, pools[i]["out"], ws)
+
+    def step(i):
+        pack()
+        attend(i)
+        merge(i)
+
+    def timed(body, n=reps):
+        """Average time of body(i) over graphs of n calls on layers 0 .. n-1."""
         graph, stream = torch.cuda.CUDAGraph(), torch.cuda.Stream()
         with torch.cuda.stream(stream):
             with torch.cuda.graph(graph, stream=stream):
-                for _ in range(reps):
-                    body()
+                for i in range(n):
+                    body(i)
         for _ in range(max(warmup, 1)):
             graph.replay()
         torch.cuda.synchronize()
@@ -154,9 +173,9 @@ def side_measure(config, seed, steps, warmup, reps, kv=None):
             graph.replay()
         e1.record(cur)
         torch.cuda.synchronize()
-        return e0.elapsed_time(e1) * 1e3 / (steps * reps)
+        return e0.elapsed_time(e1) * 1e3 / (steps * n)
 
-    step()
+    step(0)
     torch.cuda.synchronize()
     if status.item() != 0:
         raise RuntimeError(f"device packing failed: status {status.item()}")
@@ -174,13 +193,28 @@ def side_measure(config, seed, steps, warmup, reps, kv=None):
     paged = None
     if not mfma:
         sink = torch.zeros(lia.paged_read_sink_words(cfg), dtype=torch.int32, device=dev)
-        rus = timed(lambda: lia.paged_read(cfg, b.n_seqs, flat, q, kp, vp, sink, ws, ks, vs))
-        aus = timed(lambda: lia.attention_partial(cfg, b.n_seqs, flat, q, kp, vp, out, ws, ks, vs)) \
+        rus = timed(lambda i: lia.paged_read(cfg, b.n_seqs, flat, pools[i]["q"], pools[i]["kp"],
+                                             pools[i]["vp"], sink, ws, ks, vs))
+        aus = timed(lambda i: lia.attention_partial(cfg, b.n_seqs, flat, pools[i]["q"], pools[i]["kp"],
+                                                    pools[i]["vp"], pools[i]["out"], ws, ks, vs)) \
             if fp8 else kus
         rbytes = b.algorithmic_bytes()
         paged = {"us": round(rus, 3), "GBps": round(rbytes / (rus * 1e-6) / 1e9, 1),
                  "frac_of_peak": round(rbytes / (rus * 1e-6) / 1e9 / PEAK_HBM_GBPS, 4),
                  "attention_us": round(aus, 3), "kernel_frac_of_paged_read": round(rus / aus, 4)}
+
+    # a model step: the batch's packing and plan once, then every layer over its own pool
+    model = None
+    if layers > 1:
+        def model_step(_):
+            pack()
+            for i in range(layers):
+                attend(i)
+                merge(i)
+
+        mus = timed(model_step, 1) / layers
+        model = {"layers": layers, "step_us": round(mus * layers, 3), "per_layer_us": round(mus, 3)}
+    del pools
 
     def roof(t_us):
         gbps, tflops = nbytes / (t_us * 1e-6) / 1e9, flops / (t_us * 1e-6) / 1e12
@@ -200,6 +234,7 @@ def side_measure(config, seed, steps, warmup, reps, kv=None):
         "step_us": round(us, 3), "step_roofline": roof(us),
         "kernel_us": round(kus, 3), "kernel_roofline": roof(kus),
         "paged_read_ceiling": paged,
+        "model_step": dict(model, roofline=roof(model["per_layer_us"])) if model else None,
         "kernel": ("append_kernel + " if fp8 else "") +
                   ("wide_kernel (prefill)" if mfma else "attention_kernel (decode, fused append)"
                    if not fp8 else "attention_kernel (decode)"),
