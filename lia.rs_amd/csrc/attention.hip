@@ -853,10 +853,13 @@ __device__ __forceinline__ TileSpan tile_span(const TilePages &tp, int j, uint32
 }
 
 // Cache policy of the direct-to-LDS V loads of a 16-bit pool for NT column tiles: non-temporal
-// for single-row units (decode), the default for two-tile units (MTP verify and short chunks).
-// Measured: the default policy made config 4 1.7 % faster and config 2 5 % slower.
+// (every key is read once) for single-row units (decode) and two-tile units (MTP verify, short
+// chunks) alike.  Measured with every launch on its own layer's pool: config 4 attention 53.6 ->
+// 51.0-51.4 us against the default policy, which costs config 2 5 %.  (The default policy had
+// measured 1.7 % faster on config 4 when one layer's 274 MB pool was replayed, partly from the
+// last-level cache.)
 template <int NT>
-constexpr int kVAux = NT == 1 ? 2 : 0;
+constexpr int kVAux = 2;
 
 // Loads chunk t (32 tokens, t a multiple of 32) of this wave's d slice from the planes at
 // kbase / vbase (the pool, or the step's new rows).  Every load is issued unconditionally:
