@@ -141,3 +141,85 @@ def test_random_step_device_packing_fused_append(lia, wl, i):
     assert np.all(np.isfinite(got)), i
     tol_max, tol_mean = TOL[g.kv_dtype]
     assert mx < tol_max and mean < tol_mean, (i, kind, mx, mean)
+
+
+FP8_STEP_CASES = 16
+
+
+@pytest.mark.parametrize("i", range(FP8_STEP_CASES))
+def test_random_fp8_step(lia, wl, O, i):
+    """The serving step on an FP8 pool for a random batch: device packing with the plan beside it,
+    lia_attention_partial_append_fp8 (the step's bf16 rows quantised into the pool with their
+    pages' scales, fresh pages taking scale 1, then attended) and the combine.  The packed
+    metadata must equal the host packing, the pool bytes and per-(page, head) scales must equal
+    what the oracle's lia_kv_append stores, and the output is held to the FP8 bar against the
+    float64 oracle over the pool after the append."""
+    import torch
+    kind, b0 = draw_case(wl, 200 + i)
+    g0 = b0.geom
+    g = wl.Geometry(hq=g0.hq, hkv=g0.hkv, d=g0.d, page_size=g0.page_size, kv_dtype=FP8, q_dtype=BF16,
+                    out_dtype=g0.out_dtype)
+    b = wl.custom(b0.ctx, b0.q_len, geom=g, seed=200 + i, pool_slack=8)
+    P, W = g.page_size, g.hkv * g.d
+    print(f"[case] fp8 step {i} {kind}: d={g.d} hq={g.hq} hkv={g.hkv} page={P} out={g.out_dtype} "
+          f"seqs={b.n_seqs} rows={b.n_rows} ctx={b.ctx.tolist()[:6]} q_len={b.q_len.tolist()[:6]}",
+          flush=True)
+    rng = np.random.default_rng(300 + i)
+    tokens = b.pool_pages * P
+    layout = O.KVLayout(g.hkv, g.d, P, b.pool_pages, FP8)
+    kc = np.zeros(tokens * W, np.uint8)
+    vc = np.zeros_like(kc)
+    ks = np.zeros(b.pool_pages * g.hkv, np.float32)
+    vs = np.zeros_like(ks)
+    # pages holding cached keys are quantised from float pages; pages holding only new rows stay
+    # fresh (scale 0) for the append to initialise
+    cached_pages = sorted({int(t[lp]) for s, t in enumerate(b.tables)
+                           for lp in range(-(-int(b.cached[s]) // P))})
+    if cached_pages:
+        ids = np.array(cached_pages, np.uint32)
+        kf = rng.standard_normal((len(ids), P, g.hkv, g.d)).astype(np.float32)
+        vf = rng.standard_normal((len(ids), P, g.hkv, g.d)).astype(np.float32)
+        O.kv_quantize_pages(layout, ids, kf, vf, kc, vc, ks, vs)
+    newk = O.from_f32(rng.standard_normal((b.n_rows, W)).astype(np.float32), BF16)
+    newv = O.from_f32(rng.standard_normal((b.n_rows, W)).astype(np.float32), BF16)
+    kexp, vexp, ksx, vsx = kc.copy(), vc.copy(), ks.copy(), vs.copy()
+    O.kv_append(layout, b.positions(), b.sequences(), b.flat_table(), b.stride, newk, newv, kexp,
+                vexp, src_dtype=BF16, k_scales=ksx, v_scales=vsx)
+    dkc, dvc = G.to_dev(kc, torch.uint8), G.to_dev(vc, torch.uint8)
+    dks, dvs = G.to_dev(ks), G.to_dev(vs)
+    qf = O.from_f32(rng.standard_normal((b.n_rows, g.hq, g.d)).astype(np.float32), BF16)
+    cfg = lia.AttentionConfig(g.hq, g.hkv, g.d, P, b.pool_pages, b.stride, g.q_dtype, g.kv_dtype,
+                              g.out_dtype, g.scale, b.n_seqs, b.n_rows, int(b.ctx.max()))
+    ws = torch.zeros(lia.workspace_bytes(cfg), dtype=torch.uint8, device="cuda")
+    rows = b.n_rows
+    cu = torch.full((b.n_seqs + 1,), -1, dtype=torch.int32, device="cuda")
+    positions = torch.full((rows,), -1, dtype=torch.int32, device="cuda")
+    sequences = torch.full((rows,), -1, dtype=torch.int32, device="cuda")
+    slot_map = torch.full((rows,), -1, dtype=torch.int32, device="cuda")
+    status = torch.full((1,), -1, dtype=torch.int32, device="cuda")
+    flat = G.u32_dev(b.flat_table())
+    lia.pack_plan_device(cfg, G.u32_dev(np.arange(b.n_seqs)), G.u32_dev(b.q_len), G.u32_dev(b.cached),
+                         flat, rows, b.stride * P, cu, positions, sequences, slot_map, status, ws)
+    odt = torch.float32 if g.out_dtype == F32 else torch.bfloat16
+    out = torch.full((rows, g.hq, g.d), float("nan"), dtype=odt, device="cuda")
+    lia.attention_partial_append_fp8(cfg, b.n_seqs, flat, slot_map, G.to_dev(qf, torch.bfloat16),
+                                     G.to_dev(newk, torch.bfloat16), G.to_dev(newv, torch.bfloat16),
+                                     dkc, dvc, dks, dvs, out, ws)
+    lia.attention_merge(cfg, b.n_seqs, rows, out, ws)
+    torch.cuda.synchronize()
+    assert status.item() == 0
+    u32 = lambda t: t.cpu().numpy().view(np.uint32)
+    assert np.array_equal(u32(cu), b.cu_seqlens())
+    assert np.array_equal(u32(positions), b.positions())
+    assert np.array_equal(u32(sequences), b.sequences())
+    assert np.array_equal(u32(slot_map), b.slot_mapping())
+    assert np.array_equal(dks.cpu().numpy(), ksx) and np.array_equal(dvs.cpu().numpy(), vsx)
+    assert np.array_equal(dkc.cpu().numpy(), kexp) and np.array_equal(dvc.cpu().numpy(), vexp)
+    geom = O.geom(g.hq, g.hkv, g.d, P, b.stride, FP8, g.scale)
+    ref = O.attention_f64(geom, b.positions(), b.sequences(), b.flat_table(), O.to_f32(qf, BF16),
+                          kexp, vexp, ksx, vsx)
+    got = out.float().cpu().numpy()
+    mx, mean = G.errors(got, ref)
+    print(f"[case] fp8 step {i}: max_abs={mx:.3e} mean_abs={mean:.3e}", flush=True)
+    assert np.all(np.isfinite(got)), i
+    assert mx < TOL[FP8][0] and mean < TOL[FP8][1], (i, kind, mx, mean)
