@@ -1156,14 +1156,17 @@ __device__ __forceinline__ void pipeline_step(const AttnParams &p, Chunk<D, KVT>
 
 // Attends keys [s_lo, s_hi) of one source (coordinates of that source: token index in the
 // pool, or new-row index) into the running state.  Windows of at most 64 pages; the
-// first two chunks of the workgroup's first range take their pages from the plan.
-template <int D, int NT, int KVT, bool RO = false>
+// first two chunks of the workgroup's first range take their pages from the plan.  While
+// q_pending is set (single-tile units only), qload() loads the unit's queries right after the
+// first chunk's K/V loads and before the second's, so the stream starts without waiting for
+// the query addressing and the first chunk's wait covers the queries.
+template <int D, int NT, int KVT, bool RO = false, class QL>
 __device__ __forceinline__ void run_range(const AttnParams &p, const uint8_t *kbase,
                                           const uint8_t *vbase, const uint32_t *table,
                                           uint32_t s_lo, uint32_t s_hi, bool use_pre,
                                           uint4 pre, uint32_t hk, uint32_t wave, State<D, NT, KVT> &st,
                                           uint16_t *stage0, uint16_t *stage1, f32x4 *sxb,
-                                          uint32_t &parity) {
+                                          uint32_t &parity, bool &q_pending, const QL &qload) {
     using C = Cfg<D, KVT>;
     constexpr uint32_t SX = C::WAVES * NT * 2 * 64;
     const uint32_t shift = p.page_shift;
@@ -1188,6 +1191,12 @@ __device__ __forceinline__ void run_range(const AttnParams &p, const uint8_t *kb
             tp1 = tile_pages<C::FP8>(win, wbeg + 32, shift, wend);
         }
         load_chunk<D, KVT, kVAux<NT>>(p, c0, wbeg, tp0, kbase, vbase, ln, stage0);
+        if constexpr (NT == 1) {
+            if (q_pending) {
+                qload();
+                q_pending = false;
+            }
+        }
         pipeline_step<D, NT, KVT, RO>(p, c1, wbeg + 32, tp1, stage1, c0, wbeg, stage0, kbase, vbase, ln,
                                       wave, st, sxb + parity * SX);
         parity ^= 1;
@@ -1351,15 +1360,33 @@ __global__ __launch_bounds__(D / 32 * 64, kMinWavesPerEU<KVT>) void attention_ke
         State<D, NT, KVT> st;
         st.fold = 0;
         uint32_t climit[NT]; // per column: keys it attends (causal limit), 0 for padding
+        // the unit's queries: on single-tile units (decode) 16-bit queries are loaded by the first
+        // range after its first chunk's K/V loads (config 2: 19.3-19.6 -> 19.0-19.2 us); f32
+        // queries here, since their conversion waits for their loads (and would then wait for the
+        // first chunk's too), and on two-tile units too, where the deferred operands' registers
+        // made the kernel spill (config 4: 52.9 -> 57.3 us)
+        bool q_pending = NT == 1;
+        auto qload = [&]() {
+#pragma unroll
+            for (int nt = 0; nt < NT; nt++) {
+                const uint32_t col = nt * 16 + li;
+                const bool valid = col < ncols;
+                const uint32_t ri = valid ? col / p.group : 0;
+#pragma unroll
+                for (int ks = 0; ks < C::KS; ks++)
+                    st.qr[nt][ks] = load_q<D, KVT>(p, ud.rowbeg + ri, hk * p.group + col % p.group, valid, wave, ks);
+            }
+        };
+        if (!q_pending || p.q_f32) {
+            qload();
+            q_pending = false;
+        }
 #pragma unroll
         for (int nt = 0; nt < NT; nt++) {
             const uint32_t col = nt * 16 + li;
             const bool valid = col < ncols;
             const uint32_t ri = valid ? col / p.group : 0;
             climit[nt] = valid ? pos0 + ri + 1 : 0;
-#pragma unroll
-            for (int ks = 0; ks < C::KS; ks++)
-                st.qr[nt][ks] = load_q<D, KVT>(p, ud.rowbeg + ri, hk * p.group + col % p.group, valid, wave, ks);
             st.m[nt] = 0.0f;
             st.thr[nt] = -INFINITY;
             st.l[nt] = f32x4{0.0f, 0.0f, 0.0f, 0.0f};
@@ -1389,13 +1416,13 @@ __global__ __launch_bounds__(D / 32 * 64, kMinWavesPerEU<KVT>) void attention_ke
             const uint32_t r_lo = key_of(a), r_hi = min(key_of(e), kend);
             set_limits(r_lo, r_hi, 0);
             run_range<D, NT, KVT, RO>(p, kpool, vpool, table, r_lo, r_hi, use_pre, wd.pre, hk, wave, st,
-                                      stage0, stage1, sxb, parity);
+                                      stage0, stage1, sxb, parity, q_pending, qload);
         } else {
             if (a < cb) {
                 const uint32_t r_lo = 32 * a, r_hi = min(32 * min(e, cb), kcache);
                 set_limits(r_lo, r_hi, 0);
                 run_range<D, NT, KVT, RO>(p, kpool, vpool, table, r_lo, r_hi, use_pre, wd.pre, hk, wave,
-                                          st, stage0, stage1, sxb, parity);
+                                          st, stage0, stage1, sxb, parity, q_pending, qload);
             }
             if (e > cb) {
                 // new keys: row kcache + i of the sequence is packed row r0 + i
@@ -1405,7 +1432,7 @@ __global__ __launch_bounds__(D / 32 * 64, kMinWavesPerEU<KVT>) void attention_ke
                 run_range<D, NT, KVT, RO>(p, (const uint8_t *)p.newk + (size_t)r0 * row_bytes,
                                           (const uint8_t *)p.newv + (size_t)r0 * row_bytes, nullptr,
                                           r_lo, r_hi, false, wd.pre, hk, wave, st, stage0, stage1, sxb,
-                                          parity);
+                                          parity, q_pending, qload);
             }
         }
 
