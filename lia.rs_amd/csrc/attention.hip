@@ -1142,7 +1142,7 @@ __device__ __forceinline__ void fold_chunk(const Chunk<D, KVT> &c, uint32_t t, S
 // compute chunk `tc` from stage `sc` (registers cc).  The two stages are restrict
 // parameters: the transpose reads of `sc` are then known not to alias the direct-to-LDS
 // loads still in flight into `sn`, so no full vmcnt drain is needed before them.
-template <int D, int NT, int KVT, bool RO = false>
+template <int D, int NT, int KVT, bool RO = false, int VW = kLoadsPerChunk<D, KVT>>
 __device__ __forceinline__ void pipeline_step(const AttnParams &p, Chunk<D, KVT> &cn, uint32_t tn,
                                               const TilePages &tpn, uint16_t *__restrict__ sn,
                                               const Chunk<D, KVT> &cc, uint32_t tc,
@@ -1150,8 +1150,8 @@ __device__ __forceinline__ void pipeline_step(const AttnParams &p, Chunk<D, KVT>
                                               const uint8_t *vbase, const DecLanes<D, KVT> &ln,
                                               uint32_t wave, State<D, NT, KVT> &st, f32x4 *sx) {
     load_chunk<D, KVT, kVAux<NT>>(p, cn, tn, tpn, kbase, vbase, ln, sn);
-    if constexpr (RO) fold_chunk<D, NT, KVT>(cc, tc, st, wave);
-    else compute_chunk<D, NT, KVT>(p, cc, tc, st, sc, sx, wave);
+    if constexpr (RO) fold_chunk<D, NT, KVT, VW>(cc, tc, st, wave);
+    else compute_chunk<D, NT, KVT, VW>(p, cc, tc, st, sc, sx, wave);
 }
 
 // Attends keys [s_lo, s_hi) of one source (coordinates of that source: token index in the
@@ -1178,27 +1178,40 @@ __device__ __forceinline__ void run_range(const AttnParams &p, const uint8_t *kb
     for (uint32_t wbeg = s_lo & ~31u; wbeg < s_hi;) {
         const uint32_t wend = min(s_hi, ((wbeg >> shift) + 64) << shift);
         PageWindow win;
-        window_load<C::FP8>(p, win, table, wbeg >> shift, page_limit, hk);
         Chunk<D, KVT> c0, c1;
         // prologue: chunks wbeg and wbeg + 32 in flight, chunk wbeg computed
-        TilePages tp0, tp1;
-        if (!C::FP8 && use_pre) {
-            tp0 = tile_pages_pre(pre, wbeg >> shift, wbeg, shift, wend, p.pool_pages);
-            tp1 = tile_pages_pre(pre, wbeg >> shift, wbeg + 32, shift, wend, p.pool_pages);
+        if (!C::FP8 && use_pre && table) {
+            // the first two chunks' pages come from the plan: their loads (and the queries) go
+            // out first and the window's table load after them, before the second chunk's, so
+            // the first chunk's wait counts one more operation after its own
+            const TilePages tp0 = tile_pages_pre(pre, wbeg >> shift, wbeg, shift, wend, p.pool_pages);
+            const TilePages tp1 = tile_pages_pre(pre, wbeg >> shift, wbeg + 32, shift, wend, p.pool_pages);
             use_pre = false;
-        } else {
-            tp0 = tile_pages<C::FP8>(win, wbeg, shift, wend);
-            tp1 = tile_pages<C::FP8>(win, wbeg + 32, shift, wend);
-        }
-        load_chunk<D, KVT, kVAux<NT>>(p, c0, wbeg, tp0, kbase, vbase, ln, stage0);
-        if constexpr (NT == 1) {
-            if (q_pending) {
-                qload();
-                q_pending = false;
+            load_chunk<D, KVT, kVAux<NT>>(p, c0, wbeg, tp0, kbase, vbase, ln, stage0);
+            if constexpr (NT == 1) {
+                if (q_pending) {
+                    qload();
+                    q_pending = false;
+                }
             }
+            window_load<C::FP8>(p, win, table, wbeg >> shift, page_limit, hk);
+            pipeline_step<D, NT, KVT, RO, kLoadsPerChunk<D, KVT> + 1>(p, c1, wbeg + 32, tp1, stage1, c0, wbeg,
+                                                                      stage0, kbase, vbase, ln, wave, st,
+                                                                      sxb + parity * SX);
+        } else {
+            window_load<C::FP8>(p, win, table, wbeg >> shift, page_limit, hk);
+            const TilePages tp0 = tile_pages<C::FP8>(win, wbeg, shift, wend);
+            const TilePages tp1 = tile_pages<C::FP8>(win, wbeg + 32, shift, wend);
+            load_chunk<D, KVT, kVAux<NT>>(p, c0, wbeg, tp0, kbase, vbase, ln, stage0);
+            if constexpr (NT == 1) {
+                if (q_pending) {
+                    qload();
+                    q_pending = false;
+                }
+            }
+            pipeline_step<D, NT, KVT, RO>(p, c1, wbeg + 32, tp1, stage1, c0, wbeg, stage0, kbase, vbase, ln,
+                                          wave, st, sxb + parity * SX);
         }
-        pipeline_step<D, NT, KVT, RO>(p, c1, wbeg + 32, tp1, stage1, c0, wbeg, stage0, kbase, vbase, ln,
-                                      wave, st, sxb + parity * SX);
         parity ^= 1;
         if (wbeg + 32 < wend) {
             for (uint32_t t = wbeg + 32;; t += 64) {
