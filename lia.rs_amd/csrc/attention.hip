@@ -1180,7 +1180,9 @@ __device__ __forceinline__ void run_range(const AttnParams &p, const uint8_t *kb
         PageWindow win;
         Chunk<D, KVT> c0, c1;
         // prologue: chunks wbeg and wbeg + 32 in flight, chunk wbeg computed
-        if (!C::FP8 && use_pre && table) {
+        bool reorder = false; // single-tile units on 16-bit pools (two-tile units spill with both forms)
+        if constexpr (NT == 1 && !C::FP8) reorder = use_pre && table != nullptr;
+        if (reorder) {
             // the first two chunks' pages come from the plan: their loads (and the queries) go
             // out first and the window's table load after them, before the second chunk's, so
             // the first chunk's wait counts one more operation after its own
@@ -1188,11 +1190,9 @@ __device__ __forceinline__ void run_range(const AttnParams &p, const uint8_t *kb
             const TilePages tp1 = tile_pages_pre(pre, wbeg >> shift, wbeg + 32, shift, wend, p.pool_pages);
             use_pre = false;
             load_chunk<D, KVT, kVAux<NT>>(p, c0, wbeg, tp0, kbase, vbase, ln, stage0);
-            if constexpr (NT == 1) {
-                if (q_pending) {
-                    qload();
-                    q_pending = false;
-                }
+            if (q_pending) {
+                qload();
+                q_pending = false;
             }
             window_load<C::FP8>(p, win, table, wbeg >> shift, page_limit, hk);
             pipeline_step<D, NT, KVT, RO, kLoadsPerChunk<D, KVT> + 1>(p, c1, wbeg + 32, tp1, stage1, c0, wbeg,
@@ -1200,8 +1200,15 @@ __device__ __forceinline__ void run_range(const AttnParams &p, const uint8_t *kb
                                                                       sxb + parity * SX);
         } else {
             window_load<C::FP8>(p, win, table, wbeg >> shift, page_limit, hk);
-            const TilePages tp0 = tile_pages<C::FP8>(win, wbeg, shift, wend);
-            const TilePages tp1 = tile_pages<C::FP8>(win, wbeg + 32, shift, wend);
+            TilePages tp0, tp1;
+            if (!C::FP8 && use_pre) {
+                tp0 = tile_pages_pre(pre, wbeg >> shift, wbeg, shift, wend, p.pool_pages);
+                tp1 = tile_pages_pre(pre, wbeg >> shift, wbeg + 32, shift, wend, p.pool_pages);
+                use_pre = false;
+            } else {
+                tp0 = tile_pages<C::FP8>(win, wbeg, shift, wend);
+                tp1 = tile_pages<C::FP8>(win, wbeg + 32, shift, wend);
+            }
             load_chunk<D, KVT, kVAux<NT>>(p, c0, wbeg, tp0, kbase, vbase, ln, stage0);
             if constexpr (NT == 1) {
                 if (q_pending) {
