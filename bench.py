@@ -14,7 +14,15 @@ replays CUDA graphs of the paged forward, src/inference/paging.rs:238-259).
 value = decode tokens/s of the whole step (8 tokens per step).  The roofline object
 covers the dominant kernel (the split attention kernel), timed alone with HIP events on
 its stream; its algorithmic bytes are K/V of every attended key + Q + O + block table +
-the appended rows it writes.
+the appended rows it writes.  Beside it, the same run times two ceilings of those bytes:
+`read_ceiling`, a contiguous read (lia_hbm_read), and `paged_read_ceiling`, the kernel's own
+plan, loads and pipeline with the attention arithmetic left out (lia_paged_read).
+
+`side` holds configs 3, 4 and 5 (parity workloads, timed for the record): a one-layer step,
+the attention launch alone, for 4 and 5 the kernel's loads alone, and a 40-layer model step
+per layer; every layer has its own KV pool, so no timed launch re-reads a pool the 256 MB
+last-level cache could still hold.  `cpu_baseline` is the reference algorithm (the oracle's
+f32 split-K + merge) on the host cores, a bounded sample scaled to the step.
 """
 import argparse
 import json
