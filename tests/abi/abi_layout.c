@@ -67,6 +67,14 @@ static int calls(void) {
            slots[0], slots[1], slots[2], info.stride, info.n_groups);
     lia_attention_config c = {16, 2, 128, 16, 64, 4, LIA_BF16, LIA_BF16, LIA_BF16, 0.088f, 8, 8, 64};
     printf("workspace %zu\n", lia_attention_workspace_bytes(&c));
+    printf("sink_words %zu\n", lia_paged_read_sink_words(&c));
+    {
+        uint32_t sink = 0;
+        printf("read_no_sink %d\n", lia_paged_read(&c, 1, 1, flat, NULL, NULL, NULL, NULL, NULL, NULL, 0,
+                                                   NULL, 0, NULL));
+        printf("read_short_sink %d\n", lia_paged_read(&c, 1, 1, flat, NULL, NULL, NULL, NULL, NULL, NULL, 0,
+                                                      &sink, 1, NULL));
+    }
     c.head_dim = 96; /* no kernel for this geometry */
     printf("unsupported %d\n", lia_paged_attention(&c, 1, 1, cu, positions, sequences, flat, NULL,
                                                    NULL, NULL, NULL, NULL, NULL, 0, NULL, NULL));

@@ -92,5 +92,8 @@ def test_calls_from_c(abi_exe, lia):
     assert got["pack"] == "0 cu 0 2 3 slots 96 97 67 stride 4 groups 2"
     cfg = lia.AttentionConfig(16, 2, 128, 16, 64, 4, lia.BF16, lia.BF16, lia.BF16, 0.088, 8, 8, 64)
     assert int(got["workspace"]) == lia.workspace_bytes(cfg)
+    assert int(got["sink_words"]) == lia.paged_read_sink_words(cfg) > 0
+    assert lia.ERRORS[int(got["read_no_sink"])] == "invalid argument"     # LIA_E_ARG: no sink
+    assert lia.ERRORS[int(got["read_short_sink"])] == "invalid argument"  # LIA_E_ARG: sink too short
     assert lia.ERRORS[int(got["unsupported"])] == "unsupported geometry"  # LIA_E_UNSUPPORTED
     assert lia.ERRORS[int(got["null_config"])] == "invalid argument"      # LIA_E_ARG
