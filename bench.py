@@ -365,7 +365,7 @@ def main():
         return
     if args.gpus != 1 or int(os.environ.get("WORLD_SIZE", "1")) > 1:
         print("bench.py: this build measures one GPU only (the path shards by sequence / KV "
-              "head with no cross-GPU exchange; see DESIGN.md); run with --gpus 1",
+              "head with no cross-GPU exchange); run with --gpus 1",
               file=sys.stderr)
         sys.exit(2)
     import torch

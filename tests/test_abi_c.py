@@ -1,6 +1,7 @@
 """The C ABI from a C consumer: include/lia_hip.h compiled as C11 with -Wall -Werror, every
 struct's sizeof / offsetof compared with the ctypes structures of the Python binding and with
-the field order of the Rust #[repr(C)] block in INTEGRATION.md, and liblia_hip.so linked from C
+the field order of the Rust #[repr(C)] block of the integration guide (the Rust binding a
+maintainer adds on the reference side), and liblia_hip.so linked from C
 and called (host packing, workspace sizing, validation errors; no GPU work)."""
 import ctypes as C
 import os
@@ -68,7 +69,7 @@ def test_ctypes_structs_match_c(c_layout, lia):
 
 
 def _rust_structs():
-    """struct name -> field names in order, from the #[repr(C)] block of INTEGRATION.md."""
+    """struct name -> field names in order, from the integration guide's #[repr(C)] block."""
     text = open(os.path.join(ROOT, "INTEGRATION.md")).read()
     out = {}
     for m in re.finditer(r"#\[repr\(C\)\][^\n]*\n\s*pub struct (lia_\w+)\s*\{(.*?)\}\s*(?://[^\n]*)?\n",
