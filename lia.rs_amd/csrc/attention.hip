@@ -663,9 +663,9 @@ struct Cfg {
     static constexpr bool MBF16 = KVT == LIA_BF16;  // MFMA operand type (f16 for f16 and FP8)
     static constexpr int EB = FP8 ? 1 : 2;          // bytes per stored KV element
     // Each wave owns a head_dim slice of SW dims: 64 dims of a 16-bit pool (128 bytes of a
-    // token, two loads per tile), 64 dims of an FP8 pool (64 bytes).  A lane loads 16
-    // contiguous bytes of a token per 16-token tile and load (its A-operand k slots), so
-    // every load instruction reads 16 tokens x 64 bytes.
+    // token, two loads per tile of 8 tokens x 128 bytes each), 64 dims of an FP8 pool (64
+    // bytes, one load per tile of 16 tokens x 64 bytes).  A lane loads 16 contiguous bytes of
+    // a token per load.
     static constexpr int SW = 64;
     static constexpr int AUX = 2;           // cache policy of the K loads and FP8 V loads (nt)
     static constexpr int WAVES = D / SW;            // one wave per slice
@@ -805,14 +805,20 @@ __device__ __forceinline__ DecLanes<D, KVT> dec_lanes(uint32_t hk, uint32_t wave
     const uint32_t lane = lane_id(), g = lane >> 4, li = lane & 15;
     const uint32_t slice_off = (hk * D + C::SW * wave) * C::EB;
     DecLanes<D, KVT> r;
-    // K: lane (g, li) of a tile reads token li, bytes 16g .. 16g+15 of the wave's slice (the
-    // four groups of a token cover its 64-byte slice contiguously): dims 32w + 8g .. +7 of a
-    // 16-bit pool, dims 64w + 16g .. +15 of an FP8 pool (k slots 8g..8g+7 of k-step s hold
-    // dims 64w + 16g + 8s .. +7, and Q is loaded to match).  A 16-bit slice of 64 dims takes
-    // two loads per tile, bytes 64q + 16g (dims 32q + 8g .. +7 = k-step q), so each load
-    // instruction still reads 64 contiguous bytes of a token.
+    if constexpr (C::FP8) {
+        // K: lane (g, li) of a tile reads token li, bytes 16g .. 16g+15 of the wave's 64-byte
+        // slice: dims 64w + 16g .. +15 (k slots 8g..8g+7 of k-step s hold dims 64w + 16g + 8s
+        // .. +7, and Q is loaded to match)
+        r.k[0] = li * row_bytes + slice_off + 16 * g;
+    } else {
+        // K of a 16-bit pool (128-byte slices, two loads per tile): load q reads tokens
+        // 8q .. 8q+7 of the tile as whole slices, lane (g, li) token 8q + li%8, bytes
+        // 16(g + 4(li/8)) .. +15, so every load instruction reads whole lines; k_operand()
+        // moves the halves into the MFMA layout (token li, dims 32s + 8g .. +7 for k-step s)
 #pragma unroll
-    for (int q = 0; q < C::KL; q++) r.k[q] = li * row_bytes + slice_off + 64 * q + 16 * g;
+        for (int q = 0; q < C::KL; q++)
+            r.k[q] = (8 * q + (li & 7)) * row_bytes + slice_off + 16 * (g + 4 * (li >> 3));
+    }
     if constexpr (C::FP8) {
         // V as whole head rows: wave w reads tokens TPI*w .. +TPI-1 of each tile (lane l:
         // token TPI*w + l/CPT, bytes 16(l%CPT) .. +15 of the head's row)
@@ -961,6 +967,24 @@ struct State {
                       // range's first chunk also loads keys of the range before it)
 };
 
+// K operand of k-step ks of a 16-bit tile from the two whole-line loads L0 (tokens 0-7) and L1
+// (tokens 8-15): lane (g, li) of L0 holds token li%8, dims 8g .. +7 (li < 8) or 32 + 8g .. +7
+// (li >= 8), and L1 the same for tokens 8-15.  The operand wants token li, dims 32ks + 8g .. +7
+// in lane (g, li): k-step 0 keeps L0 in lanes li < 8 and takes L1 from lane li - 8 in the
+// others; k-step 1 keeps L1 in lanes li >= 8 and takes L0 from lane li + 8 in the others
+// (a row rotation by 8 written to half the banks of each row).
+template <int KS>
+__device__ __forceinline__ u32x4 k_operand(const uint32_t *k) {
+    constexpr int keep = KS == 0 ? 0 : 4, take = KS == 0 ? 4 : 0;
+    constexpr int banks = KS == 0 ? 0xC : 0x3; // lanes 8-15 / 0-7 of each row take the rotation
+    u32x4 a;
+#pragma unroll
+    for (int w = 0; w < 4; w++)
+        a[w] = (uint32_t)__builtin_amdgcn_update_dpp((int)k[keep + w], (int)k[take + w], 0x128 /* row_ror:8 */,
+                                                     0xF, banks, false);
+    return a;
+}
+
 // One chunk: partial scores for this wave's d slice, cross-wave sum through LDS, online
 // softmax (identical in every wave), O^T += V^T P^T for the wave's two 16-dim tiles.
 template <int D, int NT, int KVT, int VW = kLoadsPerChunk<D, KVT>>
@@ -1015,7 +1039,7 @@ __device__ __forceinline__ void compute_chunk(const AttnParams &p, const Chunk<D
                     u32x2 x1 = e4m3x4_to_f16x4_scaled(c.k[j][2 * ks + 1]);
                     a = u32x4{x0.x, x0.y, x1.x, x1.y};
                 } else {
-                    a = u32x4{c.k[j][4 * ks], c.k[j][4 * ks + 1], c.k[j][4 * ks + 2], c.k[j][4 * ks + 3]};
+                    a = ks == 0 ? k_operand<0>(c.k[j]) : k_operand<1>(c.k[j]);
                 }
                 sp = mfma16x16x32<C::MBF16>(a, st.qr[nt][ks], sp);
             }
@@ -1114,7 +1138,8 @@ __device__ __forceinline__ void compute_chunk(const AttnParams &p, const Chunk<D
 // per-chunk barrier that keeps the workgroup's waves in step (on FP8 pools the two waves' K
 // slices share each 128-byte line: without it the waves drift apart and a line is fetched
 // twice), and fold the loaded words of its keys inside the range, with no attention arithmetic
-// or score exchange.  Lane (g, li) holds K of key t + 16j + li of tile j; on FP8 pools, whose V
+// or score exchange.  Lane (g, li) holds K of key t + 16j + li of tile j on FP8 pools, and of
+// keys t + 16j + li%8 and t + 16j + 8 + li%8 (one per load) on 16-bit pools; on FP8 pools, whose V
 // comes through registers, it also holds V of key t + 16j + TPI * wave + lane / CPT (16-bit
 // pools load V straight into LDS, which nothing reads here).
 template <int D, int NT, int KVT, int VW = kLoadsPerChunk<D, KVT>>
@@ -1127,10 +1152,19 @@ __device__ __forceinline__ void fold_chunk(const Chunk<D, KVT> &c, uint32_t t, S
     auto in = [&](uint32_t key) { return key >= st.lo && key < st.fold_hi; };
 #pragma unroll
     for (int j = 0; j < 2; j++) {
-        uint32_t x = 0;
+        if constexpr (C::FP8) {
+            uint32_t x = 0;
 #pragma unroll
-        for (int w = 0; w < C::KW; w++) x ^= c.k[j][w];
-        st.fold ^= in(t + 16 * j + li) ? x : 0u;
+            for (int w = 0; w < C::KW; w++) x ^= c.k[j][w];
+            st.fold ^= in(t + 16 * j + li) ? x : 0u;
+        } else {
+            // load q holds token 8q + li%8 of the tile
+#pragma unroll
+            for (int q = 0; q < C::KL; q++) {
+                const uint32_t x = c.k[j][4 * q] ^ c.k[j][4 * q + 1] ^ c.k[j][4 * q + 2] ^ c.k[j][4 * q + 3];
+                st.fold ^= in(t + 16 * j + 8 * q + (li & 7)) ? x : 0u;
+            }
+        }
         if constexpr (C::FP8) {
             const uint32_t y = c.v[j].x ^ c.v[j].y ^ c.v[j].z ^ c.v[j].w;
             st.fold ^= in(t + 16 * j + C::TPI * wave + lane / C::CPT) ? y : 0u;
