@@ -681,6 +681,11 @@ struct Cfg {
     static constexpr int CPT = D * EB / 16;         // FP8: 16-byte chunks of a head's row
     static constexpr int TPI = 64 / CPT;            // FP8: tokens per V load (whole rows)
     static_assert(!FP8 || TPI * WAVES == 16, "the waves' V loads cover a 16-token tile");
+    // FP8 pools with two waves: K is loaded as whole 128-byte head rows too, wave w taking
+    // tokens 8w .. 8w+7 of each tile, and each wave forms the full scores of its own 16 tokens
+    // of the chunk (QS query operands: both halves of head_dim)
+    static constexpr bool KROW = FP8 && WAVES == 2;
+    static constexpr int QS = KROW ? 4 : KS;        // query operands per column tile
 };
 
 // Staged V rows hold 64 16-bit values (8 chunks of 16 bytes); chunk c of row r sits in slot
@@ -810,6 +815,11 @@ __device__ __forceinline__ DecLanes<D, KVT> dec_lanes(uint32_t hk, uint32_t wave
         // slice: dims 64w + 16g .. +15 (k slots 8g..8g+7 of k-step s hold dims 64w + 16g + 8s
         // .. +7, and Q is loaded to match)
         r.k[0] = li * row_bytes + slice_off + 16 * g;
+        if constexpr (C::KROW) {
+            // whole head rows: lane (g, li) reads token 8w + li%8, bytes 16(g + 4(li/8)) .. +15
+            // of the head's 128-byte row (dims 64h + 16g .. +15 with h = li/8)
+            r.k[0] = (8 * wave + (li & 7)) * row_bytes + hk * D + 16 * (g + 4 * (li >> 3));
+        }
     } else {
         // K of a 16-bit pool (128-byte slices, two loads per tile): load q reads tokens
         // 8q .. 8q+7 of the tile as whole slices, lane (g, li) token 8q + li%8, bytes
@@ -920,9 +930,12 @@ __device__ __forceinline__ u32x4 load_q(const AttnParams &p, uint32_t row, uint3
                                         bool valid, uint32_t wave, uint32_t s) {
     using C = Cfg<D, KVT>;
     const uint32_t g = lane_id() >> 4;
-    // FP8: a lane's 16 bytes hold dims 16g .. 16g+15 (k-steps 0, 1); 16-bit: load s holds
-    // dims 32s + 8g .. +7
-    const uint32_t at = (row * p.hq + head) * D + C::SW * wave + (C::FP8 ? 16 * g + 8 * s : 32 * s + 8 * g);
+    // FP8: a lane's 16 bytes hold dims 16g .. 16g+15 (k-steps 0, 1) of the wave's slice, or
+    // with whole-row K (KROW) operand s = 2h + k holds dims 64h + 16g + 8k .. +7 of the head;
+    // 16-bit: load s holds dims 32s + 8g .. +7 of the wave's slice
+    const uint32_t at = (row * p.hq + head) * D +
+                        (C::KROW ? 64 * (s >> 1) + 16 * g + 8 * (s & 1)
+                                 : C::SW * wave + (C::FP8 ? 16 * g + 8 * s : 32 * s + 8 * g));
     const uint32_t qb = p.q_f32 ? 4 : 2;
     const __amdgpu_buffer_rsrc_t r = make_rsrc(p.q, p.n_rows * p.hq * D * qb);
     const uint32_t off = valid ? at * qb : 0x80000000u;
@@ -949,7 +962,7 @@ __device__ __forceinline__ u32x4 load_q(const AttnParams &p, uint32_t row, uint3
 
 template <int D, int NT, int KVT>
 struct State {
-    u32x4 qr[NT][Cfg<D, KVT>::KS];
+    u32x4 qr[NT][Cfg<D, KVT>::QS];
     uint32_t lo;       // first key of the current range (wave-uniform)
     uint32_t lim[NT];  // per column: live keys of the range, counted from lo
     uint32_t free_lo, free_hi; // keys live for every valid column of the unit (wave-uniform)
@@ -1024,26 +1037,59 @@ __device__ __forceinline__ void compute_chunk(const AttnParams &p, const Chunk<D
             vscale[j] = c.vs[j];
         }
     }
-    // partial scores of this wave's slice -> LDS
+    if constexpr (C::KROW) {
+        // Whole-row K: lane (g, li) of tile j holds token 8w + li%8, dims 64h + 16g .. +15 with
+        // h = li/8.  One row rotation by 8 (written to half the banks of each 16-lane row) makes
+        // operand h hold half h of this wave's 16 tokens of the chunk: rows 0-7 tile 0's, rows
+        // 8-15 tile 1's.  Against the queries' half h they sum to the full scores of those
+        // tokens, one tile per wave.
+        uint32_t kh[2][4];
 #pragma unroll
-    for (int nt = 0; nt < NT; nt++) {
+        for (int w = 0; w < 4; w++) {
+            kh[0][w] = (uint32_t)__builtin_amdgcn_update_dpp((int)c.k[0][w], (int)c.k[1][w], 0x128 /* row_ror:8 */,
+                                                             0xF, 0xC, false);
+            kh[1][w] = (uint32_t)__builtin_amdgcn_update_dpp((int)c.k[1][w], (int)c.k[0][w], 0x128 /* row_ror:8 */,
+                                                             0xF, 0x3, false);
+        }
+        u32x4 a[2][2]; // [half][k-step]: bytes 8k .. 8k+7 of the lane's 16 as f16
 #pragma unroll
-        for (int j = 0; j < 2; j++) {
+        for (int h = 0; h < 2; h++)
+#pragma unroll
+            for (int k = 0; k < 2; k++) {
+                const u32x2 x0 = e4m3x4_to_f16x4_scaled(kh[h][2 * k]), x1 = e4m3x4_to_f16x4_scaled(kh[h][2 * k + 1]);
+                a[h][k] = u32x4{x0.x, x0.y, x1.x, x1.y};
+            }
+#pragma unroll
+        for (int nt = 0; nt < NT; nt++) {
             f32x4 sp = f32x4{0.0f, 0.0f, 0.0f, 0.0f};
 #pragma unroll
-            for (int ks = 0; ks < C::KS; ks++) {
-                u32x4 a;
-                if constexpr (C::FP8) {
-                    // k-step ks: bytes 8ks .. 8ks+7 of the lane's 16
-                    u32x2 x0 = e4m3x4_to_f16x4_scaled(c.k[j][2 * ks]);
-                    u32x2 x1 = e4m3x4_to_f16x4_scaled(c.k[j][2 * ks + 1]);
-                    a = u32x4{x0.x, x0.y, x1.x, x1.y};
-                } else {
-                    a = ks == 0 ? k_operand<0>(c.k[j]) : k_operand<1>(c.k[j]);
+            for (int h = 0; h < 2; h++)
+#pragma unroll
+                for (int k = 0; k < 2; k++) sp = mfma16x16x32<C::MBF16>(a[h][k], st.qr[nt][2 * h + k], sp);
+            sx[(wave * NT + nt) * 64 + lane] = sp;
+        }
+    } else {
+        // partial scores of this wave's slice -> LDS
+#pragma unroll
+        for (int nt = 0; nt < NT; nt++) {
+#pragma unroll
+            for (int j = 0; j < 2; j++) {
+                f32x4 sp = f32x4{0.0f, 0.0f, 0.0f, 0.0f};
+#pragma unroll
+                for (int ks = 0; ks < C::KS; ks++) {
+                    u32x4 a;
+                    if constexpr (C::FP8) {
+                        // k-step ks: bytes 8ks .. 8ks+7 of the lane's 16
+                        u32x2 x0 = e4m3x4_to_f16x4_scaled(c.k[j][2 * ks]);
+                        u32x2 x1 = e4m3x4_to_f16x4_scaled(c.k[j][2 * ks + 1]);
+                        a = u32x4{x0.x, x0.y, x1.x, x1.y};
+                    } else {
+                        a = ks == 0 ? k_operand<0>(c.k[j]) : k_operand<1>(c.k[j]);
+                    }
+                    sp = mfma16x16x32<C::MBF16>(a, st.qr[nt][ks], sp);
                 }
-                sp = mfma16x16x32<C::MBF16>(a, st.qr[nt][ks], sp);
+                sx[((wave * NT + nt) * 2 + j) * 64 + lane] = sp;
             }
-            sx[((wave * NT + nt) * 2 + j) * 64 + lane] = sp;
         }
     }
     // Only the LDS score exchange needs ordering (a full __syncthreads would also drain the
@@ -1061,6 +1107,13 @@ __device__ __forceinline__ void compute_chunk(const AttnParams &p, const Chunk<D
         f32x4 s[2];
 #pragma unroll
         for (int j = 0; j < 2; j++) {
+            if constexpr (C::KROW) {
+                // rows 4g .. 4g+3 of tile j are tokens 4g .. of wave g/2, rows 8j + 4(g%2) ..
+                // of its tile: lane 16(2j + g%2) + li
+                const uint32_t g = lane >> 4;
+                s[j] = sx[((g >> 1) * NT + nt) * 64 + 16 * (2 * j + (g & 1)) + (lane & 15)];
+                continue;
+            }
             s[j] = sx[((0 * NT + nt) * 2 + j) * 64 + lane];
 #pragma unroll
             for (int w = 1; w < C::WAVES; w++) s[j] += sx[((w * NT + nt) * 2 + j) * 64 + lane];
@@ -1156,7 +1209,7 @@ __device__ __forceinline__ void fold_chunk(const Chunk<D, KVT> &c, uint32_t t, S
             uint32_t x = 0;
 #pragma unroll
             for (int w = 0; w < C::KW; w++) x ^= c.k[j][w];
-            st.fold ^= in(t + 16 * j + li) ? x : 0u;
+            st.fold ^= in(t + 16 * j + (C::KROW ? 8 * wave + (li & 7) : li)) ? x : 0u;
         } else {
             // load q holds token 8q + li%8 of the tile
 #pragma unroll
@@ -1427,7 +1480,7 @@ __global__ __launch_bounds__(D / 32 * 64, kMinWavesPerEU<KVT>) void attention_ke
                 const bool valid = col < ncols;
                 const uint32_t ri = valid ? col / p.group : 0;
 #pragma unroll
-                for (int ks = 0; ks < C::KS; ks++)
+                for (int ks = 0; ks < C::QS; ks++)
                     st.qr[nt][ks] = load_q<D, KVT>(p, ud.rowbeg + ri, hk * p.group + col % p.group, valid, wave, ks);
             }
         };
