@@ -662,10 +662,11 @@ struct Cfg {
     static constexpr bool FP8 = KVT == LIA_FP8_E4M3;
     static constexpr bool MBF16 = KVT == LIA_BF16;  // MFMA operand type (f16 for f16 and FP8)
     static constexpr int EB = FP8 ? 1 : 2;          // bytes per stored KV element
-    // Each wave owns a head_dim slice of SW dims: 64 dims of a 16-bit pool (128 bytes of a
-    // token, two loads per tile of 8 tokens x 128 bytes each), 64 dims of an FP8 pool (64
-    // bytes, one load per tile of 16 tokens x 64 bytes).  A lane loads 16 contiguous bytes of
-    // a token per load.
+    // Each wave owns a head_dim slice of SW dims for P.V: 64 dims of a 16-bit pool (128 bytes
+    // of a token; its K in two loads per tile of 8 tokens x 128 bytes each), 64 dims of an FP8
+    // pool (64 bytes; with two waves each K load reads 8 tokens' whole 128-byte rows, KROW,
+    // and with one wave 16 tokens x 64 bytes).  A lane loads 16 contiguous bytes of a token
+    // per load.
     static constexpr int SW = 64;
     static constexpr int AUX = 2;           // cache policy of the K loads and FP8 V loads (nt)
     static constexpr int WAVES = D / SW;            // one wave per slice
