@@ -340,7 +340,13 @@ __device__ void plan_lds(uint32_t n_seqs, const uint32_t *cu, const uint32_t *po
     // searched.
     if (skew) {
         const uint64_t FN = weight_before(N);
-        for (uint32_t r = t; r <= N; r += T) s_rlo[r] = weight_before(r) * TC / FN;
+        // at least one block of cost per range: with TC < N * 256 / (256 - lag) the late ranges'
+        // weight makes some narrower than one block, and a range empty in blocks inside a unit
+        // would be counted among the unit's records without writing one.  The weighted start
+        // has slope above 1 in the first round, and TC - N + r (one block per remaining range)
+        // has slope 1, so their minimum starts every range at least one block after the last.
+        for (uint32_t r = t; r <= N; r += T)
+            s_rlo[r] = min(weight_before(r) * TC / FN, TC - N + r);
         lds_barrier();
     }
     // equal shares in 32-bit arithmetic when TC * N fits (every batch up to 2^32 / n_wg

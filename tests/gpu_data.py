@@ -110,7 +110,10 @@ class Case:
     def run(self, lia, dev=None, max_rows=None):
         dev = dev or self.device()
         cfg = self.config(lia, max_rows)
-        ws = torch.zeros(lia.workspace_bytes(cfg), dtype=torch.uint8, device="cuda")
+        # the workspace holds no required initial state: it starts as 0x7E bytes, so a split
+        # record the merge read without the kernel writing it (m and l 8.4e37 as floats) would
+        # outweigh every written one and show in the output
+        ws = torch.full((lia.workspace_bytes(cfg),), 0x7E, dtype=torch.uint8, device="cuda")
         odt = torch.float32 if self.g.out_dtype == F32 else torch.bfloat16
         out = torch.full((self.batch.n_rows, self.g.hq, self.g.d), float("nan"), dtype=odt,
                          device="cuda")
