@@ -110,10 +110,7 @@ class Case:
     def run(self, lia, dev=None, max_rows=None):
         dev = dev or self.device()
         cfg = self.config(lia, max_rows)
-        # the workspace holds no required initial state: it starts as 0x7E bytes, so a split
-        # record the merge read without the kernel writing it (m and l 8.4e37 as floats) would
-        # outweigh every written one and show in the output
-        ws = torch.full((lia.workspace_bytes(cfg),), 0x7E, dtype=torch.uint8, device="cuda")
+        ws = dirty_workspace(lia, cfg)
         odt = torch.float32 if self.g.out_dtype == F32 else torch.bfloat16
         out = torch.full((self.batch.n_rows, self.g.hq, self.g.d), float("nan"), dtype=odt,
                          device="cuda")
@@ -123,6 +120,14 @@ class Case:
         torch.cuda.synchronize()
         self.last_ws = ws  # the plan's header (units, blocks, ranges, overflow) is its first 16 bytes
         return out.float().cpu().numpy()
+
+
+def dirty_workspace(lia, cfg):
+    """A workspace for `cfg` filled with 0x7E bytes.  The workspace holds no required initial
+    state, so every test starts it dirty: a split record the merge read without the kernel
+    writing it (m and l 8.4e37 as floats) would outweigh every written one and show in the
+    output."""
+    return torch.full((lia.workspace_bytes(cfg),), 0x7E, dtype=torch.uint8, device="cuda")
 
 
 def errors(got, ref):

@@ -241,7 +241,7 @@ def test_capacity_does_not_change_results(lia, wl):
     for max_seqs, max_rows in ((b.n_seqs, b.n_rows), (64, 4096)):
         cfg = lia.AttentionConfig(g.hq, g.hkv, g.d, g.page_size, b.pool_pages, b.stride, g.q_dtype,
                                   g.kv_dtype, g.out_dtype, g.scale, max_seqs, max_rows, int(b.ctx.max()))
-        ws = torch.zeros(lia.workspace_bytes(cfg), dtype=torch.uint8, device="cuda")
+        ws = G.dirty_workspace(lia, cfg)
         out = torch.full((b.n_rows, g.hq, g.d), float("nan"), dtype=torch.bfloat16, device="cuda")
         lia.paged_attention(cfg, b.n_seqs, dev["cu"], dev["positions"], dev["sequences"], dev["pages"],
                             dev["q"], dev["kc"], dev["vc"], out, ws)

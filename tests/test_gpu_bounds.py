@@ -141,7 +141,7 @@ def test_step_with_out_of_pool_page_writes_nothing(lia, wl, wide):
     positions, sequences, slots = (torch.zeros(rows, dtype=torch.int32, device="cuda") for _ in range(3))
     status = torch.zeros(1, dtype=torch.int32, device="cuda")
     cfg = case.config(lia)
-    ws = torch.zeros(lia.workspace_bytes(cfg), dtype=torch.uint8, device="cuda")
+    ws = G.dirty_workspace(lia, cfg)
     out = torch.full((rows, g.hq, g.d), 7.0, dtype=torch.bfloat16, device="cuda")
     newk = torch.ones((rows, W), dtype=torch.bfloat16, device="cuda")
     lia.pack_device(G.u32_dev(np.arange(b.n_seqs)), G.u32_dev(b.q_len), G.u32_dev(b.cached), dflat,

@@ -33,7 +33,7 @@ def _run_fused(case, lia, seed, garbage=True):
         dkc[idx] = G.to_dev(junk, torch.int16)
         dvc[idx] = G.to_dev(junk[::-1].copy(), torch.int16)
     cfg = case.config(lia)
-    ws = torch.zeros(lia.workspace_bytes(cfg), dtype=torch.uint8, device="cuda")
+    ws = G.dirty_workspace(lia, cfg)
     odt = torch.float32 if g.out_dtype == F32 else torch.bfloat16
     out = torch.full((b.n_rows, g.hq, g.d), float("nan"), dtype=odt, device="cuda")
     lia.attention_plan(cfg, b.n_seqs, b.n_rows, dev["cu"], dev["positions"], dev["sequences"], ws,
@@ -129,7 +129,7 @@ def test_fused_append_canonicalises_nan_like_kv_append(lia, wl, O, kv):
                 kexp, vexp, src_dtype=kv, slot_mapping=b.slot_mapping())
     dev = case.device()
     cfg = case.config(lia)
-    ws = torch.zeros(lia.workspace_bytes(cfg), dtype=torch.uint8, device="cuda")
+    ws = G.dirty_workspace(lia, cfg)
     out = torch.empty((b.n_rows, g.hq, g.d), dtype=torch.bfloat16, device="cuda")
     lia.attention_plan(cfg, b.n_seqs, b.n_rows, dev["cu"], dev["positions"], dev["sequences"], ws,
                        pages=dev["pages"])
@@ -173,7 +173,7 @@ def test_config3_full_step_with_shared_prefix_pages(lia, wl, O, seed):
     slots = torch.zeros_like(positions)
     status = torch.full((1,), -1, dtype=torch.int32, device="cuda")
     cfg = case.config(lia)
-    ws = torch.zeros(lia.workspace_bytes(cfg), dtype=torch.uint8, device="cuda")
+    ws = G.dirty_workspace(lia, cfg)
     out = torch.full((rows, g.hq, g.d), float("nan"), dtype=torch.bfloat16, device="cuda")
     lia.pack_device(G.u32_dev(np.arange(b.n_seqs)), G.u32_dev(b.q_len), G.u32_dev(b.cached), flat,
                     b.stride, P, b.pool_pages, b.stride * P, rows, cu, positions, sequences, slots,
@@ -260,7 +260,7 @@ def test_fused_fp8_append(lia, wl, O, case_name):
     qf = O.from_f32(rng.standard_normal((b.n_rows, g.hq, g.d)).astype(np.float32), BF16)
     cfg = lia.AttentionConfig(g.hq, g.hkv, g.d, P, b.pool_pages, b.stride, g.q_dtype, g.kv_dtype,
                               g.out_dtype, g.scale, b.n_seqs, b.n_rows, int(b.ctx.max()))
-    ws = torch.zeros(lia.workspace_bytes(cfg), dtype=torch.uint8, device="cuda")
+    ws = G.dirty_workspace(lia, cfg)
     out = torch.full((b.n_rows, g.hq, g.d), float("nan"), dtype=torch.bfloat16, device="cuda")
     flat = G.u32_dev(b.flat_table())
     print(f"[case] fused fp8 {case_name}: seqs={b.n_seqs} rows={b.n_rows}", flush=True)

@@ -28,7 +28,7 @@ def _load(name):
 def _attend(lia, g, n_seqs, n_rows, pool_pages, stride, max_ctx, cu, pos, seq, flat, q, kc, vc):
     cfg = lia.AttentionConfig(g.hq, g.hkv, g.d, g.page_size, pool_pages, stride, g.q_dtype,
                               g.kv_dtype, g.out_dtype, g.scale, n_seqs, n_rows, max_ctx)
-    ws = torch.zeros(lia.workspace_bytes(cfg), dtype=torch.uint8, device="cuda")
+    ws = G.dirty_workspace(lia, cfg)
     odt = torch.float32 if g.out_dtype == F32 else torch.bfloat16
     out = torch.full((n_rows, g.hq, g.d), float("nan"), dtype=odt, device="cuda")
     lia.paged_attention(cfg, n_seqs, G.u32_dev(cu), G.u32_dev(pos), G.u32_dev(seq), G.u32_dev(flat),

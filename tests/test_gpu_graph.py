@@ -44,7 +44,7 @@ def _setup(lia, wl, kind, seed):
         newv = G.to_dev(case.vc.reshape(-1, W)[slots].copy(), torch.bfloat16)
     cfg = case.config(lia)
     layout = lia.KVLayout(g.hkv, g.d, g.page_size, b.pool_pages, kv)
-    ws = torch.zeros(lia.workspace_bytes(cfg), dtype=torch.uint8, device="cuda")
+    ws = G.dirty_workspace(lia, cfg)
     meta = dict(
         seq_slots=G.u32_dev(np.arange(b.n_seqs)), q_lens=G.u32_dev(b.q_len), cached=G.u32_dev(b.cached),
         cu=torch.zeros(b.n_seqs + 1, dtype=torch.int32, device="cuda"),

@@ -31,7 +31,7 @@ def _fold(lia, case):
     b = case.batch
     dev = case.device()
     cfg = case.config(lia)
-    ws = torch.zeros(lia.workspace_bytes(cfg), dtype=torch.uint8, device="cuda")
+    ws = G.dirty_workspace(lia, cfg)
     lia.attention_plan(cfg, b.n_seqs, b.n_rows, dev["cu"], dev["positions"], dev["sequences"], ws,
                        pages=dev["pages"])
     sink = torch.zeros(lia.paged_read_sink_words(cfg), dtype=torch.int32, device="cuda")

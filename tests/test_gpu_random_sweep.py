@@ -110,7 +110,7 @@ def test_random_step_device_packing_fused_append(lia, wl, i):
     dev["kc"].view(-1, W)[idx] = G.to_dev(junk, torch.int16)
     dev["vc"].view(-1, W)[idx] = G.to_dev(junk[::-1].copy(), torch.int16)
     cfg = case.config(lia)
-    ws = torch.zeros(lia.workspace_bytes(cfg), dtype=torch.uint8, device="cuda")
+    ws = G.dirty_workspace(lia, cfg)
     rows = b.n_rows
     cu = torch.full((b.n_seqs + 1,), -1, dtype=torch.int32, device="cuda")
     positions = torch.full((rows,), -1, dtype=torch.int32, device="cuda")
@@ -190,7 +190,7 @@ def test_random_fp8_step(lia, wl, O, i):
     qf = O.from_f32(rng.standard_normal((b.n_rows, g.hq, g.d)).astype(np.float32), BF16)
     cfg = lia.AttentionConfig(g.hq, g.hkv, g.d, P, b.pool_pages, b.stride, g.q_dtype, g.kv_dtype,
                               g.out_dtype, g.scale, b.n_seqs, b.n_rows, int(b.ctx.max()))
-    ws = torch.zeros(lia.workspace_bytes(cfg), dtype=torch.uint8, device="cuda")
+    ws = G.dirty_workspace(lia, cfg)
     rows = b.n_rows
     cu = torch.full((b.n_seqs + 1,), -1, dtype=torch.int32, device="cuda")
     positions = torch.full((rows,), -1, dtype=torch.int32, device="cuda")
