@@ -134,3 +134,89 @@ def test_gather_rows(lia, O, width, offset):
     lia.gather_rows(G.u32_dev(idx), dsrc, dst)
     torch.cuda.synchronize()
     assert np.array_equal(dst.cpu().numpy().reshape(-1).view(np.uint32), ref.view(np.uint32))
+
+
+GROWING = {
+    # decode rows: every step one key longer per sequence (the decode kernel, one tile)
+    "decode": ([300, 1200, 17, 5000, 64], [1, 1, 1, 1, 1]),
+    # verify rows and short chunks (the decode kernel's two-tile path)
+    "mixed": ([2000, 1200, 5000, 900], [8, 1, 3, 2]),
+    # prefill chunks over growing prefixes (the prefill kernel and its merge)
+    "prefill": ([3000, 2500], [256, 128]),
+}
+
+
+@pytest.mark.parametrize("kind", list(GROWING))
+def test_graph_replays_follow_growing_contexts(lia, wl, kind):
+    """A serving loop over one captured step: device packing and plan in one launch
+    (lia_pack_plan_device), the fused append + attention, the merge.  Between replays only the
+    packing's inputs (each sequence's cached keys, advanced by its rows), the step's new K/V
+    rows and nothing else change, so the device plan - units, block ranges, merge descriptors,
+    split records - is rebuilt under the same graph every step, over a workspace that still
+    holds the previous step's plan.  Each replay equals the eager step bit for bit, and every
+    eager step matches the f64 oracle."""
+    import dataclasses
+    ctx_final, q_len = GROWING[kind]
+    S = 3
+    final = wl.custom(ctx_final, q_len, seed=41)
+    steps = [dataclasses.replace(final, ctx=final.ctx - (S - 1 - i) * final.q_len) for i in range(S)]
+    cases = [G.Case(b, seed=41) for b in steps]
+    g, case = final.geom, cases[-1]
+    rows, W = final.n_rows, g.hkv * g.d
+    cfg = case.config(lia)
+    dev = case.device()
+    ws = G.dirty_workspace(lia, cfg)
+    seq_slots, q_lens = G.u32_dev(np.arange(final.n_seqs)), G.u32_dev(final.q_len)
+    cached = G.u32_dev(steps[0].cached)
+    cu = torch.zeros(final.n_seqs + 1, dtype=torch.int32, device="cuda")
+    meta = [torch.zeros(rows, dtype=torch.int32, device="cuda") for _ in range(3)]
+    status = torch.zeros(1, dtype=torch.int32, device="cuda")
+    newk = torch.zeros((rows, W), dtype=torch.bfloat16, device="cuda")
+    newv = torch.zeros_like(newk)
+    out = torch.zeros((rows, g.hq, g.d), dtype=torch.bfloat16, device="cuda")
+    context = final.stride * g.page_size
+
+    def set_step(i):
+        # the step's rows are the pool's own values at their slots, so the append rewrites
+        # what the pool holds and every step attends the same pool contents
+        slots = steps[i].slot_mapping().astype(np.int64)
+        cached.copy_(G.u32_dev(steps[i].cached))
+        newk.copy_(G.to_dev(case.kc.reshape(-1, W)[slots].copy(), torch.bfloat16))
+        newv.copy_(G.to_dev(case.vc.reshape(-1, W)[slots].copy(), torch.bfloat16))
+
+    def step():
+        lia.pack_plan_device(cfg, seq_slots, q_lens, cached, dev["pages"], rows, context, cu, meta[0],
+                             meta[1], meta[2], status, ws)
+        lia.attention_partial_append(cfg, final.n_seqs, dev["pages"], meta[2], dev["q"], newk, newv,
+                                     dev["kc"], dev["vc"], out, ws)
+        lia.attention_merge(cfg, final.n_seqs, rows, out, ws)
+
+    expected = []
+    for i in range(S):
+        set_step(i)
+        step()
+        torch.cuda.synchronize()
+        assert status.item() == 0, i
+        got = out.float().cpu().numpy()
+        mx, mean = G.errors(got, cases[i].f64())
+        print(f"[case] growing {kind} eager step {i}: max_abs={mx:.3e} mean_abs={mean:.3e}", flush=True)
+        assert mx < 2e-2 and mean < 2e-3, i
+        expected.append(out.clone())
+    set_step(0)
+    graph = torch.cuda.CUDAGraph()
+    stream = torch.cuda.Stream()
+    torch.cuda.synchronize()
+    with torch.cuda.stream(stream):
+        with torch.cuda.graph(graph, stream=stream):
+            step()
+    torch.cuda.synchronize()
+    for rep in range(2):
+        for i in range(S):
+            print(f"[case] growing {kind} replay {rep} step {i}", flush=True)
+            set_step(i)
+            out.fill_(float("nan"))
+            torch.cuda.synchronize()
+            graph.replay()
+            torch.cuda.synchronize()
+            assert status.item() == 0, i
+            assert torch.equal(out.view(torch.int16), expected[i].view(torch.int16)), (rep, i)
