@@ -319,34 +319,34 @@ __device__ void plan_lds(uint32_t n_seqs, const uint32_t *cu, const uint32_t *po
     // A workgroup dispatched after the first round_wg shares its CU with an older one, which the
     // hardware issues first, so its range is weighted (256 - lag) / 256 against 1 for the first
     // round (lag 0: equal shares).  F(r) = sum of the weights of ranges before r, times 256.
-    const bool skew = lag && round_wg && round_wg < N;
-    auto weight_before = [&](uint32_t r) -> uint64_t {
-        uint32_t late = 0; // ranges before r on workgroups w >= round_wg
-        if (skew) {
-            if (xcd_major) {
-                const uint32_t X = r / per, I = r % per;
-                for (uint32_t x = 0; x <= X && x < 8; x++) {
-                    const uint32_t cx = round_wg > x ? min(per, (round_wg - x + 7) / 8) : 0u;
-                    late += x < X ? per - cx : (I > cx ? I - cx : 0u);
-                }
-            } else {
-                late = r > round_wg ? r - round_wg : 0u;
+    auto late_before = [&](uint32_t r) -> uint32_t { // ranges before r on workgroups w >= round_wg
+        uint32_t late = 0;
+        if (xcd_major) {
+            const uint32_t X = r / per, I = r % per;
+            for (uint32_t x = 0; x <= X && x < 8; x++) {
+                const uint32_t cx = round_wg > x ? min(per, (round_wg - x + 7) / 8) : 0u;
+                late += x < X ? per - cx : (I > cx ? I - cx : 0u);
             }
+        } else {
+            late = r > round_wg ? r - round_wg : 0u;
         }
-        return 256ull * r - (uint64_t)lag * late;
+        return late;
+    };
+    // Weights only when every range still spans at least one block of cost: a range weighted w
+    // of 256 spans TC * w / F(N) >= TC * (256 - lag) / F(N), so with that at least 1 each start
+    // lies at least one block after the previous one.  A range empty in blocks inside a unit
+    // would be counted among the unit's records without writing one.
+    const bool skew = lag && round_wg && round_wg < N &&
+                      TC * (256 - lag) >= 256ull * N - (uint64_t)lag * late_before(N);
+    auto weight_before = [&](uint32_t r) -> uint64_t {
+        return 256ull * r - (skew ? (uint64_t)lag * late_before(r) : 0ull);
     };
     // Equal weights: range r starts at cost r*TC/N, and cost c lies in range ((c+1)*N-1)/TC.
     // Weighted: the start cost of every range is tabulated once (one division per range) and
     // searched.
     if (skew) {
         const uint64_t FN = weight_before(N);
-        // at least one block of cost per range: with TC < N * 256 / (256 - lag) the late ranges'
-        // weight makes some narrower than one block, and a range empty in blocks inside a unit
-        // would be counted among the unit's records without writing one.  The weighted start
-        // has slope above 1 in the first round, and TC - N + r (one block per remaining range)
-        // has slope 1, so their minimum starts every range at least one block after the last.
-        for (uint32_t r = t; r <= N; r += T)
-            s_rlo[r] = min(weight_before(r) * TC / FN, TC - N + r);
+        for (uint32_t r = t; r <= N; r += T) s_rlo[r] = weight_before(r) * TC / FN;
         lds_barrier();
     }
     // equal shares in 32-bit arithmetic when TC * N fits (every batch up to 2^32 / n_wg
@@ -2912,11 +2912,10 @@ static int run_stages(int stages, const lia_attention_config *c, uint32_t n_seqs
         WorkDesc *work = (WorkDesc *)(ws + L.work);
         MergeDesc *merge = (MergeDesc *)(ws + L.merge);
         uint32_t *header = (uint32_t *)(ws + L.header);
-        // Decode ranges XCD-major (each XCD a contiguous share), prefill ranges in launch order.
-        // Measured: XCD-major makes the config-2 step 1.3-1.4 % faster (its attention launch alone
-        // 0.15 us slower), keeps config 5 2 us shorter and config 4 unchanged; launch order makes
-        // the config-3 step 2 us shorter.
-        const uint32_t xcd = NT != kWideNT;
+        // Block ranges XCD-major (each XCD a contiguous share).  Measured against launch order:
+        // the config-2 step 1.3-1.4 % faster (its attention launch alone 0.15 us slower), the
+        // config-3 prefill kernel 3 % faster, config 5 2 us shorter, config 4 unchanged.
+        const uint32_t xcd = 1;
         const uint32_t cost = NT == kWideNT ? kUnitCostWide : kUnitCostDecode;
         const uint32_t lag = NT == kWideNT ? kLagWide : kLagDecode;
         if (pk && n_seqs <= kPlanSeqs && n_wg <= kPlanThreads) {
