@@ -168,7 +168,9 @@ constexpr uint32_t kPlanGroups = 8;
 // Cost of starting a unit, in 32-key blocks, that the balanced partition charges each unit: a
 // range crossing into a unit loads its queries, unit descriptor and page window before its first
 // keys.  Measured best: 8 for the prefill kernel (config 3 step 303 -> 246 us against no charge),
-// 4 for the decode kernel (config 2 8,320 -> 8,540 tokens/s; configs 4 and 5 lose beyond 4).
+// 4 for the decode kernel (config 2 8,320 -> 8,540 tokens/s; configs 4 and 5 lose beyond 4;
+// re-swept with XCD-major ranges: 2 is 1 % slower on config 2 and 2 % on config 4, 6 and 8
+// within 0.5 % of 4 on every decode configuration).
 constexpr uint32_t kUnitCostWide = 8, kUnitCostDecode = 4;
 // Weight lag (of 256) of the workgroups that share a CU with an older one.  Measured per
 // workgroup on the prefill kernel (two per CU): with equal shares the CU's first workgroup
