@@ -167,7 +167,9 @@ constexpr uint32_t kPlanThreads = 1024;
 constexpr uint32_t kPlanGroups = 8;
 // Cost of starting a unit, in 32-key blocks, that the balanced partition charges each unit: a
 // range crossing into a unit loads its queries, unit descriptor and page window before its first
-// keys.  Measured best: 8 for the prefill kernel (config 3 step 303 -> 246 us against no charge),
+// keys.  Measured best: 8 for the prefill kernel (config 3 step 303 -> 246 us against no charge;
+// re-swept with XCD-major ranges: 40-layer step 210.5-210.6 us per layer at 8, 212.8-212.9 at 12,
+// 262.5-262.6 at 4),
 // 4 for the decode kernel (config 2 8,320 -> 8,540 tokens/s; configs 4 and 5 lose beyond 4;
 // re-swept with XCD-major ranges: 2 is 1 % slower on config 2 and 2 % on config 4, 6 and 8
 // within 0.5 % of 4 on every decode configuration).
