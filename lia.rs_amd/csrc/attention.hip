@@ -181,6 +181,10 @@ constexpr uint32_t kUnitCostWide = 8, kUnitCostDecode = 4;
 // measured 1.5-2.5 % slower on config 2): its first-round workgroups do finish earlier, but more
 // blocks for them leave the other rounds' end unchanged, since the chip's aggregate rate while
 // every workgroup runs is the cap.
+// Re-measured with XCD-major ranges (every decode launch at lag 40, or FP8 and two-tile launches
+// only): 40-layer steps per layer config 5 156.1-156.5 us against 158.3-158.4 and config 4
+// 55.64-55.72 against 55.97-56.04, but the weighted plan's searches lengthen every step by about
+// 3 us (config 4 one-layer step 67.8 against 64.4-64.8) and config 2 loses 1 % at any lag: 0 kept.
 constexpr uint32_t kLagWide = 56, kLagDecode = 0;
 
 // The plan for up to kPlanSeqs sequences, one thread each (kPlanThreads): per-sequence extents
