@@ -321,6 +321,22 @@ def test_prefill_weighted_ranges_in_launch_order(lia, wl):
     assert cus < ranges < 2 * cus
 
 
+@pytest.mark.parametrize("prefix", [8200, 9000, 9100])
+def test_prefill_xcd_major_at_the_weight_boundary(lia, wl, prefix):
+    """A 16-row chunk after `prefix` cached keys: 2 prefill units of 258-286 blocks, so the plan
+    has as many ranges as the launch's prefill workgroups (XCD-major ranges) and a total cost
+    (blocks plus the units' start charges) of 532, 582 or 588.  The dispatch-round weights need
+    588 here for every range to keep a block: below it the plan uses equal shares, at 588 the
+    weighted ranges are just over one block wide.  The workspace starts dirty, so a range left
+    without blocks inside a unit would show in the output."""
+    b = wl.custom([prefix + 16], [16], seed=34)
+    case = G.Case(b, seed=34)
+    _check(case, lia, f"prefill 16 rows after {prefix} keys")
+    units, blocks, ranges, overflow = case.last_ws[:16].view(torch.int32).cpu().tolist()
+    print(f"[case] units={units} blocks={blocks} ranges={ranges}", flush=True)
+    assert overflow == 0 and units == 2 and blocks >= ranges == 512
+
+
 def test_repeat_calls_are_identical(lia, wl):
     b = wl.custom([5000, 17, 900], [1, 1, 3], seed=8)
     case = G.Case(b, seed=8)
